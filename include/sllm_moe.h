@@ -1,0 +1,264 @@
+/*
+ * sllm_moe.h -- C-ABI of the MI355X (gfx950) mixture-of-experts library,
+ * libsllm_moe.so. Plain pointers and sizes only.
+ *
+ * Conventions (as the reference's kernels/cuda/*.cu C-ABI):
+ *   - every int-returning call returns 0 on success, -1 on bad arguments or
+ *     a runtime error, -2 on a capacity bound; the message is available from
+ *     the *_last_error getters (one thread-local buffer behind all of them);
+ *   - "_dev" variants and all sllm_moe_* calls take DEVICE pointers, enqueue
+ *     work and do not synchronise; the plain reference-named calls take HOST
+ *     pointers and copy in and out;
+ *   - `stream` arguments are hipStream_t (NULL = default stream);
+ *   - bf16 tensors are passed as their uint16 bit patterns; e4m3 / e2m1 /
+ *     e8m0 tensors as bytes.
+ *
+ * Reference file:line citations are relative to the skfine24/sLLM checkout.
+ */
+#ifndef SLLM_MOE_H
+#define SLLM_MOE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Errors                                                                 */
+/* ---------------------------------------------------------------------- */
+/* ref kernels/cuda/kernels.cu:27-29 (sllm_last_error) */
+const char* sllm_last_error(void);
+/* ref kernels/cuda/qwen4.cu:23-24 */
+const char* sllm_q4_last_error(void);
+/* ref kernels/cuda/fp8.cu:22-23 */
+const char* sllm_fp8_last_error(void);
+/* ref kernels/cuda/deepseek.cu:44 */
+const char* sllm_ds_last_error(void);
+/* new: same buffer, for the fused-layer entry points */
+const char* sllm_moe_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* Device buffers and sync (ref kernels/cuda/kernels.cu:31-194, 425)      */
+/* ---------------------------------------------------------------------- */
+/* ref kernels.cu:31 / kernels/_sllm_cuda.py:26 */
+int sllm_device_count(void);
+/* ref kernels.cu:150 / _sllm_cuda.py:48-49 */
+void* sllm_buf_new(long nbytes);
+/* ref kernels.cu:174 / _sllm_cuda.py:52-53 */
+int sllm_buf_free(void* p);
+/* ref kernels.cu:180 / _sllm_cuda.py:54-55 */
+int sllm_buf_h2d(void* dst, const float* src, long nbytes);
+/* ref kernels.cu:186 / _sllm_cuda.py:58-59 */
+int sllm_buf_h2d_raw(void* dst, const void* src, long nbytes);
+/* ref kernels.cu:191 / _sllm_cuda.py:56-57 */
+int sllm_buf_d2h(float* dst, const void* src, long nbytes);
+/* new: byte-typed D2H twin of sllm_buf_d2h for non-fp32 buffers */
+int sllm_buf_d2h_raw(void* dst, const void* src, long nbytes);
+/* ref kernels.cu:163 / _sllm_cuda.py:50-51 */
+long sllm_mem_free_bytes(void);
+/* ref kernels.cu:425 / _sllm_cuda.py:384-386 */
+int sllm_sync(void);
+
+/* ---------------------------------------------------------------------- */
+/* Reference MoE kernel surface (ref kernels/cuda/qwen4.cu)                */
+/* ---------------------------------------------------------------------- */
+/* softmax -> top-k (ties to the lower id) -> renorm p/(sum p + 1e-20).
+ * logits (n,E) f32 -> w (n,topk) f32, ids (n,topk) i32. E <= 2048,
+ * topk <= 16. ref qwen4.cu:279-298 (host), :785-793 (_dev). */
+int sllm_q4_moe_router(const float* logits, float* w_out, int* id_out, int n,
+                       int E, int topk);
+int sllm_q4_moe_router_dev(const float* logits, float* w_out, int* id_out,
+                           int n, int E, int topk);
+/* out = silu(g) * u, n floats. ref qwen4.cu:308-320, :795-799 */
+int sllm_q4_swiglu(const float* g, const float* u, float* out, long n);
+int sllm_q4_swiglu_dev(const float* g, const float* u, float* out, long n);
+/* out[t,:] += w[t] * y[t,:]. ref qwen4.cu:332-351, :801-806 */
+int sllm_q4_axpy_rows(float* out, const float* y, const float* w, int n,
+                      int H);
+int sllm_q4_axpy_rows_dev(float* out, const float* y, const float* w, int n,
+                          int H);
+/* out[t,:] += sigmoid(g[t]) * shared[t,:]. ref qwen4.cu:363-382, :808-814 */
+int sllm_q4_shared_gate_accum(float* out, const float* shared, const float* g,
+                              int n, int H);
+int sllm_q4_shared_gate_accum_dev(float* out, const float* shared,
+                                  const float* g, int n, int H);
+
+/* ---------------------------------------------------------------------- */
+/* Reference GEMM surface                                                 */
+/* ---------------------------------------------------------------------- */
+/* C (M,N) = A (M,K) f32 . dequant(B)^T, B (N,K) e4m3, scale_inv
+ * (ceil(N/bh), ceil(K/bw)) f32 with W[n,k] = e4m3(B[n,k]) * s[n/bh, k/bw]
+ * (loaders/fp8.py:98-135). ref kernels/cuda/fp8.cu:72-110,
+ * kernels/_fp8_cuda.py:87-112. */
+int sllm_fp8_gemm(const float* A, const unsigned char* B,
+                  const float* scale_inv, float* C, int M, int N, int K,
+                  int block_h, int block_w);
+int sllm_fp8_gemm_dev(const float* A, const unsigned char* B,
+                      const float* scale_inv, float* C, int M, int N, int K,
+                      int block_h, int block_w);
+/* O (M,N) = A (M,K) . B (N,K)^T, fp32, B already dequantized (host
+ * pointers). ref kernels/cuda/deepseek.cu:57-73. `scale`, `opts` unused. */
+int sllm_ds_fp4_gemm(float* o, const float* a, const float* b, int M, int N,
+                     int K, float scale, float* opts);
+/* new: the same product with the FP4 bytes on the device: packed (N,K/2)
+ * E2M1 (low nibble = even k) and (N, K/block_w) E8M0 scales
+ * (loaders/fp8.py:177-200); replaces the host dequant of
+ * kernels/_deepseek_cuda.py:89-94. Host / device pointer variants. */
+int sllm_ds_fp4_gemm_packed(float* o, const float* a, const void* packed,
+                            const void* scale_e8m0, int M, int N, int K,
+                            int block_w);
+int sllm_ds_fp4_gemm_packed_dev(float* o, const float* a, const void* packed,
+                                const void* scale_e8m0, int M, int N, int K,
+                                int block_w);
+/* c (m,n) f32 = a (m,k) . w (n,k)^T, a and w both f32 (atype 0) or bf16
+ * (atype 1); device pointers; c is fp32. ref kernels.cu:752-767
+ * (cublasGemmEx), kernels/_sllm_cuda.py:503-506. */
+int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
+                 int n, int k);
+
+/* ---------------------------------------------------------------------- */
+/* MoE building blocks (device pointers, stream-ordered, no sync)          */
+/* ---------------------------------------------------------------------- */
+/* logits (T,E) f32 = x (T,H) bf16 . W (E,H)^T bf16; H % 128 == 0.
+ * replaces x @ router_w.T of ref/qwen4_exp.py:173 and the gemv of
+ * kernels/q4_device_decode.py:322. */
+int sllm_moe_router_gemm(const void* x_bf16, const void* w_bf16,
+                         float* logits, int T, int E, int H, void* stream);
+/* softmax top-k (ref/qwen4_exp.py:125-140); E <= 2048, topk <= 64. */
+int sllm_moe_route_softmax(const float* logits, float* w_out, int* id_out,
+                           int T, int E, int topk, float eps, void* stream);
+/* scored routing with selection-only bias, optional group limit and
+ * routed scaling (ref/deepseek_v4.py:522-561). scoring: 0 softmax,
+ * 1 sigmoid, 2 sqrtsoftplus. n_group <= 1 disables the group limit. */
+int sllm_moe_route_grouped(const float* logits, const float* bias,
+                           float* w_out, int* id_out, int T, int E, int topk,
+                           int n_group, int topk_group, int scoring,
+                           float route_scale, void* stream);
+/* Stable expert-major permutation of ids (N = T*k int32) with a ragged tile
+ * table of ceil(count/bm) row tiles per expert. new (the reference has no
+ * permute; replaces the np.where grouping of ref/deepseek_v4.py:1080-1086).
+ * scratch >= sllm_moe_permute_scratch_bytes(N, E). */
+long sllm_moe_permute_scratch_bytes(int N, int E);
+int sllm_moe_permute(const int* ids, int N, int E, int bm, int* counts,
+                     int* offsets, int* sorted_idx, int* inv_pos,
+                     int* tile_info, int* num_tiles, int max_tiles,
+                     void* scratch, void* stream);
+/* Per-1x128 e4m3 activation quant (ref/hf_sources/dsv4/kernel.py:40-125);
+ * pow2 = 1 selects the ue8m0 power-of-two scale. Optional fused shared-
+ * expert gate: gate_out[t] = sigmoid(x[t] . gate_w) (ref/qwen4_exp.py:182). */
+int sllm_moe_act_quant(const void* x_bf16, int T, int H, int pow2,
+                       void* q_e4m3, float* scale, const void* gate_w_bf16,
+                       float* gate_out, void* stream);
+/* out[t] = sum_j y[inv_pos[t*k+j]] + y_shared[t] (y rows bf16 or f32). */
+int sllm_moe_combine(const void* y, int y_f32, const int* inv_pos, int topk,
+                     const void* y_shared, int T, int H, int out_f32,
+                     void* out, void* stream);
+/* Synthetic-weight quantizers (data preparation): FP8 128x128 block
+ * (s = amax/448, optionally its power-of-two ceiling) and MXFP4 per 32. */
+int sllm_quantize_weight_fp8(const float* w, int N, int K, int pow2,
+                             void* q_e4m3, float* scale, void* stream);
+int sllm_quantize_weight_mxfp4(const float* w, int N, int K, void* packed,
+                               void* scale_e8m0, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Fused MoE layers                                                       */
+/* ---------------------------------------------------------------------- */
+/* mode: which arithmetic the expert products use */
+#define SLLM_MOE_MODE_AUTO 0    /* decode when T <= 64, else prefill */
+#define SLLM_MOE_MODE_PREFILL 1 /* e4m3 activations, grouped MFMA GEMMs */
+#define SLLM_MOE_MODE_DECODE 2  /* fp32 activations, dequant GEMV */
+
+/* Qwen-style layer (ref/qwen4_exp.py:153-184): softmax top-k routing,
+ * SwiGLU experts with FP8 e4m3 weights and fp32 128x128 block scales
+ * (orientation (ceil(out/128), ceil(in/128)), loaders/fp8.py:98-135),
+ * optional shared expert with a sigmoid scalar gate.
+ *   x (T,H) bf16; router_w (E,H) bf16 [or logits (T,E) f32 when
+ *   logits_given]; wg/wu (E,I,H) + (E,I/128,H/128); wd (E,H,I) +
+ *   (E,H/128,I/128); shared sg/su (Is,H), sd (H,Is) + scales; sgl (H) bf16.
+ *   out (T,H) bf16 or f32. Optional debug copies: logits_out (T,E),
+ *   w_out (T,k) f32, ids_out (T,k) i32, counts_out (E) i32.
+ * Replaces qwen4_exp.moe_block_forward (the numpy oracle that runs today)
+ * and kernels/q4_device_decode.py:316-339 (_moe). */
+typedef struct sllm_moe_qwen_args {
+  int T, H, E, I, Is, topk;
+  int mode;
+  int out_f32;
+  int logits_given;
+  int wdtype; /* 0: FP8 e4m3 + fp32 block scales; 1: bf16 (scales unused,
+                 always the fp32-activation GEMV path) */
+  float renorm_eps;
+  const void* x;
+  const float* logits;
+  const void* router_w;
+  const void* wg;
+  const float* wg_s;
+  const void* wu;
+  const float* wu_s;
+  const void* wd;
+  const float* wd_s;
+  const void* sg;
+  const float* sg_s;
+  const void* su;
+  const float* su_s;
+  const void* sd;
+  const float* sd_s;
+  const void* sgl;
+  void* out;
+  float* logits_out;
+  float* w_out;
+  int* ids_out;
+  int* counts_out;
+  void* workspace;
+  long workspace_bytes;
+  void* stream;
+} sllm_moe_qwen_args;
+
+long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
+int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a);
+
+/* DeepSeek-style layer (ref/deepseek_v4.py:522-570 with the upstream
+ * combine of ref/hf_sources/dsv4/model.py:684-699): scored routing with a
+ * selection-only bias, optional group limit, routed scaling; routed experts
+ * MXFP4 (w1/w3 (E,I,H/2) + (E,I,H/32) e8m0, w2 (E,H,I/2) + (E,H,I/32));
+ * optional un-gated shared expert in FP8 with fp32 power-of-two 128x128
+ * block scales (s1/s3 (Is,H), s2 (H,Is)); swiglu_limit clamps as
+ * ref/deepseek_v4.py:564-570 (0 disables). */
+typedef struct sllm_moe_ds_args {
+  int T, H, E, I, Is, topk;
+  int mode;
+  int out_f32;
+  int logits_given;
+  int n_group, topk_group, scoring;
+  float route_scale, swiglu_limit;
+  const void* x;
+  const float* logits;
+  const void* router_w;
+  const float* bias;
+  const void* w1;
+  const void* w1_s;
+  const void* w3;
+  const void* w3_s;
+  const void* w2;
+  const void* w2_s;
+  const void* s1;
+  const float* s1_s;
+  const void* s3;
+  const float* s3_s;
+  const void* s2;
+  const float* s2_s;
+  void* out;
+  float* logits_out;
+  float* w_out;
+  int* ids_out;
+  int* counts_out;
+  void* workspace;
+  long workspace_bytes;
+  void* stream;
+} sllm_moe_ds_args;
+
+long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a);
+int sllm_moe_ds_forward(const sllm_moe_ds_args* a);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SLLM_MOE_H */

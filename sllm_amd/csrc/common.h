@@ -1,0 +1,129 @@
+// Shared definitions for the sLLM MoE HIP library (gfx950 / MI355X).
+//
+// Error model (mirrors the reference's C-ABI, kernels/cuda/qwen4.cu:23-34):
+// every entry point returns 0 on success, -1 on bad arguments or a runtime
+// error, -2 on a capacity bound; the message is kept in a THREAD-LOCAL
+// buffer (the reference's buffers are process-global statics) that all the
+// *_last_error getters return.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace sllm {
+
+// --------------------------------------------------------------------------
+// errors
+// --------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+const char* last_error();
+
+#define SLLM_HIP(expr)                                                        \
+  do {                                                                        \
+    hipError_t _e = (expr);                                                   \
+    if (_e != hipSuccess) {                                                   \
+      ::sllm::set_error("%s:%d %s: %s", __FILE__, __LINE__, #expr,            \
+                        hipGetErrorString(_e));                               \
+      return -1;                                                              \
+    }                                                                         \
+  } while (0)
+
+#define SLLM_REQUIRE(cond, ...)                                               \
+  do {                                                                        \
+    if (!(cond)) {                                                            \
+      ::sllm::set_error(__VA_ARGS__);                                         \
+      return -1;                                                              \
+    }                                                                         \
+  } while (0)
+
+// Checks the launch that was just issued.
+#define SLLM_LAUNCHED()                                                       \
+  do {                                                                        \
+    hipError_t _e = hipGetLastError();                                        \
+    if (_e != hipSuccess) {                                                   \
+      ::sllm::set_error("%s:%d launch failed: %s", __FILE__, __LINE__,        \
+                        hipGetErrorString(_e));                               \
+      return -1;                                                              \
+    }                                                                         \
+  } while (0)
+
+constexpr int kWave = 64;
+
+// --------------------------------------------------------------------------
+// number formats
+// --------------------------------------------------------------------------
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (inputs are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// One OCP E4M3FN byte (selected by `sel`, 0..3 of a dword) -> fp32, using the
+// gfx950 hardware conversion (exact for every finite code).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t dword, int sel) {
+  switch (sel) {
+    case 0: return __builtin_amdgcn_cvt_f32_fp8(dword, 0);
+    case 1: return __builtin_amdgcn_cvt_f32_fp8(dword, 1);
+    case 2: return __builtin_amdgcn_cvt_f32_fp8(dword, 2);
+    default: return __builtin_amdgcn_cvt_f32_fp8(dword, 3);
+  }
+}
+
+// Four fp32 values (already clamped to +-448) -> four E4M3FN bytes packed
+// little-endian in a dword, round to nearest even (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c,
+                                                  float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// Order-preserving map of fp32 onto uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t f32_order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// --------------------------------------------------------------------------
+// wave64 reductions
+// --------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o, kWave);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float silu_f32(float x) {
+  return x / (1.0f + expf(-x));
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  return 1.0f / (1.0f + expf(-x));
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace sllm

@@ -1,0 +1,60 @@
+// Internal launchers shared between the library's translation units.
+#pragma once
+#include "common.h"
+
+namespace sllm {
+
+int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
+                       int T, int E, int H, hipStream_t st);
+int launch_route_softmax(const float* logits, float* w, int* ids, int T,
+                         int E, int topk, float eps, hipStream_t st);
+int launch_route_grouped(const float* logits, const float* bias, float* w,
+                         int* ids, int T, int E, int topk, int n_group,
+                         int topk_group, int scoring, float route_scale,
+                         hipStream_t st);
+size_t permute_scratch_bytes(int N, int E);
+int launch_permute(const int* ids, int N, int E, int bm, int* counts,
+                   int* offsets, int* sorted_idx, int* inv_pos,
+                   int* tile_info, int* num_tiles, int max_tiles,
+                   void* scratch, hipStream_t st);
+int launch_act_quant(const uint16_t* x, int T, int H, int pow2, uint8_t* q,
+                     float* s, const uint16_t* gate_w, float* gate_out,
+                     hipStream_t st);
+int launch_gemm1_fp8(const uint8_t* xq, const float* sx, const int* sorted_idx,
+                     int topk, int total_rows, const int* tile_info,
+                     const int* num_tiles, int max_tiles, const int* offsets,
+                     const uint8_t* wg, const float* wg_s, const uint8_t* wu,
+                     const float* wu_s, int I, int H, const float* route_w,
+                     float limit, int pow2, uint8_t* hq, float* hs,
+                     hipStream_t st);
+int launch_gemm2_fp8(const uint8_t* hq, const float* hs, const int* sorted_idx,
+                     int topk, int total_rows, const int* tile_info,
+                     const int* num_tiles, int max_tiles, const int* offsets,
+                     const uint8_t* wd, const float* wd_s, int I, int H,
+                     const float* row_w, uint16_t* y, hipStream_t st);
+// MX-scaled grouped GEMMs (A e4m3 with power-of-two per-128 scales; B
+// MXFP4 with e8m0 per 32, or FP8 with power-of-two 128x128 block scales).
+int launch_gemm1_mx(int b_fp4, const uint8_t* xq, const float* sx,
+                    const int* sorted_idx, int topk, int total_rows,
+                    const int* tile_info, const int* num_tiles, int max_tiles,
+                    const int* offsets, const uint8_t* w1, const void* w1_s,
+                    const uint8_t* w3, const void* w3_s, int I, int H,
+                    const float* route_w, float limit, uint8_t* hq, float* hs,
+                    hipStream_t st);
+int launch_gemm2_mx(int b_fp4, const uint8_t* hq, const float* hs,
+                    const int* sorted_idx, int topk, int total_rows,
+                    const int* tile_info, const int* num_tiles, int max_tiles,
+                    const int* offsets, const uint8_t* w2, const void* w2_s,
+                    int I, int H, uint16_t* y, hipStream_t st);
+int launch_gemv(int wf, int swiglu, const void* act, int act_bf16,
+                int gather_tokens, const int* sorted_idx, int topk,
+                int total_rows, const int* tile_info, const int* num_tiles,
+                int max_tiles, const int* offsets, const uint8_t* w0,
+                const void* s0, const uint8_t* w1, const void* s1, int N,
+                int K, const float* row_w, float limit, float* out,
+                hipStream_t st);
+int launch_combine(const void* y, int y_f32, const int* inv_pos, int topk,
+                   const void* y_shared, int T, int H, int out_f32, void* out,
+                   hipStream_t st);
+
+}  // namespace sllm

@@ -1,0 +1,374 @@
+// Fused MoE layer entry points: router -> permute -> expert GEMMs ->
+// shared expert -> combine, all stream-ordered on one HIP stream with no
+// host synchronisation and no allocation (the caller provides the
+// workspace; its size comes from the *_workspace_bytes query).
+//
+// Replaces ref/qwen4_exp.py:153-184 (moe_block_forward, the numpy oracle the
+// serving path runs today), kernels/q4_device_decode.py:316-339 (_moe) and,
+// for the DeepSeek layer, ref/deepseek_v4.py:1070-1087 (Block.moe) with the
+// upstream combine of ref/hf_sources/dsv4/model.py:684-699.
+//
+// Two arithmetic modes:
+//  prefill: activations quantized to e4m3 per 1x128 (upstream act_quant)
+//           before the gate/up GEMM and again before the down GEMM; grouped
+//           MFMA GEMMs over ragged row tiles.
+//  decode:  fp32 activations against dequantized weights in a
+//           bandwidth-bound GEMV over the touched experts only.
+#include "../../include/sllm_moe.h"
+#include "launch.h"
+
+namespace sllm {
+
+constexpr int PREFILL_BM = 128;
+constexpr int DECODE_MAX_T = 64;
+
+struct Plan {
+  bool decode;
+  int N;          // T * topk
+  int bm, max_tiles;
+  size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
+  size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh;
+  size_t total;
+};
+
+static size_t take(size_t& cur, size_t bytes) {
+  size_t at = cur;
+  cur += align_up(bytes ? bytes : 1, 256);
+  return at;
+}
+
+static bool pick_decode(int mode, int T) {
+  return mode == SLLM_MOE_MODE_DECODE ||
+         (mode == SLLM_MOE_MODE_AUTO && T <= DECODE_MAX_T);
+}
+
+static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
+                      bool has_shared, bool need_logits, bool force_gemv) {
+  Plan p{};
+  p.decode = force_gemv || pick_decode(mode, T);
+  p.N = T * topk;
+  if (p.decode) {
+    p.bm = p.N;  // one tile per touched expert
+    p.max_tiles = E < p.N ? E : p.N;
+  } else {
+    p.bm = PREFILL_BM;
+    p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N);
+  }
+  size_t c = 0;
+  p.logits = need_logits ? take(c, (size_t)T * E * 4) : 0;
+  p.w = take(c, (size_t)p.N * 4);
+  p.ids = take(c, (size_t)p.N * 4);
+  p.counts = take(c, (size_t)E * 4);
+  p.offsets = take(c, (size_t)(E + 1) * 4);
+  p.sorted = take(c, (size_t)p.N * 4);
+  p.inv = take(c, (size_t)p.N * 4);
+  p.tiles = take(c, (size_t)p.max_tiles * 8);
+  p.ntiles = take(c, 4);
+  p.pscr = take(c, permute_scratch_bytes(p.N, E));
+  p.gate = take(c, (size_t)T * 4);
+  if (p.decode) {
+    p.hq = take(c, (size_t)p.N * I * 4);                      // h fp32
+    p.hq_sh = has_shared ? take(c, (size_t)T * Is * 4) : 0;   // h_sh fp32
+    p.y = take(c, (size_t)p.N * H * 4);                       // y fp32
+    p.y_sh = has_shared ? take(c, (size_t)T * H * 4) : 0;
+  } else {
+    p.xq = take(c, (size_t)T * H);
+    p.sx = take(c, (size_t)T * (H / 128) * 4);
+    p.hq = take(c, (size_t)p.N * I);
+    p.hs = take(c, (size_t)p.N * (I / 128) * 4);
+    if (has_shared) {
+      p.hq_sh = take(c, (size_t)T * Is);
+      p.hs_sh = take(c, (size_t)T * (Is / 128) * 4);
+    }
+    p.y = take(c, (size_t)p.N * H * 2);                       // y bf16
+    p.y_sh = has_shared ? take(c, (size_t)T * H * 2) : 0;
+  }
+  p.total = c;
+  return p;
+}
+
+template <typename A>
+static int check_common(const A* a, const char* who) {
+  SLLM_REQUIRE(a, "%s: null args", who);
+  SLLM_REQUIRE(a->T > 0 && a->H > 0 && a->E > 0 && a->I > 0 && a->topk > 0,
+               "%s: sizes must be positive", who);
+  SLLM_REQUIRE(a->topk <= a->E && a->E <= 2048 && a->topk <= 64,
+               "%s: need topk <= E <= 2048 and topk <= 64 (E=%d k=%d)", who,
+               a->E, a->topk);
+  SLLM_REQUIRE(a->H % 256 == 0 && a->I % 128 == 0,
+               "%s: need H %% 256 == 0 and I %% 128 == 0 (H=%d I=%d)", who,
+               a->H, a->I);
+  SLLM_REQUIRE((long)a->T * a->topk < (1L << 30), "%s: T*topk too large", who);
+  SLLM_REQUIRE(a->mode >= 0 && a->mode <= 2, "%s: bad mode %d", who, a->mode);
+  SLLM_REQUIRE(a->x && a->out && a->workspace, "%s: null x/out/workspace", who);
+  SLLM_REQUIRE(a->logits_given ? a->logits != nullptr : a->router_w != nullptr,
+               "%s: need logits (logits_given) or router_w", who);
+  return 0;
+}
+
+static int copy_debug(const float* logits, const float* w, const int* ids,
+                      const int* counts, int T, int E, int N, float* logits_out,
+                      float* w_out, int* ids_out, int* counts_out,
+                      hipStream_t st) {
+  if (logits_out)
+    SLLM_HIP(hipMemcpyAsync(logits_out, logits, (size_t)T * E * 4,
+                            hipMemcpyDeviceToDevice, st));
+  if (w_out)
+    SLLM_HIP(hipMemcpyAsync(w_out, w, (size_t)N * 4, hipMemcpyDeviceToDevice, st));
+  if (ids_out)
+    SLLM_HIP(hipMemcpyAsync(ids_out, ids, (size_t)N * 4, hipMemcpyDeviceToDevice, st));
+  if (counts_out)
+    SLLM_HIP(hipMemcpyAsync(counts_out, counts, (size_t)E * 4,
+                            hipMemcpyDeviceToDevice, st));
+  return 0;
+}
+
+}  // namespace sllm
+
+using namespace sllm;
+
+extern "C" {
+
+long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a) {
+  if (!a || a->T <= 0 || a->E <= 0 || a->topk <= 0) {
+    set_error("sllm_moe_qwen_workspace_bytes: bad args");
+    return -1;
+  }
+  const bool sh = a->su != nullptr;
+  return (long)make_plan(a->T, a->H, a->E, a->I, sh ? a->Is : 0, a->topk,
+                         a->mode, sh, !a->logits_given, a->wdtype == 1)
+      .total;
+}
+
+int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
+  if (check_common(a, "sllm_moe_qwen_forward")) return -1;
+  const bool sh = a->su != nullptr;
+  SLLM_REQUIRE(a->wdtype == 0 || a->wdtype == 1,
+               "sllm_moe_qwen_forward: wdtype must be 0 (fp8) or 1 (bf16)");
+  const bool bf16w = a->wdtype == 1;
+  SLLM_REQUIRE(a->wg && a->wu && a->wd &&
+                   (bf16w || (a->wg_s && a->wu_s && a->wd_s)),
+               "sllm_moe_qwen_forward: null expert weights");
+  if (sh)
+    SLLM_REQUIRE(a->sg && a->sd && a->sgl && a->Is > 0 && a->Is % 128 == 0 &&
+                     (bf16w || (a->sg_s && a->su_s && a->sd_s)),
+                 "sllm_moe_qwen_forward: incomplete shared expert");
+  const int T = a->T, H = a->H, E = a->E, I = a->I, k = a->topk;
+  const int Is = sh ? a->Is : 0;
+  const int wf = bf16w ? 2 : 0;  // gemv weight format
+  const Plan p = make_plan(T, H, E, I, Is, k, a->mode, sh, !a->logits_given,
+                           bf16w);
+  SLLM_REQUIRE(a->workspace_bytes >= (long)p.total,
+               "sllm_moe_qwen_forward: workspace %ld < %zu bytes",
+               a->workspace_bytes, p.total);
+  hipStream_t st = (hipStream_t)a->stream;
+  char* ws = (char*)a->workspace;
+  float* logits = a->logits_given ? (float*)a->logits : (float*)(ws + p.logits);
+  float* w = (float*)(ws + p.w);
+  int* ids = (int*)(ws + p.ids);
+  int* counts = (int*)(ws + p.counts);
+  int* offsets = (int*)(ws + p.offsets);
+  int* sorted = (int*)(ws + p.sorted);
+  int* inv = (int*)(ws + p.inv);
+  int* tiles = (int*)(ws + p.tiles);
+  int* ntiles = (int*)(ws + p.ntiles);
+  float* gate = (float*)(ws + p.gate);
+  const float eps = a->renorm_eps;
+
+  if (!a->logits_given &&
+      launch_router_gemm((const uint16_t*)a->x, (const uint16_t*)a->router_w,
+                         logits, T, E, H, st))
+    return -1;
+  if (launch_route_softmax(logits, w, ids, T, E, k, eps, st)) return -1;
+  if (launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
+                     ntiles, p.max_tiles, ws + p.pscr, st))
+    return -1;
+
+  if (p.decode) {
+    float* h = (float*)(ws + p.hq);
+    float* y = (float*)(ws + p.y);
+    if (sh && launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr, nullptr,
+                               (const uint16_t*)a->sgl, gate, st))
+      return -1;
+    if (launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
+                    p.max_tiles, offsets, (const uint8_t*)a->wg, a->wg_s,
+                    (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, h, st))
+      return -1;
+    if (launch_gemv(wf, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                    offsets, (const uint8_t*)a->wd, a->wd_s, nullptr, nullptr,
+                    H, I, w, 0.f, y, st))
+      return -1;
+    float* y_sh = nullptr;
+    if (sh) {
+      float* h_sh = (float*)(ws + p.hq_sh);
+      y_sh = (float*)(ws + p.y_sh);
+      if (launch_gemv(wf, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
+                      nullptr, (const uint8_t*)a->sg, a->sg_s,
+                      (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
+                      h_sh, st))
+        return -1;
+      if (launch_gemv(wf, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
+                      nullptr, (const uint8_t*)a->sd, a->sd_s, nullptr,
+                      nullptr, H, Is, gate, 0.f, y_sh, st))
+        return -1;
+    }
+    if (launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st))
+      return -1;
+  } else {
+    uint8_t* xq = (uint8_t*)(ws + p.xq);
+    float* sx = (float*)(ws + p.sx);
+    uint8_t* hq = (uint8_t*)(ws + p.hq);
+    float* hs = (float*)(ws + p.hs);
+    uint16_t* y = (uint16_t*)(ws + p.y);
+    if (launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
+                         sh ? (const uint16_t*)a->sgl : nullptr, gate, st))
+      return -1;
+    if (launch_gemm1_fp8(xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                         offsets, (const uint8_t*)a->wg, a->wg_s,
+                         (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, 0,
+                         hq, hs, st))
+      return -1;
+    if (launch_gemm2_fp8(hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                         offsets, (const uint8_t*)a->wd, a->wd_s, I, H, w, y,
+                         st))
+      return -1;
+    uint16_t* y_sh = nullptr;
+    if (sh) {
+      uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
+      float* hs_sh = (float*)(ws + p.hs_sh);
+      y_sh = (uint16_t*)(ws + p.y_sh);
+      if (launch_gemm1_fp8(xq, sx, nullptr, k, T, nullptr, nullptr, 0, nullptr,
+                           (const uint8_t*)a->sg, a->sg_s,
+                           (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
+                           0, hq_sh, hs_sh, st))
+        return -1;
+      if (launch_gemm2_fp8(hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
+                           nullptr, (const uint8_t*)a->sd, a->sd_s, Is, H, gate,
+                           y_sh, st))
+        return -1;
+    }
+    if (launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st))
+      return -1;
+  }
+  return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
+                    a->ids_out, a->counts_out, st);
+}
+
+long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
+  if (!a || a->T <= 0 || a->E <= 0 || a->topk <= 0) {
+    set_error("sllm_moe_ds_workspace_bytes: bad args");
+    return -1;
+  }
+  const bool sh = a->s1 != nullptr;
+  return (long)make_plan(a->T, a->H, a->E, a->I, sh ? a->Is : 0, a->topk,
+                         a->mode, sh, !a->logits_given, false)
+      .total;
+}
+
+int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
+  if (check_common(a, "sllm_moe_ds_forward")) return -1;
+  const bool sh = a->s1 != nullptr;
+  SLLM_REQUIRE(a->w1 && a->w1_s && a->w3 && a->w3_s && a->w2 && a->w2_s,
+               "sllm_moe_ds_forward: null expert weights");
+  SLLM_REQUIRE(a->H % 32 == 0 && a->I % 32 == 0, "sllm_moe_ds_forward: H, I");
+  if (sh)
+    SLLM_REQUIRE(a->s1_s && a->s3 && a->s3_s && a->s2 && a->s2_s && a->Is > 0 &&
+                     a->Is % 128 == 0,
+                 "sllm_moe_ds_forward: incomplete shared expert");
+  const int T = a->T, H = a->H, E = a->E, I = a->I, k = a->topk;
+  const int Is = sh ? a->Is : 0;
+  const float L = a->swiglu_limit;
+  const Plan p = make_plan(T, H, E, I, Is, k, a->mode, sh, !a->logits_given,
+                           false);
+  SLLM_REQUIRE(a->workspace_bytes >= (long)p.total,
+               "sllm_moe_ds_forward: workspace %ld < %zu bytes",
+               a->workspace_bytes, p.total);
+  hipStream_t st = (hipStream_t)a->stream;
+  char* ws = (char*)a->workspace;
+  float* logits = a->logits_given ? (float*)a->logits : (float*)(ws + p.logits);
+  float* w = (float*)(ws + p.w);
+  int* ids = (int*)(ws + p.ids);
+  int* counts = (int*)(ws + p.counts);
+  int* offsets = (int*)(ws + p.offsets);
+  int* sorted = (int*)(ws + p.sorted);
+  int* inv = (int*)(ws + p.inv);
+  int* tiles = (int*)(ws + p.tiles);
+  int* ntiles = (int*)(ws + p.ntiles);
+
+  if (!a->logits_given &&
+      launch_router_gemm((const uint16_t*)a->x, (const uint16_t*)a->router_w,
+                         logits, T, E, H, st))
+    return -1;
+  if (launch_route_grouped(logits, a->bias, w, ids, T, E, k, a->n_group,
+                           a->topk_group, a->scoring, a->route_scale, st))
+    return -1;
+  if (launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
+                     ntiles, p.max_tiles, ws + p.pscr, st))
+    return -1;
+
+  if (p.decode) {
+    float* h = (float*)(ws + p.hq);
+    float* y = (float*)(ws + p.y);
+    if (launch_gemv(1, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
+                    p.max_tiles, offsets, (const uint8_t*)a->w1, a->w1_s,
+                    (const uint8_t*)a->w3, a->w3_s, I, H, nullptr, L, h, st))
+      return -1;
+    if (launch_gemv(1, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                    offsets, (const uint8_t*)a->w2, a->w2_s, nullptr, nullptr,
+                    H, I, w, 0.f, y, st))
+      return -1;
+    float* y_sh = nullptr;
+    if (sh) {
+      float* h_sh = (float*)(ws + p.hq_sh);
+      y_sh = (float*)(ws + p.y_sh);
+      if (launch_gemv(0, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
+                      nullptr, (const uint8_t*)a->s1, a->s1_s,
+                      (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L, h_sh,
+                      st))
+        return -1;
+      if (launch_gemv(0, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
+                      nullptr, (const uint8_t*)a->s2, a->s2_s, nullptr,
+                      nullptr, H, Is, nullptr, 0.f, y_sh, st))
+        return -1;
+    }
+    if (launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st))
+      return -1;
+  } else {
+    uint8_t* xq = (uint8_t*)(ws + p.xq);
+    float* sx = (float*)(ws + p.sx);
+    uint8_t* hq = (uint8_t*)(ws + p.hq);
+    float* hs = (float*)(ws + p.hs);
+    uint16_t* y = (uint16_t*)(ws + p.y);
+    if (launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx, nullptr,
+                         nullptr, st))
+      return -1;
+    if (launch_gemm1_mx(1, xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                        offsets, (const uint8_t*)a->w1, a->w1_s,
+                        (const uint8_t*)a->w3, a->w3_s, I, H, w, L, hq, hs, st))
+      return -1;
+    if (launch_gemm2_mx(1, hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+                        offsets, (const uint8_t*)a->w2, a->w2_s, I, H, y, st))
+      return -1;
+    uint16_t* y_sh = nullptr;
+    if (sh) {
+      uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
+      float* hs_sh = (float*)(ws + p.hs_sh);
+      y_sh = (uint16_t*)(ws + p.y_sh);
+      if (launch_gemm1_mx(0, xq, sx, nullptr, k, T, nullptr, nullptr, 0,
+                          nullptr, (const uint8_t*)a->s1, a->s1_s,
+                          (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L,
+                          hq_sh, hs_sh, st))
+        return -1;
+      if (launch_gemm2_mx(0, hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
+                          nullptr, (const uint8_t*)a->s2, a->s2_s, Is, H, y_sh,
+                          st))
+        return -1;
+    }
+    if (launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st))
+      return -1;
+  }
+  return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
+                    a->ids_out, a->counts_out, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+// Expert-major token permutation (dispatch) and the ragged tile table.
+//
+// The reference has no permute: its numpy oracle loops per token
+// (ref/qwen4_exp.py:175-179) or per expert with np.where
+// (ref/deepseek_v4.py:1080-1086, upstream ref/hf_sources/dsv4/model.py:
+// 689-695 torch.where(indices == i)). This file produces the same
+// grouping as an explicit permutation so that each expert's rows are
+// contiguous for the grouped GEMMs.
+//
+// Canonical order (bit-exact with oracle/permute.py): ascending expert id,
+// then ascending flat assignment index a = t*k + j, i.e.
+// np.argsort(ids.ravel(), kind="stable").
+//
+// Three kernels, all deterministic:
+//  1. hist:    chunks of PERM_CHUNK assignments, LDS histogram per chunk.
+//  2. scan:    one workgroup; per-expert exclusive scan over chunks, then an
+//              exclusive scan over experts (offsets), chunk bases, and the
+//              tile table {expert, first row} of ceil(count/bm) tiles/expert.
+//  3. scatter: one wave per chunk walks its assignments in order, 64 at a
+//              time; lanes holding the same expert are matched with one
+//              ballot per id bit, so the rank among equal ids is the popcount
+//              of lower matching lanes -- a stable, atomic-free scatter.
+#include "launch.h"
+
+namespace sllm {
+
+constexpr int PERM_CHUNK = 1024;
+
+__global__ __launch_bounds__(256) void permute_hist_kernel(
+    const int* __restrict__ ids, int N, int E, int* __restrict__ chunk_hist) {
+  extern __shared__ int h[];
+  const int c = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) h[e] = 0;
+  __syncthreads();
+  const int a0 = c * PERM_CHUNK, a1 = min(N, a0 + PERM_CHUNK);
+  for (int a = a0 + threadIdx.x; a < a1; a += blockDim.x) {
+    int e = ids[a];
+    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    chunk_hist[(size_t)c * E + e] = h[e];
+}
+
+// Block-wide exclusive scan of one value per thread (1024 threads).
+__device__ int block_excl_scan(int v, int* sh, int& total) {
+  const int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    int add = tid >= o ? sh[tid - o] : 0;
+    __syncthreads();
+    sh[tid] += add;
+    __syncthreads();
+  }
+  int incl = sh[tid];
+  total = sh[1023];
+  __syncthreads();
+  return incl - v;
+}
+
+__global__ __launch_bounds__(1024) void permute_scan_kernel(
+    int* __restrict__ chunk_hist, int nchunks, int E, int bm,
+    int* __restrict__ counts, int* __restrict__ offsets,
+    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles) {
+  __shared__ int sh[1024];
+  __shared__ int carry_rows, carry_tiles;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    carry_rows = 0;
+    carry_tiles = 0;
+  }
+  __syncthreads();
+  for (int e0 = 0; e0 < E; e0 += 1024) {
+    const int e = e0 + tid;
+    int cnt = 0;
+    if (e < E) {
+      for (int c = 0; c < nchunks; ++c) {
+        int v = chunk_hist[(size_t)c * E + e];
+        chunk_hist[(size_t)c * E + e] = cnt;  // exclusive within expert
+        cnt += v;
+      }
+    }
+    int ntile = (e < E && cnt > 0) ? (cnt + bm - 1) / bm : 0;
+    int tot_rows, tot_tiles;
+    int off = block_excl_scan(cnt, sh, tot_rows) + carry_rows;
+    int toff = block_excl_scan(ntile, sh, tot_tiles) + carry_tiles;
+    if (e < E) {
+      counts[e] = cnt;
+      offsets[e] = off;
+      for (int c = 0; c < nchunks; ++c) chunk_hist[(size_t)c * E + e] += off;
+      for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
+        tile_info[2 * (toff + i)] = e;
+        tile_info[2 * (toff + i) + 1] = i * bm;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      carry_rows += tot_rows;
+      carry_tiles += tot_tiles;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    offsets[E] = carry_rows;
+    *num_tiles = min(carry_tiles, max_tiles);
+  }
+}
+
+__global__ __launch_bounds__(64) void permute_scatter_kernel(
+    const int* __restrict__ ids, int N, int E, int nbits,
+    const int* __restrict__ chunk_base, int* __restrict__ sorted_idx,
+    int* __restrict__ inv_pos) {
+  extern __shared__ int run[];
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = chunk_base[(size_t)c * E + e];
+  __syncthreads();
+  const int a0 = c * PERM_CHUNK, a1 = min(N, a0 + PERM_CHUNK);
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int base = a0; base < a1; base += 64) {
+    const int a = base + lane;
+    const int raw = a < a1 ? ids[a] : -1;
+    const bool valid = raw >= 0 && raw < E;  // out-of-range ids are dropped
+    const int e = valid ? raw : 0;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const int bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    if (valid) {
+      const int rank = __popcll(peers & lt);
+      const int pos = run[e] + rank;
+      sorted_idx[pos] = a;
+      inv_pos[a] = pos;
+    }
+    __syncthreads();  // every lane has read run[] before it advances
+    if (valid && (peers >> lane) == 1ull) run[e] += __popcll(peers);
+    __syncthreads();
+  }
+}
+
+size_t permute_scratch_bytes(int N, int E) {
+  int nchunks = N > 0 ? (N + PERM_CHUNK - 1) / PERM_CHUNK : 1;
+  return align_up((size_t)nchunks * E * sizeof(int), 256);
+}
+
+// ids (N = T*k) int32 -> counts[E], offsets[E+1], sorted_idx[N], inv_pos[N],
+// tile_info[2*max_tiles] {expert, first row}, num_tiles[1].
+int launch_permute(const int* ids, int N, int E, int bm, int* counts,
+                   int* offsets, int* sorted_idx, int* inv_pos,
+                   int* tile_info, int* num_tiles, int max_tiles,
+                   void* scratch, hipStream_t st) {
+  SLLM_REQUIRE(ids && counts && offsets && sorted_idx && inv_pos &&
+                   tile_info && num_tiles && scratch,
+               "permute: null pointer");
+  SLLM_REQUIRE(N > 0 && E > 0 && E <= 4096 && bm > 0,
+               "permute: bad sizes (N=%d E=%d bm=%d)", N, E, bm);
+  const int nchunks = (N + PERM_CHUNK - 1) / PERM_CHUNK;
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  int* chunk_hist = (int*)scratch;
+  const size_t lds = (size_t)E * sizeof(int);
+  permute_hist_kernel<<<nchunks, 256, lds, st>>>(ids, N, E, chunk_hist);
+  SLLM_LAUNCHED();
+  permute_scan_kernel<<<1, 1024, 0, st>>>(chunk_hist, nchunks, E, bm, counts,
+                                          offsets, tile_info, num_tiles,
+                                          max_tiles);
+  SLLM_LAUNCHED();
+  permute_scatter_kernel<<<nchunks, 64, lds, st>>>(
+      ids, N, E, nbits, chunk_hist, sorted_idx, inv_pos);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+}  // namespace sllm
+
+using namespace sllm;
+
+extern "C" {
+
+long sllm_moe_permute_scratch_bytes(int N, int E) {
+  return (long)permute_scratch_bytes(N, E);
+}
+
+int sllm_moe_permute(const int* ids, int N, int E, int bm, int* counts,
+                     int* offsets, int* sorted_idx, int* inv_pos,
+                     int* tile_info, int* num_tiles, int max_tiles,
+                     void* scratch, void* stream) {
+  return launch_permute(ids, N, E, bm, counts, offsets, sorted_idx, inv_pos,
+                        tile_info, num_tiles, max_tiles, scratch,
+                        (hipStream_t)stream);
+}
+
+}  // extern "C"

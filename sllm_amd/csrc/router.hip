@@ -1,0 +1,438 @@
+// MoE router: logits GEMM and per-token top-k selection.
+//
+// Replaces kernels/cuda/qwen4.cu:229-298 + 785-793 (moe_router_kernel,
+// sllm_q4_moe_router(_dev)) and the numpy routing of ref/qwen4_exp.py:
+// 118-140 and ref/deepseek_v4.py:522-561.
+//
+// Design (gfx950): one wave64 per token. Lane l holds experts l, l+64, ...
+// so each logits row is read with coalesced loads; softmax max/sum and the
+// k rounds of arg-max are wave shuffles, never a serial thread-0 loop.
+//
+// Selection contract (bit-exact with the oracle):
+// - softmax routing selects by the fp32 LOGIT, ties to the lower expert id.
+//   Softmax is monotone, so this is the order of the exact probabilities;
+//   the oracle's fp32 probabilities can only disagree where two different
+//   logits round to the same probability (a certified rounding tie).
+// - sigmoid routing selects by the fp32 biased score s + bias, where
+//   s = fp32(1 / (1 + exp(-x))) is evaluated in fp64 as the reference does
+//   (ref/deepseek_v4.py:526-528), ties to the lower expert id.
+#include "launch.h"
+
+namespace sllm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// --------------------------------------------------------------------------
+// router GEMM: logits (T, E) fp32 = x (T, H) bf16 . W (E, H)^T bf16
+// --------------------------------------------------------------------------
+// WG = 4 waves, tile 64 tokens x 64 experts, each wave a 32x32 quadrant made
+// of 2x2 MFMA 16x16x32 bf16 subtiles. K advances 128 at a time; every lane
+// loads 64 contiguous bytes per row (4 MFMAs worth). The MFMA's K order is
+// irrelevant as long as both operands use the same lane->K assignment.
+constexpr int RG_TILE = 64;
+
+__global__ __launch_bounds__(256) void router_gemm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    float* __restrict__ logits, int T, int E, int H) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile_e = blockIdx.x, tile_t = blockIdx.y;
+  const int r0 = tile_t * RG_TILE + (wave >> 1) * 32;
+  const int c0 = tile_e * RG_TILE + (wave & 1) * 32;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  const uint16_t* arow[2];
+  const uint16_t* brow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int r = min(r0 + i * 16 + lr, T - 1);
+    int c = min(c0 + i * 16 + lr, E - 1);
+    arow[i] = x + (size_t)r * H + lg * 32;
+    brow[i] = w + (size_t)c * H + lg * 32;
+  }
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < H; k0 += 128) {
+    bf16x8 a[2][4], b[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[i][q] = *(const bf16x8*)(arow[i] + k0 + q * 8);
+        b[i][q] = *(const bf16x8*)(brow[i] + k0 + q * 8);
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+  }
+  // output layout of a 16x16 MFMA tile: lane l, element v holds
+  // row 4*(l/16)+v, column l%16
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        int r = r0 + i * 16 + lg * 4 + v;
+        int c = c0 + j * 16 + lr;
+        if (r < T && c < E) logits[(size_t)r * E + c] = acc[i][j][v];
+      }
+}
+
+// --------------------------------------------------------------------------
+// softmax top-k with renormalisation (ref/qwen4_exp.py:118-140)
+// --------------------------------------------------------------------------
+template <int EPL>
+__global__ __launch_bounds__(256) void route_softmax_kernel(
+    const float* __restrict__ logits, float* __restrict__ w_out,
+    int* __restrict__ id_out, int T, int E, int topk, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + (size_t)t * E;
+  float v[EPL];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : -INFINITY;
+    m = fmaxf(m, v[i]);
+  }
+  m = wave_max(m);
+  float p[EPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + 64 * i;
+    p[i] = e < E ? expf(v[i] - m) : 0.f;
+    s += p[i];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) p[i] = p[i] / s;
+
+  uint64_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + 64 * i;
+    key[i] = e < E ? (((uint64_t)f32_order_key(v[i]) << 32) |
+                      (uint64_t)(0xFFFFFFFFu - (uint32_t)e))
+                   : 0ull;
+  }
+  float wsum = 0.f;
+  float mine = 0.f;  // lane j < topk keeps slot j's probability
+  int myid = 0;
+  for (int kk = 0; kk < topk; ++kk) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+    int owner = e & 63, slot = e >> 6;
+    float pe = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane == owner && i == slot) {
+        pe = p[i];
+        key[i] = 0;
+      }
+    pe = __shfl(pe, owner, kWave);
+    wsum += pe;
+    if (lane == kk) {
+      mine = pe;
+      myid = e;
+    }
+  }
+  if (lane < topk) {
+    w_out[(size_t)t * topk + lane] = mine / (wsum + eps);
+    id_out[(size_t)t * topk + lane] = myid;
+  }
+}
+
+// --------------------------------------------------------------------------
+// scored routing with selection bias and optional group limit
+// (ref/deepseek_v4.py:522-561; group limit per DeepSeek-V3 noaux_tc)
+// --------------------------------------------------------------------------
+enum Scoring { SCORE_SOFTMAX = 0, SCORE_SIGMOID = 1, SCORE_SQRTSOFTPLUS = 2 };
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_grouped_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias,
+    float* __restrict__ w_out, int* __restrict__ id_out, int T, int E,
+    int topk, int n_group, int topk_group, int scoring, float route_scale) {
+  __shared__ float sb[4][EPL * 64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int t_raw = blockIdx.x * 4 + wv;
+  const bool active = t_raw < T;
+  const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
+  const float* row = logits + (size_t)t * E;
+  float sc[EPL];
+  if (scoring == SCORE_SOFTMAX) {
+    double m = -INFINITY;
+    double xv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      int e = lane + 64 * i;
+      xv[i] = e < E ? (double)row[e] : -INFINITY;
+      m = xv[i] > m ? xv[i] : m;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      double q = __shfl_xor(m, o, kWave);
+      m = q > m ? q : m;
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      xv[i] = (lane + 64 * i) < E ? exp(xv[i] - m) : 0.0;
+      s += xv[i];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sc[i] = (float)(xv[i] / s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      int e = lane + 64 * i;
+      double xv = e < E ? (double)row[e] : 0.0;
+      if (scoring == SCORE_SIGMOID) {
+        sc[i] = (float)(1.0 / (1.0 + exp(-xv)));
+      } else {
+        double sp = log1p(exp(-fabs(xv))) + (xv > 0.0 ? xv : 0.0);
+        sc[i] = sqrtf((float)sp);
+      }
+    }
+  }
+  float b[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + 64 * i;
+    b[i] = e < E ? sc[i] + (bias ? bias[e] : 0.f) : -INFINITY;
+  }
+  bool keep_all = n_group <= 1;
+  uint64_t gkeep = ~0ull;  // bit g set: group g kept (n_group <= 64)
+  if (!keep_all) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i < E) sb[wv][lane + 64 * i] = b[i];
+    __syncthreads();  // n_group is uniform: every wave of the block is here
+    const int gs = E / n_group;
+    // lane g < n_group: group score = sum of the two largest biased scores
+    uint64_t gkey = 0;
+    if (lane < n_group) {
+      float m1 = -INFINITY, m2 = -INFINITY;
+      for (int q = 0; q < gs; ++q) {
+        float val = sb[wv][lane * gs + q];
+        if (val > m1) {
+          m2 = m1;
+          m1 = val;
+        } else if (val > m2) {
+          m2 = val;
+        }
+      }
+      float gsum = m1 + m2;
+      gkey = ((uint64_t)f32_order_key(gsum) << 32) |
+             (uint64_t)(0xFFFFFFFFu - (uint32_t)lane);
+    }
+    gkeep = 0;
+    for (int r = 0; r < topk_group; ++r) {
+      uint64_t best = wave_max_u64(gkey);
+      int g = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+      gkeep |= 1ull << g;
+      if (lane == g) gkey = 0;
+    }
+  }
+  uint64_t key[EPL];
+  const int gs = keep_all ? E : E / n_group;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    int e = lane + 64 * i;
+    bool ok = e < E && (keep_all || ((gkeep >> (e / gs)) & 1ull));
+    key[i] = ok ? (((uint64_t)f32_order_key(b[i]) << 32) |
+                   (uint64_t)(0xFFFFFFFFu - (uint32_t)e))
+                : 0ull;
+  }
+  float wsum = 0.f, mine = 0.f;
+  int myid = 0;
+  for (int kk = 0; kk < topk; ++kk) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+    int owner = e & 63, slot = e >> 6;
+    float se = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane == owner && i == slot) {
+        se = sc[i];
+        key[i] = 0;
+      }
+    se = __shfl(se, owner, kWave);
+    wsum += se;
+    if (lane == kk) {
+      mine = se;
+      myid = e;
+    }
+  }
+  if (active && lane < topk) {
+    float wv_ = scoring == SCORE_SOFTMAX ? mine : mine / wsum;
+    w_out[(size_t)t * topk + lane] = wv_ * route_scale;
+    id_out[(size_t)t * topk + lane] = myid;
+  }
+}
+
+static int epl_for(int E) {
+  int epl = 1;
+  while (epl * 64 < E) epl *= 2;
+  return epl;
+}
+
+int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
+                       int T, int E, int H, hipStream_t st) {
+  SLLM_REQUIRE(x && w && logits, "router_gemm: null pointer");
+  SLLM_REQUIRE(T > 0 && E > 0 && H > 0 && H % 128 == 0,
+               "router_gemm: need T,E>0 and H %% 128 == 0 (T=%d E=%d H=%d)",
+               T, E, H);
+  dim3 grid(ceil_div(E, RG_TILE), ceil_div(T, RG_TILE));
+  router_gemm_kernel<<<grid, 256, 0, st>>>(x, w, logits, T, E, H);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_route_softmax(const float* logits, float* w, int* ids, int T,
+                         int E, int topk, float eps, hipStream_t st) {
+  SLLM_REQUIRE(logits && w && ids, "route_softmax: null pointer");
+  SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
+                   topk <= 64,
+               "route_softmax: need 0<topk<=E<=2048, topk<=64 (E=%d k=%d)",
+               E, topk);
+  dim3 grid(ceil_div(T, 4));
+  switch (epl_for(E)) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_softmax_kernel<n><<<grid, 256, 0, st>>>(logits, w, ids, T, E,       \
+                                                  topk, eps);                 \
+    break;
+    CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
+#undef CASE
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_route_grouped(const float* logits, const float* bias, float* w,
+                         int* ids, int T, int E, int topk, int n_group,
+                         int topk_group, int scoring, float route_scale,
+                         hipStream_t st) {
+  SLLM_REQUIRE(logits && w && ids, "route_grouped: null pointer");
+  SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
+                   topk <= 64,
+               "route_grouped: need 0<topk<=E<=2048, topk<=64");
+  SLLM_REQUIRE(scoring >= 0 && scoring <= 2, "route_grouped: bad scoring %d",
+               scoring);
+  if (n_group > 1) {
+    SLLM_REQUIRE(n_group <= 64 && E % n_group == 0 && topk_group >= 1 &&
+                     topk_group <= n_group &&
+                     topk_group * (E / n_group) >= topk,
+                 "route_grouped: bad group config (E=%d G=%d kg=%d k=%d)", E,
+                 n_group, topk_group, topk);
+  }
+  dim3 grid(ceil_div(T, 4));
+  switch (epl_for(E)) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_grouped_kernel<n><<<grid, 256, 0, st>>>(                            \
+        logits, bias, w, ids, T, E, topk, n_group, topk_group, scoring,       \
+        route_scale);                                                         \
+    break;
+    CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
+#undef CASE
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+}  // namespace sllm
+
+using namespace sllm;
+
+extern "C" {
+
+// ref: kernels/cuda/qwen4.cu:279-298 (host-pointer variant).
+int sllm_q4_moe_router(const float* logits, float* w_out, int* id_out, int n,
+                       int E, int topk) {
+  if (n <= 0 || E <= 0 || topk <= 0 || topk > E || E > 2048 || topk > 16) {
+    set_error("sllm_q4_moe_router: bad args (n=%d E=%d topk=%d)", n, E, topk);
+    return -1;
+  }
+  float *dl = nullptr, *dw = nullptr;
+  int* di = nullptr;
+  int rc = -1;
+  if (hipMalloc(&dl, (size_t)n * E * sizeof(float)) != hipSuccess ||
+      hipMalloc(&dw, (size_t)n * topk * sizeof(float)) != hipSuccess ||
+      hipMalloc(&di, (size_t)n * topk * sizeof(int)) != hipSuccess) {
+    set_error("sllm_q4_moe_router: hipMalloc failed");
+  } else if (hipMemcpy(dl, logits, (size_t)n * E * sizeof(float),
+                       hipMemcpyHostToDevice) != hipSuccess) {
+    set_error("sllm_q4_moe_router: H2D failed");
+  } else if (launch_route_softmax(dl, dw, di, n, E, topk, 1e-20f, 0) == 0 &&
+             hipMemcpy(w_out, dw, (size_t)n * topk * sizeof(float),
+                       hipMemcpyDeviceToHost) == hipSuccess &&
+             hipMemcpy(id_out, di, (size_t)n * topk * sizeof(int),
+                       hipMemcpyDeviceToHost) == hipSuccess) {
+    rc = 0;
+  } else if (last_error()[0] == 0) {
+    set_error("sllm_q4_moe_router: D2H failed");
+  }
+  (void)hipFree(dl);
+  (void)hipFree(dw);
+  (void)hipFree(di);
+  return rc;
+}
+
+// ref: kernels/cuda/qwen4.cu:785-793 (device-pointer variant, no sync).
+int sllm_q4_moe_router_dev(const float* logits, float* w_out, int* id_out,
+                           int n, int E, int topk) {
+  if (n <= 0 || E <= 0 || topk <= 0 || topk > E || E > 2048 || topk > 16) {
+    set_error("sllm_q4_moe_router_dev: bad args (n=%d E=%d topk=%d)", n, E,
+              topk);
+    return -1;
+  }
+  return launch_route_softmax(logits, w_out, id_out, n, E, topk, 1e-20f, 0);
+}
+
+int sllm_moe_router_gemm(const void* x_bf16, const void* w_bf16,
+                         float* logits, int T, int E, int H, void* stream) {
+  return launch_router_gemm((const uint16_t*)x_bf16, (const uint16_t*)w_bf16,
+                            logits, T, E, H, (hipStream_t)stream);
+}
+
+int sllm_moe_route_softmax(const float* logits, float* w_out, int* id_out,
+                           int T, int E, int topk, float eps, void* stream) {
+  return launch_route_softmax(logits, w_out, id_out, T, E, topk, eps,
+                              (hipStream_t)stream);
+}
+
+int sllm_moe_route_grouped(const float* logits, const float* bias,
+                           float* w_out, int* id_out, int T, int E, int topk,
+                           int n_group, int topk_group, int scoring,
+                           float route_scale, void* stream) {
+  return launch_route_grouped(logits, bias, w_out, id_out, T, E, topk,
+                              n_group, topk_group, scoring, route_scale,
+                              (hipStream_t)stream);
+}
+
+}  // extern "C"

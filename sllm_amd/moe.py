@@ -1,0 +1,317 @@
+"""Fused MoE layer entry points over libsllm_moe.so.
+
+The layer the reference computes in numpy (ref/qwen4_exp.py:153-184
+moe_block_forward; ref/deepseek_v4.py:1070-1087 Block.moe with the upstream
+combine of ref/hf_sources/dsv4/model.py:684-699) and, on the device, as a
+host loop of per-expert cuBLAS GEMVs (kernels/q4_device_decode.py:316-339).
+
+Two levels:
+- `qwen_forward_dev` / `deepseek_forward_dev`: device pointers in, device
+  pointers out, stream-ordered, no allocation (caller-owned workspace).
+  Buffers may be DeviceBuffer / DeviceView objects, torch tensors or raw
+  addresses.
+- `QwenMoE` / `DeepseekMoE`: device-resident weights uploaded once from host
+  arrays, with `forward(x)` taking and returning numpy arrays -- the drop-in
+  for `moe_block_forward` and for `Q4DeviceDecodeState._moe`.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from .runtime import DeviceBuffer, ptr, stream_handle, to_bf16, to_device, to_device_raw
+
+MODES = {"auto": 0, "prefill": 1, "decode": 2}
+SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+
+
+def _mode(m) -> int:
+    return MODES[m] if isinstance(m, str) else int(m)
+
+
+# ---------------------------------------------------------------------------
+# Qwen-style layer
+# ---------------------------------------------------------------------------
+
+def _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
+               weights, out, debug, workspace, workspace_bytes, stream):
+    a = _lib.QwenArgs()
+    a.T, a.H, a.E, a.I, a.Is, a.topk = T, H, E, I, Is, topk
+    a.mode = _mode(mode)
+    a.out_f32 = int(bool(out_f32))
+    a.logits_given = int(logits is not None)
+    a.wdtype = int(wdtype)
+    a.renorm_eps = float(eps)
+    a.x = ptr(x)
+    a.logits = ptr(logits)
+    w = weights
+    a.router_w = ptr(w.get("router_w"))
+    for k in ("wg", "wg_s", "wu", "wu_s", "wd", "wd_s", "sg", "sg_s", "su",
+              "su_s", "sd", "sd_s", "sgl"):
+        setattr(a, k, ptr(w.get(k)))
+    a.out = ptr(out)
+    debug = debug or {}
+    for k in ("logits_out", "w_out", "ids_out", "counts_out"):
+        setattr(a, k, ptr(debug.get(k)))
+    a.workspace = ptr(workspace)
+    a.workspace_bytes = int(workspace_bytes or 0)
+    a.stream = stream_handle(stream)
+    return a
+
+
+def qwen_workspace_bytes(T, H, E, I, Is, topk, mode="auto", has_shared=True,
+                         logits_given=False, wdtype=0) -> int:
+    """Workspace size for one qwen_forward_dev call of these shapes."""
+    w = {"su": 1} if has_shared else {}
+    a = _qwen_args(T, H, E, I, Is, topk, mode, False, wdtype, 1e-20, None,
+                   1 if logits_given else None, w, None, None, None, 0, None)
+    n = _lib.lib().sllm_moe_qwen_workspace_bytes(a)
+    if n < 0:
+        raise RuntimeError(_lib.last_error())
+    return int(n)
+
+
+def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
+                     mode="auto", out_f32=False, wdtype=0, eps=1e-20,
+                     logits=None, workspace=None, workspace_bytes=None,
+                     stream=None, debug=None) -> None:
+    """One Qwen-style MoE layer on device buffers (see include/sllm_moe.h
+    sllm_moe_qwen_args for shapes). `weights` maps router_w, wg, wg_s, wu,
+    wu_s, wd, wd_s [, sg, sg_s, su, su_s, sd, sd_s, sgl] to device buffers;
+    `debug` may map logits_out / w_out / ids_out / counts_out."""
+    if workspace_bytes is None:
+        workspace_bytes = getattr(workspace, "nbytes", None)
+        if workspace_bytes is None and hasattr(workspace, "numel"):
+            workspace_bytes = workspace.numel() * workspace.element_size()
+    a = _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
+                   weights, out, debug, workspace, workspace_bytes, stream)
+    _lib.check(_lib.lib().sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
+
+
+# ---------------------------------------------------------------------------
+# DeepSeek-style layer
+# ---------------------------------------------------------------------------
+
+def _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
+             scoring, route_scale, swiglu_limit, x, logits, weights, out,
+             debug, workspace, workspace_bytes, stream):
+    a = _lib.DeepseekArgs()
+    a.T, a.H, a.E, a.I, a.Is, a.topk = T, H, E, I, Is, topk
+    a.mode = _mode(mode)
+    a.out_f32 = int(bool(out_f32))
+    a.logits_given = int(logits is not None)
+    a.n_group, a.topk_group = int(n_group), int(topk_group)
+    a.scoring = SCORING[scoring] if isinstance(scoring, str) else int(scoring)
+    a.route_scale = float(route_scale)
+    a.swiglu_limit = float(swiglu_limit)
+    a.x = ptr(x)
+    a.logits = ptr(logits)
+    w = weights
+    for k in ("router_w", "bias", "w1", "w1_s", "w3", "w3_s", "w2", "w2_s",
+              "s1", "s1_s", "s3", "s3_s", "s2", "s2_s"):
+        setattr(a, k, ptr(w.get(k)))
+    a.out = ptr(out)
+    debug = debug or {}
+    for k in ("logits_out", "w_out", "ids_out", "counts_out"):
+        setattr(a, k, ptr(debug.get(k)))
+    a.workspace = ptr(workspace)
+    a.workspace_bytes = int(workspace_bytes or 0)
+    a.stream = stream_handle(stream)
+    return a
+
+
+def deepseek_workspace_bytes(T, H, E, I, Is, topk, mode="auto",
+                             has_shared=True, logits_given=False) -> int:
+    w = {"s1": 1} if has_shared else {}
+    a = _ds_args(T, H, E, I, Is, topk, mode, False, 1, 1, 1, 1.0, 0.0, None,
+                 1 if logits_given else None, w, None, None, None, 0, None)
+    n = _lib.lib().sllm_moe_ds_workspace_bytes(a)
+    if n < 0:
+        raise RuntimeError(_lib.last_error())
+    return int(n)
+
+
+def deepseek_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
+                         mode="auto", out_f32=False, n_group=1, topk_group=1,
+                         scoring="sigmoid", route_scale=1.0, swiglu_limit=0.0,
+                         logits=None, workspace=None, workspace_bytes=None,
+                         stream=None, debug=None) -> None:
+    """One DeepSeek-style MoE layer on device buffers (shapes in
+    include/sllm_moe.h sllm_moe_ds_args). `weights` maps router_w, bias, w1,
+    w1_s, w3, w3_s, w2, w2_s [, s1, s1_s, s3, s3_s, s2, s2_s]."""
+    if workspace_bytes is None:
+        workspace_bytes = getattr(workspace, "nbytes", None)
+        if workspace_bytes is None and hasattr(workspace, "numel"):
+            workspace_bytes = workspace.numel() * workspace.element_size()
+    a = _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
+                 scoring, route_scale, swiglu_limit, x, logits, weights, out,
+                 debug, workspace, workspace_bytes, stream)
+    _lib.check(_lib.lib().sllm_moe_ds_forward(a), "sllm_moe_ds_forward")
+
+
+# ---------------------------------------------------------------------------
+# device-resident layers with numpy in / out
+# ---------------------------------------------------------------------------
+
+def _up(arr, raw=True):
+    if arr is None:
+        return None
+    return to_device_raw(np.ascontiguousarray(arr)) if raw else to_device(arr)
+
+
+@dataclass
+class _Resident:
+    bufs: dict = field(default_factory=dict)
+
+    def get(self, k):
+        return self.bufs.get(k)
+
+
+class QwenMoE:
+    """Qwen-style layer with device-resident weights.
+
+    FP8 weights: e4m3 codes (uint8) with fp32 block scales, reference
+    orientation (out, in): wg/wu (E, I, H), wd (E, H, I), scales
+    (E, ceil(out/128), ceil(in/128)); shared sg/su (Is, H), sd (H, Is).
+    bf16 weights (wdtype=1): float arrays (rounded to bf16), no scales.
+    router_w (E, H) and sgl (1, H) are rounded to bf16.
+    """
+
+    def __init__(self, router_w, wg, wu, wd, wg_s=None, wu_s=None, wd_s=None,
+                 sg=None, su=None, sd=None, sg_s=None, su_s=None, sd_s=None,
+                 sgl=None, top_k=8, eps=1e-20):
+        self.wdtype = 0 if wg_s is not None else 1
+        self.E, self.I, self.H = np.asarray(wg).shape
+        self.Is = 0 if su is None else np.asarray(su).shape[0]
+        self.top_k = int(top_k)
+        self.eps = float(eps)
+        cast = (lambda a: np.ascontiguousarray(a, np.uint8)) if self.wdtype == 0 \
+            else (lambda a: to_bf16(a))
+        b = {"router_w": _up(to_bf16(router_w)),
+             "wg": _up(cast(wg)), "wu": _up(cast(wu)), "wd": _up(cast(wd))}
+        if self.wdtype == 0:
+            b.update(wg_s=_up(np.asarray(wg_s, np.float32)),
+                     wu_s=_up(np.asarray(wu_s, np.float32)),
+                     wd_s=_up(np.asarray(wd_s, np.float32)))
+        if su is not None:
+            b.update(sg=_up(cast(sg)), su=_up(cast(su)), sd=_up(cast(sd)),
+                     sgl=_up(to_bf16(np.asarray(sgl).reshape(-1))))
+            if self.wdtype == 0:
+                b.update(sg_s=_up(np.asarray(sg_s, np.float32)),
+                         su_s=_up(np.asarray(su_s, np.float32)),
+                         sd_s=_up(np.asarray(sd_s, np.float32)))
+        self._w = b
+        self._ws = None
+
+    def _workspace(self, T, mode, logits_given):
+        n = qwen_workspace_bytes(T, self.H, self.E, self.I, self.Is, self.top_k,
+                                 mode, self.Is > 0, logits_given, self.wdtype)
+        if self._ws is None or self._ws.nbytes < n:
+            self._ws = DeviceBuffer(n)
+        return self._ws
+
+    def forward(self, x, logits=None, mode="auto", return_routing=False):
+        """x (T, H) float (rounded to bf16) -> out (T, H) float32."""
+        x = np.asarray(x, np.float32)
+        T = x.shape[0]
+        xb = _up(to_bf16(x))
+        lg = _up(np.asarray(logits, np.float32)) if logits is not None else None
+        out = DeviceBuffer(T * self.H * 4)
+        dbg = {}
+        if return_routing:
+            dbg = {"logits_out": DeviceBuffer(T * self.E * 4),
+                   "w_out": DeviceBuffer(T * self.top_k * 4),
+                   "ids_out": DeviceBuffer(T * self.top_k * 4),
+                   "counts_out": DeviceBuffer(self.E * 4)}
+        ws = self._workspace(T, mode, logits is not None)
+        qwen_forward_dev(xb, out, self._w, T=T, H=self.H, E=self.E, I=self.I,
+                         Is=self.Is, topk=self.top_k, mode=mode, out_f32=True,
+                         wdtype=self.wdtype, eps=self.eps, logits=lg,
+                         workspace=ws, debug=dbg)
+        y = out.copy_host().reshape(T, self.H)
+        if not return_routing:
+            return y
+        r = {"logits": dbg["logits_out"].copy_host().reshape(T, self.E),
+             "w": dbg["w_out"].copy_host().reshape(T, self.top_k),
+             "ids": dbg["ids_out"].copy_host_raw(np.int32, (T, self.top_k)),
+             "counts": dbg["counts_out"].copy_host_raw(np.int32, (self.E,))}
+        return y, r
+
+
+class DeepseekMoE:
+    """DeepSeek-style layer with device-resident weights: routed MXFP4
+    (w1/w3 (E, I, H/2) packed + (E, I, H/32) e8m0; w2 (E, H, I/2) + (E, H,
+    I/32)), optional FP8 shared expert with power-of-two fp32 block scales."""
+
+    def __init__(self, router_w, bias, w1, w1_s, w3, w3_s, w2, w2_s, s1=None,
+                 s1_s=None, s3=None, s3_s=None, s2=None, s2_s=None, top_k=8,
+                 n_group=1, topk_group=1, scoring="sigmoid", route_scale=1.0,
+                 swiglu_limit=0.0):
+        self.E, self.I = np.asarray(w1).shape[:2]
+        self.H = np.asarray(w2).shape[1]
+        self.Is = 0 if s1 is None else np.asarray(s1).shape[0]
+        self.top_k, self.n_group, self.topk_group = int(top_k), int(n_group), int(topk_group)
+        self.scoring, self.route_scale = scoring, float(route_scale)
+        self.swiglu_limit = float(swiglu_limit)
+        b = {"router_w": _up(to_bf16(router_w)),
+             "bias": _up(np.asarray(bias, np.float32)) if bias is not None else None}
+        for k, v in (("w1", w1), ("w1_s", w1_s), ("w3", w3), ("w3_s", w3_s),
+                     ("w2", w2), ("w2_s", w2_s)):
+            b[k] = _up(np.ascontiguousarray(v, np.uint8))
+        if s1 is not None:
+            for k, v in (("s1", s1), ("s3", s3), ("s2", s2)):
+                b[k] = _up(np.ascontiguousarray(v, np.uint8))
+            for k, v in (("s1_s", s1_s), ("s3_s", s3_s), ("s2_s", s2_s)):
+                b[k] = _up(np.asarray(v, np.float32))
+        self._w = b
+        self._ws = None
+
+    def forward(self, x, logits=None, mode="auto", return_routing=False):
+        x = np.asarray(x, np.float32)
+        T = x.shape[0]
+        n = deepseek_workspace_bytes(T, self.H, self.E, self.I, self.Is,
+                                     self.top_k, mode, self.Is > 0,
+                                     logits is not None)
+        if self._ws is None or self._ws.nbytes < n:
+            self._ws = DeviceBuffer(n)
+        xb = _up(to_bf16(x))
+        lg = _up(np.asarray(logits, np.float32)) if logits is not None else None
+        out = DeviceBuffer(T * self.H * 4)
+        dbg = {}
+        if return_routing:
+            dbg = {"logits_out": DeviceBuffer(T * self.E * 4),
+                   "w_out": DeviceBuffer(T * self.top_k * 4),
+                   "ids_out": DeviceBuffer(T * self.top_k * 4),
+                   "counts_out": DeviceBuffer(self.E * 4)}
+        deepseek_forward_dev(xb, out, self._w, T=T, H=self.H, E=self.E,
+                             I=self.I, Is=self.Is, topk=self.top_k, mode=mode,
+                             out_f32=True, n_group=self.n_group,
+                             topk_group=self.topk_group, scoring=self.scoring,
+                             route_scale=self.route_scale,
+                             swiglu_limit=self.swiglu_limit, logits=lg,
+                             workspace=self._ws, debug=dbg)
+        y = out.copy_host().reshape(T, self.H)
+        if not return_routing:
+            return y
+        r = {"logits": dbg["logits_out"].copy_host().reshape(T, self.E),
+             "w": dbg["w_out"].copy_host().reshape(T, self.top_k),
+             "ids": dbg["ids_out"].copy_host_raw(np.int32, (T, self.top_k)),
+             "counts": dbg["counts_out"].copy_host_raw(np.int32, (self.E,))}
+        return y, r
+
+
+def moe_block_forward(x, router_w, expert_gate, expert_up, expert_down,
+                      shared_gate_w, shared_gate_linear_w, shared_up_w,
+                      shared_down_w, top_k, eps=1e-20):
+    """Device twin of ref/qwen4_exp.py:153-184 moe_block_forward with the
+    same signature: weights are float arrays used at bf16 precision (the
+    bf16 GEMV path, fp32 activations). Returns (n, H) float32."""
+    layer = QwenMoE(router_w, expert_gate, expert_up, expert_down,
+                    sg=shared_gate_w if shared_up_w is not None else None,
+                    su=shared_up_w, sd=shared_down_w,
+                    sgl=shared_gate_linear_w if shared_up_w is not None else None,
+                    top_k=top_k, eps=eps)
+    return layer.forward(x)

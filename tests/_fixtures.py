@@ -1,0 +1,193 @@
+"""Synthetic MoE layers for the tests (seeded numpy, oracle quantizers).
+
+Generation follows the BASELINE config recipes: activations bf16 N(0,1),
+weights N(0, 0.02) quantized to e4m3 with fp32 128x128 block scales
+(amax/448) or to MXFP4 (e2m1 + e8m0 per 32), router weights bf16
+N(0, 0.02), DeepSeek selection bias N(0, 0.01).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import codecs, quant
+from oracle import deepseek_moe as dm
+from oracle import qwen_moe as qm
+
+bf = codecs.round_bf16
+
+
+def qwen_fp8(seed=0, T=64, H=512, E=8, I=256, Is=256, shared=True,
+             x_scale=1.0):
+    rng = np.random.default_rng(seed)
+    x = bf((rng.standard_normal((T, H)) * x_scale).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+
+    def qw(n, k):
+        return quant.quantize_weight_fp8_block(
+            (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    g = [qw(I, H) for _ in range(E)]
+    u = [qw(I, H) for _ in range(E)]
+    d = [qw(H, I) for _ in range(E)]
+    W = qm.QwenFp8Weights(
+        router_w=rw,
+        wg_q=np.stack([a for a, _ in g]), wg_s=np.stack([b for _, b in g]),
+        wu_q=np.stack([a for a, _ in u]), wu_s=np.stack([b for _, b in u]),
+        wd_q=np.stack([a for a, _ in d]), wd_s=np.stack([b for _, b in d]))
+    if shared:
+        (W.sg_q, W.sg_s), (W.su_q, W.su_s), (W.sd_q, W.sd_s) = \
+            qw(Is, H), qw(Is, H), qw(H, Is)
+        W.sgl = bf((rng.standard_normal((1, H)) * 0.02).astype(np.float32))
+    return x, W
+
+
+def _gpu_normal(gen, rows, cols, std):
+    import torch
+    return torch.randn((rows, cols), generator=gen, device="cuda",
+                       dtype=torch.float32) * std
+
+
+def _gpu_fp8(gen, E, N, K, pow2=False):
+    """E stacked (N, K) weights ~N(0, 0.02) quantized on the device with
+    sllm_quantize_weight_fp8 (bit-exact with oracle.quant, see
+    test_gpu_kernels.py) -> host (q (E,N,K) uint8, s (E,N/128,K/128))."""
+    import torch
+    from sllm_amd import _lib
+    assert N % 128 == 0
+    w = _gpu_normal(gen, E * N, K, 0.02)
+    q = torch.empty((E * N, K), dtype=torch.uint8, device="cuda")
+    sc = torch.empty((E * N // 128, -(-K // 128)), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.lib().sllm_quantize_weight_fp8(w.data_ptr(), E * N, K, int(pow2),
+                                                   q.data_ptr(), sc.data_ptr(), None))
+    torch.cuda.synchronize()
+    del w
+    return (q.cpu().numpy().reshape(E, N, K),
+            sc.cpu().numpy().reshape(E, N // 128, -(-K // 128)))
+
+
+def _gpu_fp4(gen, E, N, K):
+    import torch
+    from sllm_amd import _lib
+    w = _gpu_normal(gen, E * N, K, 0.02)
+    p = torch.empty((E * N, K // 2), dtype=torch.uint8, device="cuda")
+    sc = torch.empty((E * N, K // 32), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.lib().sllm_quantize_weight_mxfp4(w.data_ptr(), E * N, K,
+                                                     p.data_ptr(), sc.data_ptr(), None))
+    torch.cuda.synchronize()
+    del w
+    return (p.cpu().numpy().reshape(E, N, K // 2),
+            sc.cpu().numpy().reshape(E, N, K // 32))
+
+
+def qwen_fp8_gpu(seed=0, T=64, H=2048, E=128, I=512, Is=512, shared=True):
+    """qwen_fp8 with the expert weights generated and quantized on the GPU
+    (seeded torch generator): the numpy route is minutes at C2 geometry."""
+    import torch
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    g, u, d = _gpu_fp8(gen, E, I, H), _gpu_fp8(gen, E, I, H), _gpu_fp8(gen, E, H, I)
+    W = qm.QwenFp8Weights(router_w=rw, wg_q=g[0], wg_s=g[1], wu_q=u[0],
+                          wu_s=u[1], wd_q=d[0], wd_s=d[1])
+    if shared:
+        sg, su, sd = _gpu_fp8(gen, 1, Is, H), _gpu_fp8(gen, 1, Is, H), _gpu_fp8(gen, 1, H, Is)
+        W.sg_q, W.sg_s = sg[0][0], sg[1][0]
+        W.su_q, W.su_s = su[0][0], su[1][0]
+        W.sd_q, W.sd_s = sd[0][0], sd[1][0]
+        W.sgl = bf((rng.standard_normal((1, H)) * 0.02).astype(np.float32))
+    return x, W
+
+
+def deepseek_mxfp4_gpu(seed=0, T=64, H=7168, E=32, I=2048, Is=2048, shared=True):
+    import torch
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    w1, w3, w2 = _gpu_fp4(gen, E, I, H), _gpu_fp4(gen, E, I, H), _gpu_fp4(gen, E, H, I)
+    W = dm.DeepseekMxfp4Weights(router_w=rw, bias=bias, w1_p=w1[0], w1_s=w1[1],
+                                w3_p=w3[0], w3_s=w3[1], w2_p=w2[0], w2_s=w2[1])
+    if shared:
+        s1, s3, s2 = (_gpu_fp8(gen, 1, Is, H, True), _gpu_fp8(gen, 1, Is, H, True),
+                      _gpu_fp8(gen, 1, H, Is, True))
+        W.s1_q, W.s1_s = s1[0][0], s1[1][0]
+        W.s3_q, W.s3_s = s3[0][0], s3[1][0]
+        W.s2_q, W.s2_s = s2[0][0], s2[1][0]
+    return x, W
+
+
+def qwen_layer(W, top_k):
+    from sllm_amd.moe import QwenMoE
+    kw = {}
+    if W.has_shared:
+        kw = dict(sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
+                  sd_s=W.sd_s, sgl=W.sgl)
+    return QwenMoE(W.router_w, W.wg_q, W.wu_q, W.wd_q, W.wg_s, W.wu_s,
+                   W.wd_s, top_k=top_k, **kw)
+
+
+def deepseek_mxfp4(seed=0, T=64, H=512, E=16, I=256, Is=256, shared=True):
+    rng = np.random.default_rng(seed)
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+
+    def q4(n, k):
+        return quant.quantize_weight_mxfp4(
+            (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+
+    def q8(n, k):
+        return quant.quantize_weight_fp8_block(
+            (rng.standard_normal((n, k)) * 0.02).astype(np.float32), pow2=True)
+    w1 = [q4(I, H) for _ in range(E)]
+    w3 = [q4(I, H) for _ in range(E)]
+    w2 = [q4(H, I) for _ in range(E)]
+    W = dm.DeepseekMxfp4Weights(
+        router_w=rw, bias=bias,
+        w1_p=np.stack([a for a, _ in w1]), w1_s=np.stack([b for _, b in w1]),
+        w3_p=np.stack([a for a, _ in w3]), w3_s=np.stack([b for _, b in w3]),
+        w2_p=np.stack([a for a, _ in w2]), w2_s=np.stack([b for _, b in w2]))
+    if shared:
+        (W.s1_q, W.s1_s), (W.s3_q, W.s3_s), (W.s2_q, W.s2_s) = \
+            q8(Is, H), q8(Is, H), q8(H, Is)
+    return x, W
+
+
+def deepseek_layer(W, top_k, **route):
+    from sllm_amd.moe import DeepseekMoE
+    kw = {}
+    if W.has_shared:
+        kw = dict(s1=W.s1_q, s1_s=W.s1_s, s3=W.s3_q, s3_s=W.s3_s, s2=W.s2_q,
+                  s2_s=W.s2_s)
+    return DeepseekMoE(W.router_w, W.bias, W.w1_p, W.w1_s, W.w3_p, W.w3_s,
+                       W.w2_p, W.w2_s, top_k=top_k, **kw, **route)
+
+
+def rel_l2(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def certified_route_ties(ids_dev, ids_ref, p_ref) -> int:
+    """Count positions where device and oracle ids differ but the oracle's
+    fp32 probabilities of the two experts are bitwise equal (a rounding
+    tie that only the logit order can break). Raises on any other
+    mismatch."""
+    bad = np.argwhere(ids_dev != ids_ref)
+    ties = 0
+    for t, j in bad:
+        a, b = int(ids_dev[t, j]), int(ids_ref[t, j])
+        if p_ref[t, a] == p_ref[t, b]:
+            ties += 1
+        else:
+            raise AssertionError(
+                f"routing mismatch at token {t} slot {j}: device {a} "
+                f"(p={p_ref[t, a]!r}) vs oracle {b} (p={p_ref[t, b]!r})")
+    return ties

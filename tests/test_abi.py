@@ -1,0 +1,72 @@
+"""CPU checks of the drop-in boundary: the library loads without a GPU and
+exports every function include/sllm_moe.h declares; the ctypes signature
+table covers the same set; the argument structs match the header."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    src = open(os.path.join(ROOT, "include", "sllm_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"\b(sllm_\w+)\s*\(", src)
+    return sorted(set(names))
+
+
+def test_header_declares_reference_names():
+    names = _header_functions()
+    for ref in ("sllm_q4_moe_router", "sllm_q4_moe_router_dev", "sllm_q4_swiglu",
+                "sllm_q4_axpy_rows", "sllm_q4_shared_gate_accum", "sllm_fp8_gemm",
+                "sllm_fp8_gemm_dev", "sllm_ds_fp4_gemm", "sllm_buf_new",
+                "sllm_buf_free", "sllm_buf_h2d", "sllm_buf_h2d_raw", "sllm_buf_d2h",
+                "sllm_mem_free_bytes", "sllm_sync", "sllm_device_count",
+                "sllm_last_error", "sllm_q4_last_error", "sllm_fp8_last_error",
+                "sllm_ds_last_error", "sllm_gemm_ex"):
+        assert ref in names, ref
+
+
+def test_library_exports_every_declared_symbol():
+    from sllm_amd import _lib
+    if not os.path.isfile(_lib.LIB_PATH):
+        pytest.fail("library not built: run python -m sllm_amd.build")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _header_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(_lib.SIGNATURES) == _header_functions()
+    assert _lib.available()
+
+
+def test_struct_layout_matches_header():
+    from sllm_amd import _lib
+    src = open(os.path.join(ROOT, "include", "sllm_moe.h")).read()
+    for cname, py in (("sllm_moe_qwen_args", _lib.QwenArgs),
+                      ("sllm_moe_ds_args", _lib.DeepseekArgs)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), src,
+                         re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        fields = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            parts = decl.replace("*", " ").split()
+            names = " ".join(parts[1:]).replace(",", " ").split()
+            if parts[0] == "const":
+                names = " ".join(parts[2:]).replace(",", " ").split()
+            fields += names
+        assert [f for f, _ in py._fields_] == fields, cname
+
+
+def test_error_contract_without_gpu():
+    from sllm_amd import _lib, q4
+    lib = _lib.lib()
+    rc = lib.sllm_q4_moe_router(None, None, None, 0, 4, 2)
+    assert rc == -1
+    assert "bad args" in _lib.last_error()
+    with pytest.raises(RuntimeError, match="rc=-1"):
+        _lib.check(rc, "q4 kernel")
+    assert q4.available()

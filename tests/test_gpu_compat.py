@@ -1,0 +1,128 @@
+"""GPU parity of the reference-named C-ABI surface (the drop-in boundary):
+the restated reference kernel tests (tests/test_qwen4_kernels.py:81-97,
+tests/test_fp8_gemm.py:44-68, tests/test_deepseek_cuda.py:18-30) plus the
+scale-orientation case the reference's 1x1-scale test cannot see."""
+import numpy as np
+import pytest
+
+from oracle import codecs, quant
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib_loaded():
+    from sllm_amd import _lib
+    if not _lib.available():
+        pytest.fail(f"libsllm_moe.so not loadable: {_lib._lib_error}")
+
+
+def _silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def test_swiglu_axpy_shared_gate():
+    from sllm_amd import q4
+    rng = np.random.default_rng(34)
+    g = rng.standard_normal((3, 6)).astype(np.float32)
+    u = rng.standard_normal((3, 6)).astype(np.float32)
+    np.testing.assert_allclose(q4.swiglu(g, u), _silu(g) * u, rtol=1e-5, atol=1e-7)
+    out = rng.standard_normal((3, 6)).astype(np.float32)
+    y = rng.standard_normal((3, 6)).astype(np.float32)
+    w = rng.random(3).astype(np.float32)
+    np.testing.assert_allclose(q4.axpy_rows(out, y, w), out + w[:, None] * y,
+                               rtol=1e-6, atol=1e-7)
+    gate = rng.standard_normal(3).astype(np.float32)
+    sh = rng.standard_normal((3, 6)).astype(np.float32)
+    np.testing.assert_allclose(q4.shared_gate_accum(out, sh, gate),
+                               out + (1.0 / (1.0 + np.exp(-gate)))[:, None] * sh,
+                               rtol=1e-5, atol=1e-7)
+
+
+def test_dev_variants_match_host():
+    from sllm_amd import q4
+    from sllm_amd.runtime import DeviceBuffer, sync, to_device
+    rng = np.random.default_rng(35)
+    logits = rng.standard_normal((40, 128)).astype(np.float32)
+    w_h, ids_h = q4.moe_router(logits, 8)
+    w_d, i_d = DeviceBuffer(40 * 8 * 4), DeviceBuffer(40 * 8 * 4)
+    q4.moe_router_dev(to_device(logits), w_d, i_d, 40, 128, 8)
+    sync()
+    np.testing.assert_array_equal(w_d.copy_host().reshape(40, 8), w_h)
+    np.testing.assert_array_equal(i_d.copy_host_raw(np.int32, (40, 8)), ids_h)
+    g = rng.standard_normal(1000).astype(np.float32)
+    u = rng.standard_normal(1000).astype(np.float32)
+    o = DeviceBuffer(4000)
+    q4.swiglu_dev(to_device(g), to_device(u), o, 1000)
+    sync()
+    np.testing.assert_array_equal(o.copy_host(), q4.swiglu(g, u))
+
+
+def test_router_rejects_bad_args():
+    from sllm_amd import q4
+    with pytest.raises(RuntimeError, match="rc=-1"):
+        q4.moe_router(np.zeros((2, 4), np.float32), 5)     # topk > E
+    with pytest.raises(RuntimeError, match="rc=-1"):
+        q4.moe_router(np.zeros((2, 4096), np.float32), 4)  # E > 2048
+
+
+def test_fp8_gemm_reference_cases():
+    from sllm_amd import fp8
+    rng = np.random.default_rng(7)
+    M, N, K = 4, 5, 64
+    a = rng.standard_normal((M, K)).astype(np.float32) * 0.1
+    b8 = codecs.encode_e4m3fn_rne(np.clip(rng.standard_normal((N, K)).astype(np.float32)
+                                          * 0.05, -448, 448))
+    scale = (rng.standard_normal((1, 1)).astype(np.float32) * 0.5 + 1.0)
+    want = codecs.dequant_fp8_block(b8, scale)
+    np.testing.assert_allclose(fp8.fp8_gemm(a, b8, scale), a @ want.T, rtol=2e-4, atol=2e-4)
+
+
+def test_fp8_gemm_scale_orientation():
+    """Non-square scale grid: (ceil(N/128), ceil(K/128)) N-block-major, the
+    loader's orientation (loaders/fp8.py:98-135)."""
+    from sllm_amd import fp8
+    rng = np.random.default_rng(8)
+    M, N, K = 7, 300, 200
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b8 = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    b8[(b8 & 0x7F) == 0x7F] = 0x30
+    scale = (rng.random((3, 2)) + 0.5).astype(np.float32)
+    want = a.astype(np.float64) @ codecs.dequant_fp8_block(b8, scale).astype(np.float64).T
+    got = fp8.fp8_gemm(a, b8, scale)
+    mag = np.abs(a) @ np.abs(codecs.dequant_fp8_block(b8, scale)).T
+    assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6)
+    # other block shapes
+    s2 = (rng.random((5, 4)) + 0.5).astype(np.float32)
+    got2 = fp8.fp8_gemm(a, b8, s2, 64, 64)
+    want2 = a @ codecs.dequant_fp8_block(b8, s2, (64, 64)).T
+    np.testing.assert_allclose(got2, want2, rtol=1e-4, atol=1e-3)
+
+
+def test_fp4_linear_matches_dequant():
+    from sllm_amd import deepseek
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    w = (rng.standard_normal((6, 64)) * 0.1).astype(np.float32)
+    packed, s = quant.quantize_weight_mxfp4(w)
+    got = deepseek.fp4_moe_linear(x, packed, s)
+    want = x @ codecs.dequant_fp4_block(packed, s).T
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    got2 = deepseek.fp4_gemm_dequantized(x, codecs.dequant_fp4_block(packed, s))
+    np.testing.assert_allclose(got2, want, rtol=1e-5, atol=1e-6)
+
+
+def test_gemm_ex_f32_and_bf16():
+    from sllm_amd.runtime import DeviceBuffer, T_BF16, T_F32, gemm_ex, sync, to_bf16, to_device, to_device_raw
+    rng = np.random.default_rng(9)
+    m, n, k = 1, 300, 257
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    c = DeviceBuffer(m * n * 4)
+    gemm_ex(to_device(a), to_device(w), c, m, n, k, T_F32)
+    sync()
+    np.testing.assert_allclose(c.copy_host().reshape(m, n), a @ w.T, rtol=1e-4, atol=1e-4)
+    gemm_ex(to_device_raw(to_bf16(a)), to_device_raw(to_bf16(w)), c, m, n, k, T_BF16)
+    sync()
+    ab, wb = codecs.round_bf16(a), codecs.round_bf16(w)
+    np.testing.assert_allclose(c.copy_host().reshape(m, n), ab @ wb.T, rtol=1e-4, atol=1e-4)

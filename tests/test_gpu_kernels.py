@@ -1,0 +1,231 @@
+"""GPU parity of the layer's building blocks against the oracle, through the
+C-ABI (libsllm_moe.so). Integer / byte / index results are compared bit for
+bit; fp32 routing weights to rtol 1e-5 (the reference kernel test's bar,
+tests/test_qwen4_kernels.py:73-79)."""
+import numpy as np
+import pytest
+
+from oracle import codecs, quant
+from oracle import deepseek_moe as dm
+from oracle import qwen_moe as qm
+from oracle.permute import permute as oracle_permute
+
+from tests._fixtures import certified_route_ties
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def L():
+    from sllm_amd import _lib
+    if not _lib.available():
+        pytest.fail(f"libsllm_moe.so not loadable: {_lib._lib_error}")
+    return _lib
+
+
+def dev(a):
+    from sllm_amd.runtime import to_device_raw
+    return to_device_raw(np.ascontiguousarray(a))
+
+
+def empty(nbytes):
+    from sllm_amd.runtime import DeviceBuffer
+    return DeviceBuffer(max(int(nbytes), 4))
+
+
+def host(buf, dtype, shape):
+    from sllm_amd.runtime import sync
+    sync()
+    n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+    return buf.copy_host_raw(np.uint8)[:n].view(dtype).reshape(shape)
+
+
+# ---------------------------------------------------------------- codecs --
+
+def test_hw_e4m3_decode_all_codes(L):
+    """fp8 GEMM with an identity A reproduces every finite e4m3 code."""
+    from sllm_amd import fp8
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    K = 256
+    B = np.zeros((1, K), np.uint8)
+    B[0, :codes.size] = codes
+    A = np.eye(K, dtype=np.float32)
+    got = fp8.fp8_gemm(A, B, np.ones((1, 2), np.float32), 128, 128)[:, 0]
+    want = codecs.decode_e4m3fn(B[0])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_act_quant_bit_exact(L):
+    import os
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "codecs.npz"))
+    rng = np.random.default_rng(0)
+    T, H = 256, 2048
+    x = codecs.round_bf16((rng.standard_normal((T, H)) *
+                           rng.uniform(0.01, 30, (T, 1))).astype(np.float32))
+    # include exact e4m3 midpoints scaled so that s = 1 (amax 448)
+    mids = gold["enc_x"][:H - 1]
+    x[0, :H - 1] = codecs.round_bf16(mids)
+    x[0, H - 1] = 448.0
+    xb = dev(codecs.encode_bf16_rne(x))
+    for pow2 in (0, 1):
+        q = empty(T * H)
+        s = empty(T * (H // 128) * 4)
+        L.check(L.lib().sllm_moe_act_quant(xb.ptr, T, H, pow2, q.ptr, s.ptr,
+                                           None, None, None))
+        qh = host(q, np.uint8, (T, H))
+        sh = host(s, np.float32, (T, H // 128))
+        qr, sr = quant.act_quant(x, pow2=bool(pow2))
+        np.testing.assert_array_equal(sh.view(np.uint32), sr.view(np.uint32))
+        np.testing.assert_array_equal(qh, qr)
+
+
+def test_act_quant_gate(L):
+    rng = np.random.default_rng(1)
+    T, H = 37, 1024
+    x = codecs.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    gw = codecs.round_bf16((rng.standard_normal(H) * 0.02).astype(np.float32))
+    q, s, g = empty(T * H), empty(T * H // 128 * 4), empty(T * 4)
+    L.check(L.lib().sllm_moe_act_quant(dev(codecs.encode_bf16_rne(x)).ptr, T, H, 0,
+                                       q.ptr, s.ptr,
+                                       dev(codecs.encode_bf16_rne(gw)).ptr, g.ptr,
+                                       None))
+    want = 1.0 / (1.0 + np.exp(-(x.astype(np.float64) @ gw.astype(np.float64))))
+    np.testing.assert_allclose(host(g, np.float32, (T,)), want, rtol=2e-6, atol=1e-7)
+
+
+def test_weight_quantizers_bit_exact(L):
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((384, 640)) * 0.02).astype(np.float32)
+    w[0, :5] = [0.0, -0.0, 1e-9, -3e-3, 0.07]
+    wd = dev(w)
+    for pow2 in (0, 1):
+        q, s = empty(w.size), empty(3 * 5 * 4)
+        L.check(L.lib().sllm_quantize_weight_fp8(wd.ptr, 384, 640, pow2, q.ptr,
+                                                 s.ptr, None))
+        qr, sr = quant.quantize_weight_fp8_block(w, pow2=bool(pow2))
+        np.testing.assert_array_equal(host(s, np.float32, (3, 5)), sr)
+        np.testing.assert_array_equal(host(q, np.uint8, w.shape), qr)
+    p, e = empty(w.size // 2), empty(w.size // 32)
+    L.check(L.lib().sllm_quantize_weight_mxfp4(wd.ptr, 384, 640, p.ptr, e.ptr, None))
+    pr, er = quant.quantize_weight_mxfp4(w)
+    np.testing.assert_array_equal(host(e, np.uint8, er.shape), er)
+    np.testing.assert_array_equal(host(p, np.uint8, pr.shape), pr)
+
+
+# ---------------------------------------------------------------- router --
+
+def test_router_reference_case(L):
+    """tests/test_qwen4_kernels.py:73-79 restated (seed 33, (5,16), k=4)."""
+    from sllm_amd import q4
+    rng = np.random.default_rng(33)
+    logits = rng.standard_normal((5, 16)).astype(np.float32) * 2.0
+    w, ids = q4.moe_router(logits, 4)
+    w_ref, ids_ref = qm.moe_route(logits, 4)
+    np.testing.assert_array_equal(ids, ids_ref.astype(np.int32))
+    np.testing.assert_allclose(w, w_ref, rtol=1e-5, atol=1e-7)
+
+
+def test_router_ties_lowest_ids(L):
+    from sllm_amd import q4
+    w, ids = q4.moe_router(np.zeros((3, 6), np.float32), 3)
+    np.testing.assert_array_equal(ids, [[0, 1, 2]] * 3)
+    np.testing.assert_allclose(w, 1 / 3, rtol=1e-6)
+
+
+@pytest.mark.parametrize("T,E,k", [(4096, 512, 10), (64, 16, 4), (300, 2048, 16),
+                                   (17, 100, 7), (5, 64, 64)])
+def test_route_softmax_matches_oracle(L, T, E, k):
+    rng = np.random.default_rng(T + E)
+    logits = (rng.standard_normal((T, E)) * 0.9).astype(np.float32)
+    logits[0, :] = logits[0, 0]          # an all-tie row
+    logits[1, 5:9] = logits[1, 1]        # partial ties
+    w, ids = empty(T * k * 4), empty(T * k * 4)
+    L.check(L.lib().sllm_moe_route_softmax(dev(logits).ptr, w.ptr, ids.ptr, T, E,
+                                           k, np.float32(1e-20), None))
+    wr, ir = qm.moe_route(logits, k)
+    ih = host(ids, np.int32, (T, k))
+    p = qm.softmax_rows(logits)
+    ties = certified_route_ties(ih, ir.astype(np.int32), p)
+    assert ties <= 2
+    if ties == 0:
+        np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("G,kg,scoring", [(1, 1, "sigmoid"), (8, 4, "sigmoid"),
+                                          (4, 2, "softmax"), (8, 3, "sqrtsoftplus")])
+def test_route_grouped_matches_oracle(L, G, kg, scoring):
+    rng = np.random.default_rng(7 + G)
+    T, E, k = 2048, 256, 8
+    logits = (rng.standard_normal((T, E)) * 0.9).astype(np.float32)
+    logits[0] = 0.25                       # full tie row
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    w, ids = empty(T * k * 4), empty(T * k * 4)
+    sc = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}[scoring]
+    L.check(L.lib().sllm_moe_route_grouped(dev(logits).ptr, dev(bias).ptr, w.ptr,
+                                           ids.ptr, T, E, k, G, kg, sc,
+                                           np.float32(2.5), None))
+    wr, ir = dm.moe_route(logits, bias, k, scoring, 2.5, G, kg)
+    np.testing.assert_array_equal(host(ids, np.int32, (T, k)), ir.astype(np.int32))
+    np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=2e-6, atol=1e-7)
+
+
+def test_router_gemm_matches_fp64(L):
+    rng = np.random.default_rng(3)
+    for T, E, H in [(4096, 512, 2048), (64, 16, 1024), (33, 100, 256)]:
+        x = codecs.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+        wr = codecs.round_bf16((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+        out = empty(T * E * 4)
+        L.check(L.lib().sllm_moe_router_gemm(dev(codecs.encode_bf16_rne(x)).ptr,
+                                             dev(codecs.encode_bf16_rne(wr)).ptr,
+                                             out.ptr, T, E, H, None))
+        got = host(out, np.float32, (T, E))
+        want = x.astype(np.float64) @ wr.astype(np.float64).T
+        mag = np.abs(x.astype(np.float64)) @ np.abs(wr.astype(np.float64)).T
+        assert np.all(np.abs(got - want) <= 4 * 2.0 ** -24 * mag + 1e-30)
+
+
+# --------------------------------------------------------------- permute --
+
+def _run_permute(L, ids, E, bm):
+    from sllm_amd.runtime import sync
+    T, k = ids.shape
+    N = T * k
+    max_tiles = -(-N // bm) + min(E, N)
+    bufs = dict(counts=empty(E * 4), offsets=empty((E + 1) * 4),
+                sorted=empty(N * 4), inv=empty(N * 4),
+                tiles=empty(max_tiles * 8), nt=empty(4))
+    scr = empty(L.lib().sllm_moe_permute_scratch_bytes(N, E))
+    L.check(L.lib().sllm_moe_permute(dev(ids.astype(np.int32)).ptr, N, E, bm,
+                                     bufs["counts"].ptr, bufs["offsets"].ptr,
+                                     bufs["sorted"].ptr, bufs["inv"].ptr,
+                                     bufs["tiles"].ptr, bufs["nt"].ptr, max_tiles,
+                                     scr.ptr, None))
+    sync()
+    nt = int(host(bufs["nt"], np.int32, (1,))[0])
+    return dict(counts=host(bufs["counts"], np.int32, (E,)),
+                offsets=host(bufs["offsets"], np.int32, (E + 1,)),
+                sorted_idx=host(bufs["sorted"], np.int32, (N,)),
+                inv_pos=host(bufs["inv"], np.int32, (N,)),
+                tiles=host(bufs["tiles"], np.int32, (max_tiles, 2))[:nt])
+
+
+@pytest.mark.parametrize("T,E,k,skew", [(4096, 512, 10, False), (16384, 512, 10, True),
+                                        (1, 512, 10, False), (3, 7, 2, False),
+                                        (1000, 2048, 16, True)])
+def test_permute_bit_exact(L, T, E, k, skew):
+    rng = np.random.default_rng(T + E)
+    if skew:
+        # Zipf-like popularity with many empty experts
+        pop = 1.0 / np.arange(1, E + 1) ** 1.2
+        pop[E // 2:] = 0.0
+        pop /= pop.sum()
+        ids = np.stack([rng.choice(E, size=k, replace=False, p=pop) for _ in range(T)])
+    else:
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    got = _run_permute(L, ids, E, 128)
+    want = oracle_permute(ids, E)
+    for key in ("counts", "offsets", "sorted_idx", "inv_pos"):
+        np.testing.assert_array_equal(got[key], want[key], err_msg=key)
+    # tile table: every non-empty expert in order, ceil(count/128) tiles
+    exp_tiles = [(e, r) for e in range(E) for r in range(0, want["counts"][e], 128)]
+    np.testing.assert_array_equal(got["tiles"], np.array(exp_tiles, np.int32).reshape(-1, 2))

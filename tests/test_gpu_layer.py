@@ -1,0 +1,190 @@
+"""GPU parity of the fused MoE layers against the oracle.
+
+Routing (ids, per-expert counts) must be bit-exact at the logits boundary:
+the oracle routes the fp32 logits the device produced (the boundary the
+reference's sllm_q4_moe_router exposes); the router GEMM itself is checked
+separately against fp64 in test_gpu_kernels.py. Layer outputs must be
+within the bf16-noise tolerance: relative L2 <= 1e-2 (asserted tighter where
+the arithmetic allows) and a max-abs bound, both printed.
+"""
+import numpy as np
+import pytest
+
+from oracle import deepseek_moe as dm
+from oracle import qwen_moe as qm
+
+from tests._fixtures import (certified_route_ties, deepseek_layer,
+                             deepseek_mxfp4, deepseek_mxfp4_gpu, qwen_fp8,
+                             qwen_fp8_gpu, qwen_layer, rel_l2)
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib_loaded():
+    from sllm_amd import _lib
+    if not _lib.available():
+        pytest.fail(f"libsllm_moe.so not loadable: {_lib._lib_error}")
+
+
+def _check_routing(r, W_router_E, k, logits_fn=qm.moe_route):
+    w_ref, ids_ref = logits_fn(r["logits"], k)
+    p = qm.softmax_rows(r["logits"])
+    ties = certified_route_ties(r["ids"], ids_ref.astype(np.int32), p)
+    counts = np.bincount(r["ids"].ravel(), minlength=W_router_E)
+    np.testing.assert_array_equal(r["counts"], counts)
+    if ties == 0:
+        np.testing.assert_allclose(r["w"], w_ref, rtol=1e-5, atol=1e-7)
+    return ties
+
+
+def _report(name, got, want):
+    rel = rel_l2(got, want)
+    mabs = float(np.abs(got - want).max())
+    scale = float(np.abs(want).max())
+    print(f"{name}: rel-L2 {rel:.3e} max-abs {mabs:.3e} (max |ref| {scale:.3e})")
+    return rel, mabs, scale
+
+
+@pytest.mark.parametrize("T,E,k,shared", [(256, 8, 2, True), (130, 16, 4, False),
+                                          (512, 64, 6, True)])
+def test_qwen_prefill_small(T, E, k, shared):
+    x, W = qwen_fp8(seed=T, T=T, H=512, E=E, I=256, Is=256, shared=shared)
+    layer = qwen_layer(W, k)
+    y, r = layer.forward(x, mode="prefill", return_routing=True)
+    _check_routing(r, E, k)
+    want = qm.moe_layer_fp8(x, r["logits"], W, k)
+    rel, mabs, scale = _report("qwen prefill", y, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+
+
+def test_qwen_prefill_c2_shapes():
+    """C2 geometry (H 2048, I = Is = 512, top-10) with E = 128 experts at
+    T = 512 tokens (full E = 512 routing and permute are covered by
+    test_gpu_kernels.py at T = 4096 / 16384)."""
+    T, H, E, I, k = 512, 2048, 128, 512, 10
+    x, W = qwen_fp8_gpu(seed=2, T=T, H=H, E=E, I=I, Is=I)
+    layer = qwen_layer(W, k)
+    y, r = layer.forward(x, mode="prefill", return_routing=True)
+    _check_routing(r, E, k)
+    want = qm.moe_layer_fp8(x, r["logits"], W, k)
+    rel, mabs, scale = _report("qwen prefill C2 shapes", y, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+    info = qm.moe_layer_fp8_dequant(x, r["logits"], W, k)
+    print(f"  (information only) vs un-quantized-activation oracle: "
+          f"rel-L2 {rel_l2(y, info):.3e}")
+
+
+@pytest.mark.parametrize("B", [1, 8, 32, 64])
+def test_qwen_decode_c3_shapes(B):
+    """C3 decode batches on C2 geometry (fp32-activation GEMV path)."""
+    H, E, I, k = 2048, 512, 512, 10
+    x, W = qwen_fp8_gpu(seed=100 + B, T=B, H=H, E=E, I=I, Is=I)
+    layer = qwen_layer(W, k)
+    y, r = layer.forward(x, mode="decode", return_routing=True)
+    _check_routing(r, E, k)
+    want = qm.moe_layer_fp8_dequant(x, r["logits"], W, k)
+    rel, mabs, scale = _report(f"qwen decode B={B}", y, want)
+    assert rel < 1e-4
+
+
+def test_qwen_logits_given_and_auto_mode():
+    x, W = qwen_fp8(seed=5, T=96, H=512, E=8, I=256, Is=256)
+    layer = qwen_layer(W, 3)
+    logits = (x @ W.router_w.T).astype(np.float32)
+    y, r = layer.forward(x, logits=logits, mode="auto", return_routing=True)
+    np.testing.assert_array_equal(r["logits"], logits)
+    want = qm.moe_layer_fp8(x, logits, W, 3)      # T=96 > 64: prefill
+    assert rel_l2(y, want) < 3e-3
+    yd = layer.forward(x[:10], logits=logits[:10], mode="auto")  # decode
+    assert rel_l2(yd, qm.moe_layer_fp8_dequant(x[:10], logits[:10], W, 3)) < 1e-4
+
+
+def test_c1_bf16_literal_oracle():
+    """C1: 64 tokens, H 1024, E 16, top-4, I 512, no shared expert, bf16
+    weights, seed 0 -- against the reference's literal per-token loop."""
+    from oracle.codecs import round_bf16 as bf
+    from sllm_amd.moe import moe_block_forward
+    rng = np.random.default_rng(0)
+    T, H, E, k, I = 64, 1024, 16, 4, 512
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    eg = bf((rng.standard_normal((E, I, H)) * 0.02).astype(np.float32))
+    eu = bf((rng.standard_normal((E, I, H)) * 0.02).astype(np.float32))
+    ed = bf((rng.standard_normal((E, H, I)) * 0.02).astype(np.float32))
+    got = moe_block_forward(x, rw, eg, eu, ed, None, None, None, None, k)
+    want = qm.moe_block_forward(x, rw, eg, eu, ed, None, None, None, None, k)
+    rel, mabs, scale = _report("C1 bf16", got, want)
+    assert rel < 1e-4
+
+
+def test_qwen_skewed_with_empty_experts():
+    """C5-style skew: biased logits concentrate load, many experts empty."""
+    T, H, E, I, k = 2048, 512, 64, 256, 6
+    x, W = qwen_fp8(seed=9, T=T, H=H, E=E, I=I, Is=256)
+    rng = np.random.default_rng(9)
+    ranks = rng.permutation(E) + 1
+    bias = (-3.0 * np.log(ranks)).astype(np.float32)
+    bias[ranks > 40] = -60.0          # these experts never win
+    logits = (x @ W.router_w.T + bias).astype(np.float32)
+    layer = qwen_layer(W, k)
+    y, r = layer.forward(x, logits=logits, mode="prefill", return_routing=True)
+    assert (r["counts"] == 0).sum() >= 20 and r["counts"].max() > 128
+    _check_routing(r, E, k)
+    want = qm.moe_layer_fp8(x, logits, W, k)
+    rel, mabs, scale = _report("qwen skewed", y, want)
+    assert rel < 3e-3
+
+
+@pytest.mark.parametrize("T,G,kg,L", [(200, 4, 2, 10.0), (256, 1, 1, 0.0)])
+def test_deepseek_prefill_small(T, G, kg, L):
+    x, W = deepseek_mxfp4(seed=T, T=T, H=512, E=16, I=256, Is=256)
+    route = dict(n_group=G, topk_group=kg, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=L)
+    layer = deepseek_layer(W, 4, **route)
+    y, r = layer.forward(x, mode="prefill", return_routing=True)
+    w_ref, ids_ref = dm.moe_route(r["logits"], W.bias, 4, "sigmoid", 2.5, G, kg)
+    np.testing.assert_array_equal(r["ids"], ids_ref.astype(np.int32))
+    np.testing.assert_allclose(r["w"], w_ref, rtol=2e-6)
+    want = dm.moe_layer_mxfp4(x, r["logits"], W, 4, L, "sigmoid", 2.5, G, kg)
+    rel, mabs, scale = _report("deepseek prefill", y, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+
+
+def test_deepseek_prefill_c4_shapes():
+    """C4 geometry (H 7168, I = Is = 2048, top-8, 8 groups keep 4) with
+    E = 32 experts and T = 256 tokens so the CPU oracle stays fast."""
+    T, H, E, I, k = 256, 7168, 32, 2048, 8
+    x, W = deepseek_mxfp4_gpu(seed=4, T=T, H=H, E=E, I=I, Is=I)
+    route = dict(n_group=8, topk_group=4, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=10.0)
+    layer = deepseek_layer(W, k, **route)
+    y, r = layer.forward(x, mode="prefill", return_routing=True)
+    _, ids_ref = dm.moe_route(r["logits"], W.bias, k, "sigmoid", 2.5, 8, 4)
+    np.testing.assert_array_equal(r["ids"], ids_ref.astype(np.int32))
+    want = dm.moe_layer_mxfp4(x, r["logits"], W, k, 10.0, "sigmoid", 2.5, 8, 4)
+    rel, mabs, scale = _report("deepseek prefill C4 shapes", y, want)
+    assert rel < 3e-3
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_deepseek_decode(B):
+    x, W = deepseek_mxfp4(seed=50 + B, T=B, H=1024, E=16, I=512, Is=512)
+    route = dict(n_group=4, topk_group=2, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=10.0)
+    layer = deepseek_layer(W, 4, **route)
+    y, r = layer.forward(x, mode="decode", return_routing=True)
+    from oracle.codecs import dequant_fp4_block, dequant_fp8_block
+
+    def ex(e):
+        return (dequant_fp4_block(W.w1_p[e], W.w1_s[e]),
+                dequant_fp4_block(W.w3_p[e], W.w3_s[e]),
+                dequant_fp4_block(W.w2_p[e], W.w2_s[e]))
+    sh = (dequant_fp8_block(W.s1_q, W.s1_s), dequant_fp8_block(W.s3_q, W.s3_s),
+          dequant_fp8_block(W.s2_q, W.s2_s))
+    want = dm.moe_block_forward(x, r["logits"], W.bias, ex, sh, 4, 10.0,
+                                "sigmoid", 2.5, 4, 2)
+    rel, mabs, scale = _report(f"deepseek decode B={B}", y, want)
+    assert rel < 1e-4
