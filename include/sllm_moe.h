@@ -59,6 +59,23 @@ long sllm_mem_free_bytes(void);
 int sllm_sync(void);
 
 /* ---------------------------------------------------------------------- */
+/* Measurement and synthetic-data helpers (new; no reference counterpart:  */
+/* the reference times with wall clocks only, bench/gpu_decode_timing.py)  */
+/* ---------------------------------------------------------------------- */
+/* hipEvent wrappers: time work on the stream the layer is launched on. */
+void* sllm_event_new(void);
+int sllm_event_free(void* ev);
+int sllm_event_record(void* ev, void* stream);
+int sllm_event_sync(void* ev);
+/* milliseconds between two recorded events, -1 on error */
+float sllm_event_elapsed_ms(void* start, void* stop);
+/* stream-ordered byte fill (cache flushing between timed decode calls) */
+int sllm_memset(void* dst, int value, long nbytes, void* stream);
+/* dst[i] ~ N(0, std^2), a pure function of (seed, i) */
+int sllm_fill_normal(float* dst, long n, unsigned long long seed, float stdv,
+                     void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Reference MoE kernel surface (ref kernels/cuda/qwen4.cu)                */
 /* ---------------------------------------------------------------------- */
 /* softmax -> top-k (ties to the lower id) -> renorm p/(sum p + 1e-20).

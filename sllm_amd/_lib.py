@@ -73,6 +73,13 @@ SIGNATURES = {
     "sllm_buf_d2h_raw": (c_int, [P, P, c_long]),
     "sllm_mem_free_bytes": (c_long, []),
     "sllm_sync": (c_int, []),
+    "sllm_event_new": (c_void_p, []),
+    "sllm_event_free": (c_int, [P]),
+    "sllm_event_record": (c_int, [P, P]),
+    "sllm_event_sync": (c_int, [P]),
+    "sllm_event_elapsed_ms": (c_float, [P, P]),
+    "sllm_memset": (c_int, [P, c_int, c_long, P]),
+    "sllm_fill_normal": (c_int, [P, c_long, ctypes.c_ulonglong, c_float, P]),
     "sllm_q4_moe_router": (c_int, [F, F, I, c_int, c_int, c_int]),
     "sllm_q4_moe_router_dev": (c_int, [P, P, P, c_int, c_int, c_int]),
     "sllm_q4_swiglu": (c_int, [F, F, F, c_long]),

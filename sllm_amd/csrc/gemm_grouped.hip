@@ -41,10 +41,17 @@
 // workgroups exit at once. Consecutive column slabs of one row tile are
 // mapped onto one XCD so the gathered A rows are reused from its L2.
 //
-// MFMA lane layout used here: lane l supplies row (l % 16) of A / column
-// (l % 16) of B with the 32 K values [32 (l / 16), +32) of the 128-wide K
-// step, and the e8m0 scale of exactly those 32 values; the 16x16 result
-// holds row 4 (l / 16) + v, column l % 16 in element v.
+// MFMA lane layout (v_mfma_*_16x16x128_f8f6f4, measured on gfx950 with
+// one-hot operands): lane l supplies row (l % 16) of A and column (l % 16)
+// of B. An e4m3 operand holds, in lane group g = l / 16, the K values
+// [16 g, 16 g + 16) in bytes 0-15 and [64 + 16 g, 64 + 16 g + 16) in bytes
+// 16-31; an e2m1 operand holds the contiguous K values [32 g, 32 g + 32)
+// (low nibble first); lane group b supplies the e8m0 scale of the K block
+// [32 b, 32 b + 32). fp8 x fp8 products only need both operands loaded the
+// same way (their scales are uniform over the 128-wide step), so they load
+// 32 contiguous bytes; fp8 x fp4 loads the A operand in the split order so
+// that it pairs with the contiguous fp4 B operand and its per-32 scales.
+// The 16x16 fp32 result holds row 4 (l / 16) + v, column l % 16 in element v.
 #include "launch.h"
 
 namespace sllm {
@@ -134,11 +141,16 @@ __device__ __forceinline__ void store_a(uint8_t* lds, int row, int half,
   for (int i = 0; i < 4; ++i) p[i] = f.v[i];
 }
 
+// A operand for row subtile mi from the LDS tile: 32 contiguous bytes at
+// 32 g (fp8 x fp8), or 16 bytes at 16 g and 16 at 64 + 16 g (fp8 x fp4).
+template <int BF>
 __device__ __forceinline__ v8i lds_a_frag(const uint8_t* lds, int mi,
                                           int lane) {
-  const uint8_t* p =
-      lds + (mi * 16 + (lane & 15)) * G_LDS_STRIDE + (lane >> 4) * 32;
-  const uint4 lo = *(const uint4*)p, hi = *(const uint4*)(p + 16);
+  const uint8_t* row = lds + (mi * 16 + (lane & 15)) * G_LDS_STRIDE;
+  const int g = lane >> 4;
+  const uint8_t* p0 = BF == BF_FP4 ? row + g * 16 : row + g * 32;
+  const uint8_t* p1 = BF == BF_FP4 ? row + 64 + g * 16 : row + g * 32 + 16;
+  const uint4 lo = *(const uint4*)p0, hi = *(const uint4*)p1;
   return (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
@@ -265,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void moe_gemm1_kernel(
 #pragma unroll
     for (int mi = 0; mi < 8; ++mi) {
       if (mi < nmi) {
-        const v8i a = lds_a_frag(a_lds, mi, lane);
+        const v8i a = lds_a_frag<BF>(a_lds, mi, lane);
         if constexpr (BF == BF_FP8_F32S) {
           const float4 sav =
               *(const float4*)(sa_lds + mi * 16 + lg * 4);
@@ -441,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void moe_gemm2_kernel(
 #pragma unroll
     for (int mi = 0; mi < 8; ++mi) {
       if (mi < nmi) {
-        const v8i a = lds_a_frag(a_lds, mi, lane);
+        const v8i a = lds_a_frag<BF>(a_lds, mi, lane);
         if constexpr (BF == BF_FP8_F32S) {
           const float4 sav = *(const float4*)(sa_lds + mi * 16 + lg * 4);
           const float c[4] = {sav.x * sbf, sav.y * sbf, sav.z * sbf,

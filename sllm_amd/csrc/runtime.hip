@@ -23,6 +23,32 @@ void set_error(const char* fmt, ...) {
 
 const char* last_error() { return g_err; }
 
+// Counter-based normal generator for synthetic data: value i is a pure
+// function of (seed, i) -- splitmix64 of the pair index gives two uniforms,
+// Box-Muller gives two normals -- so any launch shape yields the same array.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__global__ void fill_normal_kernel(float* __restrict__ dst, long n,
+                                   uint64_t seed, float stdv) {
+  const long pair = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long i = 2 * pair;
+  if (i >= n) return;
+  const uint64_t r = splitmix64(seed * 0xD1B54A32D192ED03ull + (uint64_t)pair);
+  // uniforms in (0, 1] and [0, 1)
+  const float u1 = ((float)(r >> 40) + 1.0f) * (1.0f / 16777216.0f);
+  const float u2 = (float)((r >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+  const float rad = sqrtf(-2.0f * logf(u1)) * stdv;
+  float sv, cv;
+  sincosf(6.28318530717958647692f * u2, &sv, &cv);
+  dst[i] = rad * cv;
+  if (i + 1 < n) dst[i + 1] = rad * sv;
+}
+
 }  // namespace sllm
 
 using namespace sllm;
@@ -60,6 +86,9 @@ void* sllm_buf_new(long nbytes) {
 
 int sllm_buf_free(void* p) {
   if (!p) return 0;
+  // work already queued may still read the buffer: drain the device first
+  // (the reference's cudaFree gives the same guarantee implicitly)
+  SLLM_HIP(hipDeviceSynchronize());
   SLLM_HIP(hipFree(p));
   return 0;
 }
@@ -99,6 +128,61 @@ long sllm_mem_free_bytes(void) {
 
 int sllm_sync(void) {
   SLLM_HIP(hipDeviceSynchronize());
+  return 0;
+}
+
+void* sllm_event_new(void) {
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) {
+    set_error("hipEventCreate: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  return (void*)ev;
+}
+
+int sllm_event_free(void* ev) {
+  if (!ev) return 0;
+  SLLM_HIP(hipEventDestroy((hipEvent_t)ev));
+  return 0;
+}
+
+int sllm_event_record(void* ev, void* stream) {
+  SLLM_REQUIRE(ev, "sllm_event_record: null event");
+  SLLM_HIP(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+  return 0;
+}
+
+int sllm_event_sync(void* ev) {
+  SLLM_REQUIRE(ev, "sllm_event_sync: null event");
+  SLLM_HIP(hipEventSynchronize((hipEvent_t)ev));
+  return 0;
+}
+
+float sllm_event_elapsed_ms(void* start, void* stop) {
+  float ms = -1.f;
+  hipError_t e = hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop);
+  if (e != hipSuccess) {
+    set_error("hipEventElapsedTime: %s", hipGetErrorString(e));
+    return -1.f;
+  }
+  return ms;
+}
+
+int sllm_memset(void* dst, int value, long nbytes, void* stream) {
+  SLLM_REQUIRE(dst && nbytes >= 0, "sllm_memset: bad args");
+  SLLM_HIP(hipMemsetAsync(dst, value, (size_t)nbytes, (hipStream_t)stream));
+  return 0;
+}
+
+int sllm_fill_normal(float* dst, long n, unsigned long long seed, float stdv,
+                     void* stream) {
+  SLLM_REQUIRE(dst && n >= 0, "sllm_fill_normal: bad args");
+  if (n == 0) return 0;
+  const long pairs = (n + 1) / 2;
+  fill_normal_kernel<<<(unsigned)((pairs + 255) / 256), 256, 0,
+                       (hipStream_t)stream>>>(dst, n, (uint64_t)seed, stdv);
+  SLLM_LAUNCHED();
   return 0;
 }
 

@@ -173,6 +173,48 @@ def alloc_n(nbytes: int) -> DeviceBuffer:
     return DeviceBuffer(int(nbytes))
 
 
+class Event:
+    """hipEvent on the library's side of the process (torch must not touch
+    the GPU in a process that uses this library: it bundles its own HIP
+    runtime)."""
+
+    def __init__(self):
+        self._ev = _lib.lib().sllm_event_new()
+        if not self._ev:
+            raise RuntimeError("sllm_event_new failed: " + _lib.last_error())
+
+    def record(self, stream=None) -> None:
+        _lib.check(_lib.lib().sllm_event_record(c_void_p(self._ev),
+                                                stream_handle(stream)), "event")
+
+    def synchronize(self) -> None:
+        _lib.check(_lib.lib().sllm_event_sync(c_void_p(self._ev)), "event")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _lib.lib().sllm_event_elapsed_ms(c_void_p(self._ev), c_void_p(end._ev))
+        if ms < 0:
+            raise RuntimeError("hipEventElapsedTime failed: " + _lib.last_error())
+        return float(ms)
+
+    def __del__(self):
+        try:
+            _lib.lib().sllm_event_free(c_void_p(self._ev))
+        except Exception:
+            pass
+
+
+def fill_normal(buf, n: int, seed: int, std: float = 1.0, stream=None) -> None:
+    """buf[:n] (fp32) ~ N(0, std^2), deterministic in (seed, index)."""
+    _lib.check(_lib.lib().sllm_fill_normal(ptr(buf), int(n), int(seed) & (2**64 - 1),
+                                           float(std), stream_handle(stream)),
+               "sllm_fill_normal")
+
+
+def memset(buf, value: int, nbytes: int, stream=None) -> None:
+    _lib.check(_lib.lib().sllm_memset(ptr(buf), int(value), int(nbytes),
+                                      stream_handle(stream)), "sllm_memset")
+
+
 def gemm_ex(a, w, c, m: int, n: int, k: int, atype: int = T_F32) -> None:
     """c (m,n) fp32 = a (m,k) . w (n,k)^T with a, w in dtype `atype`
     (ref kernels/_sllm_cuda.py:503-506)."""

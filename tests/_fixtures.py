@@ -41,60 +41,65 @@ def qwen_fp8(seed=0, T=64, H=512, E=8, I=256, Is=256, shared=True,
     return x, W
 
 
-def _gpu_normal(gen, rows, cols, std):
-    import torch
-    return torch.randn((rows, cols), generator=gen, device="cuda",
-                       dtype=torch.float32) * std
+class _DevRng:
+    """Seeded stream of N(0, std^2) device arrays from sllm_fill_normal
+    (torch must not touch the GPU here: it bundles another HIP runtime)."""
+
+    def __init__(self, seed):
+        self.seed = int(seed) * 1000003
+        self.k = 0
+
+    def normal(self, n, std):
+        from sllm_amd.runtime import DeviceBuffer, fill_normal
+        buf = DeviceBuffer(int(n) * 4)
+        fill_normal(buf, n, self.seed + self.k, std)
+        self.k += 1
+        return buf
 
 
-def _gpu_fp8(gen, E, N, K, pow2=False):
+def _gpu_fp8(rng, E, N, K, pow2=False):
     """E stacked (N, K) weights ~N(0, 0.02) quantized on the device with
     sllm_quantize_weight_fp8 (bit-exact with oracle.quant, see
     test_gpu_kernels.py) -> host (q (E,N,K) uint8, s (E,N/128,K/128))."""
-    import torch
     from sllm_amd import _lib
+    from sllm_amd.runtime import DeviceBuffer
     assert N % 128 == 0
-    w = _gpu_normal(gen, E * N, K, 0.02)
-    q = torch.empty((E * N, K), dtype=torch.uint8, device="cuda")
-    sc = torch.empty((E * N // 128, -(-K // 128)), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    _lib.check(_lib.lib().sllm_quantize_weight_fp8(w.data_ptr(), E * N, K, int(pow2),
-                                                   q.data_ptr(), sc.data_ptr(), None))
-    torch.cuda.synchronize()
-    del w
-    return (q.cpu().numpy().reshape(E, N, K),
-            sc.cpu().numpy().reshape(E, N // 128, -(-K // 128)))
+    kb = -(-K // 128)
+    w = rng.normal(E * N * K, 0.02)
+    q = DeviceBuffer(E * N * K)
+    sc = DeviceBuffer(E * N // 128 * kb * 4)
+    _lib.check(_lib.lib().sllm_quantize_weight_fp8(w.ptr, E * N, K, int(pow2),
+                                                   q.ptr, sc.ptr, None))
+    w.free()
+    return (q.copy_host_raw(np.uint8, (E, N, K)),
+            sc.copy_host_raw(np.float32, (E, N // 128, kb)))
 
 
-def _gpu_fp4(gen, E, N, K):
-    import torch
+def _gpu_fp4(rng, E, N, K):
     from sllm_amd import _lib
-    w = _gpu_normal(gen, E * N, K, 0.02)
-    p = torch.empty((E * N, K // 2), dtype=torch.uint8, device="cuda")
-    sc = torch.empty((E * N, K // 32), dtype=torch.uint8, device="cuda")
-    torch.cuda.synchronize()
-    _lib.check(_lib.lib().sllm_quantize_weight_mxfp4(w.data_ptr(), E * N, K,
-                                                     p.data_ptr(), sc.data_ptr(), None))
-    torch.cuda.synchronize()
-    del w
-    return (p.cpu().numpy().reshape(E, N, K // 2),
-            sc.cpu().numpy().reshape(E, N, K // 32))
+    from sllm_amd.runtime import DeviceBuffer
+    w = rng.normal(E * N * K, 0.02)
+    p = DeviceBuffer(E * N * K // 2)
+    sc = DeviceBuffer(E * N * K // 32)
+    _lib.check(_lib.lib().sllm_quantize_weight_mxfp4(w.ptr, E * N, K, p.ptr,
+                                                     sc.ptr, None))
+    w.free()
+    return (p.copy_host_raw(np.uint8, (E, N, K // 2)),
+            sc.copy_host_raw(np.uint8, (E, N, K // 32)))
 
 
 def qwen_fp8_gpu(seed=0, T=64, H=2048, E=128, I=512, Is=512, shared=True):
-    """qwen_fp8 with the expert weights generated and quantized on the GPU
-    (seeded torch generator): the numpy route is minutes at C2 geometry."""
-    import torch
+    """qwen_fp8 with the expert weights generated (sllm_fill_normal) and
+    quantized on the GPU: the numpy route takes minutes at C2 geometry."""
     rng = np.random.default_rng(seed)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
+    dr = _DevRng(seed)
     x = bf(rng.standard_normal((T, H)).astype(np.float32))
     rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
-    g, u, d = _gpu_fp8(gen, E, I, H), _gpu_fp8(gen, E, I, H), _gpu_fp8(gen, E, H, I)
+    g, u, d = _gpu_fp8(dr, E, I, H), _gpu_fp8(dr, E, I, H), _gpu_fp8(dr, E, H, I)
     W = qm.QwenFp8Weights(router_w=rw, wg_q=g[0], wg_s=g[1], wu_q=u[0],
                           wu_s=u[1], wd_q=d[0], wd_s=d[1])
     if shared:
-        sg, su, sd = _gpu_fp8(gen, 1, Is, H), _gpu_fp8(gen, 1, Is, H), _gpu_fp8(gen, 1, H, Is)
+        sg, su, sd = _gpu_fp8(dr, 1, Is, H), _gpu_fp8(dr, 1, Is, H), _gpu_fp8(dr, 1, H, Is)
         W.sg_q, W.sg_s = sg[0][0], sg[1][0]
         W.su_q, W.su_s = su[0][0], su[1][0]
         W.sd_q, W.sd_s = sd[0][0], sd[1][0]
@@ -103,19 +108,17 @@ def qwen_fp8_gpu(seed=0, T=64, H=2048, E=128, I=512, Is=512, shared=True):
 
 
 def deepseek_mxfp4_gpu(seed=0, T=64, H=7168, E=32, I=2048, Is=2048, shared=True):
-    import torch
     rng = np.random.default_rng(seed)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
+    dr = _DevRng(seed)
     x = bf(rng.standard_normal((T, H)).astype(np.float32))
     rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
     bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
-    w1, w3, w2 = _gpu_fp4(gen, E, I, H), _gpu_fp4(gen, E, I, H), _gpu_fp4(gen, E, H, I)
+    w1, w3, w2 = _gpu_fp4(dr, E, I, H), _gpu_fp4(dr, E, I, H), _gpu_fp4(dr, E, H, I)
     W = dm.DeepseekMxfp4Weights(router_w=rw, bias=bias, w1_p=w1[0], w1_s=w1[1],
                                 w3_p=w3[0], w3_s=w3[1], w2_p=w2[0], w2_s=w2[1])
     if shared:
-        s1, s3, s2 = (_gpu_fp8(gen, 1, Is, H, True), _gpu_fp8(gen, 1, Is, H, True),
-                      _gpu_fp8(gen, 1, H, Is, True))
+        s1, s3, s2 = (_gpu_fp8(dr, 1, Is, H, True), _gpu_fp8(dr, 1, Is, H, True),
+                      _gpu_fp8(dr, 1, H, Is, True))
         W.s1_q, W.s1_s = s1[0][0], s1[1][0]
         W.s3_q, W.s3_s = s3[0][0], s3[1][0]
         W.s2_q, W.s2_s = s2[0][0], s2[1][0]

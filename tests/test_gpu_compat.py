@@ -46,14 +46,16 @@ def test_dev_variants_match_host():
     logits = rng.standard_normal((40, 128)).astype(np.float32)
     w_h, ids_h = q4.moe_router(logits, 8)
     w_d, i_d = DeviceBuffer(40 * 8 * 4), DeviceBuffer(40 * 8 * 4)
-    q4.moe_router_dev(to_device(logits), w_d, i_d, 40, 128, 8)
+    lg_d = to_device(logits)
+    q4.moe_router_dev(lg_d, w_d, i_d, 40, 128, 8)
     sync()
     np.testing.assert_array_equal(w_d.copy_host().reshape(40, 8), w_h)
     np.testing.assert_array_equal(i_d.copy_host_raw(np.int32, (40, 8)), ids_h)
     g = rng.standard_normal(1000).astype(np.float32)
     u = rng.standard_normal(1000).astype(np.float32)
     o = DeviceBuffer(4000)
-    q4.swiglu_dev(to_device(g), to_device(u), o, 1000)
+    g_d, u_d = to_device(g), to_device(u)
+    q4.swiglu_dev(g_d, u_d, o, 1000)
     sync()
     np.testing.assert_array_equal(o.copy_host(), q4.swiglu(g, u))
 
@@ -119,10 +121,12 @@ def test_gemm_ex_f32_and_bf16():
     a = rng.standard_normal((m, k)).astype(np.float32)
     w = rng.standard_normal((n, k)).astype(np.float32)
     c = DeviceBuffer(m * n * 4)
-    gemm_ex(to_device(a), to_device(w), c, m, n, k, T_F32)
+    a_d, w_d = to_device(a), to_device(w)
+    gemm_ex(a_d, w_d, c, m, n, k, T_F32)
     sync()
     np.testing.assert_allclose(c.copy_host().reshape(m, n), a @ w.T, rtol=1e-4, atol=1e-4)
-    gemm_ex(to_device_raw(to_bf16(a)), to_device_raw(to_bf16(w)), c, m, n, k, T_BF16)
+    ab_d, wb_d = to_device_raw(to_bf16(a)), to_device_raw(to_bf16(w))
+    gemm_ex(ab_d, wb_d, c, m, n, k, T_BF16)
     sync()
     ab, wb = codecs.round_bf16(a), codecs.round_bf16(w)
     np.testing.assert_allclose(c.copy_host().reshape(m, n), ab @ wb.T, rtol=1e-4, atol=1e-4)

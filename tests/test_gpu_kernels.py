@@ -23,14 +23,32 @@ def L():
     return _lib
 
 
+# Device buffers made by dev()/empty() stay referenced until the test ends:
+# an inline temporary (dev(a).ptr) would otherwise be freed by Python before
+# the kernel that reads it is launched.
+_KEEP = []
+
+
+@pytest.fixture(autouse=True)
+def _pin_buffers():
+    yield
+    from sllm_amd.runtime import sync
+    sync()
+    _KEEP.clear()
+
+
 def dev(a):
     from sllm_amd.runtime import to_device_raw
-    return to_device_raw(np.ascontiguousarray(a))
+    b = to_device_raw(np.ascontiguousarray(a))
+    _KEEP.append(b)
+    return b
 
 
 def empty(nbytes):
     from sllm_amd.runtime import DeviceBuffer
-    return DeviceBuffer(max(int(nbytes), 4))
+    b = DeviceBuffer(max(int(nbytes), 4))
+    _KEEP.append(b)
+    return b
 
 
 def host(buf, dtype, shape):
@@ -229,3 +247,15 @@ def test_permute_bit_exact(L, T, E, k, skew):
     # tile table: every non-empty expert in order, ceil(count/128) tiles
     exp_tiles = [(e, r) for e in range(E) for r in range(0, want["counts"][e], 128)]
     np.testing.assert_array_equal(got["tiles"], np.array(exp_tiles, np.int32).reshape(-1, 2))
+
+
+def test_fill_normal_deterministic_and_normal(L):
+    from sllm_amd.runtime import fill_normal
+    n = 1 << 20
+    a, b = empty(n * 4), empty(n * 4)
+    fill_normal(a, n, 7, 2.0)
+    fill_normal(b, n, 7, 2.0)
+    x = host(a, np.float32, (n,))
+    np.testing.assert_array_equal(x, host(b, np.float32, (n,)))
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 2.0) < 0.01
+    assert abs((np.abs(x) < 2.0).mean() - 0.6827) < 0.003
