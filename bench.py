@@ -1,0 +1,377 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE layer on the BASELINE configs.
+
+One "step" is one full Qwen-style FP8 MoE layer (router GEMM, softmax top-10,
+permute, activation quant, grouped gate/up + SwiGLU + re-quant, grouped down,
+shared expert with sigmoid gate, combine) over the C2 workload: 4096 tokens,
+hidden 2048, 512 routed experts, top-10, intermediate 512, one shared expert
+(intermediate 512). Inputs and weights are resident in HBM before the timed
+region; weights are synthetic N(0, 0.02) quantized to e4m3 with fp32 128x128
+block scales, activations bf16 N(0, 1).
+
+Timing: HIP events on the stream the layer is launched on, K steps after W
+warm-up steps, bracketed by device synchronisation. Then, outside the headline
+number: a per-stage event breakdown (the roofline of the dominant kernel),
+the C3 decode batches (B = 1, 8, 32, 64; per-call events, L2/MALL flushed with
+a 512 MiB fill between calls), and the CPU baseline (the numpy restatement of
+the quantized layer on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("MoE layer tokens/s @4096-tok prefill; decode-layer µs @32 tok; "
+          "% roofline")
+PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5033.0        # MI355X dense FP8 MFMA (no sparsity)
+
+C2 = dict(T=4096, H=2048, E=512, I=512, Is=512, k=10)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# synthetic C2 layer on the device
+# --------------------------------------------------------------------------
+class DeviceLayer:
+    def __init__(self, cfg, seed=0):
+        import numpy as np
+        from sllm_amd import _lib
+        from sllm_amd.runtime import (DeviceBuffer, fill_normal, sync, to_bf16,
+                                      to_device_raw)
+        self.cfg = cfg
+        T, H, E, I, Is = cfg["T"], cfg["H"], cfg["E"], cfg["I"], cfg["Is"]
+        L = _lib.lib()
+        self.w = {}
+        tmp = DeviceBuffer(max(E * I * H, Is * H) * 4)
+        sub = [0]
+
+        def q8(name, rows, cols):
+            n = rows * cols
+            fill_normal(tmp, n, seed * 1000 + sub[0], 0.02)
+            sub[0] += 1
+            q = DeviceBuffer(n)
+            s = DeviceBuffer((rows // 128) * (cols // 128) * 4)
+            _lib.check(L.sllm_quantize_weight_fp8(tmp.ptr, rows, cols, 0, q.ptr,
+                                                  s.ptr, None), "quantize")
+            self.w[name], self.w[name + "_s"] = q, s
+
+        q8("wg", E * I, H)
+        q8("wu", E * I, H)
+        q8("wd", E * H, I)
+        q8("sg", Is, H)
+        q8("su", Is, H)
+        q8("sd", H, Is)
+        sync()
+        tmp.free()
+        rng = np.random.default_rng(seed)
+        self.router_w_host = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        self.w["router_w"] = to_device_raw(to_bf16(self.router_w_host))
+        self.sgl_host = (rng.standard_normal(H) * 0.02).astype(np.float32)
+        self.w["sgl"] = to_device_raw(to_bf16(self.sgl_host))
+        self.rng = rng
+
+    def host_expert(self, name, e, rows, cols):
+        """Host copy (q, s) of expert e of stacked weight `name`."""
+        import numpy as np
+        from sllm_amd import _lib
+        q = np.empty((rows, cols), np.uint8)
+        s = np.empty((rows // 128, cols // 128), np.float32)
+        L = _lib.lib()
+        qb, sb = self.w[name], self.w[name + "_s"]
+        _lib.check(L.sllm_buf_d2h_raw(q.ctypes.data, qb.ptr + e * rows * cols, q.nbytes))
+        _lib.check(L.sllm_buf_d2h_raw(s.ctypes.data, sb.ptr + e * s.nbytes, s.nbytes))
+        return q, s
+
+
+def layer_call(layer, x, out, ws, T, mode, debug=None, stage_events=None):
+    from sllm_amd.moe import qwen_forward_dev
+    c = layer.cfg
+    qwen_forward_dev(x, out, layer.w, T=T, H=c["H"], E=c["E"], I=c["I"],
+                     Is=c["Is"], topk=c["k"], mode=mode, out_f32=False,
+                     workspace=ws, debug=debug, stage_events=stage_events)
+
+
+# --------------------------------------------------------------------------
+# algorithmic work (formulas as in SURVEY section 8(d))
+# --------------------------------------------------------------------------
+def prefill_work(c, touched):
+    T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
+    flops = 6 * H * I * T * k + 6 * H * Is * T
+    wbytes = touched * 3 * H * I + touched * 3 * (H // 128) * (I // 128) * 4
+    bytes_ = (wbytes + 3 * H * Is + E * H * 2 + H * 2 + 2 * T * H * 2)
+    return flops, bytes_
+
+
+def gemm1_bytes(c, touched):
+    """Algorithmic HBM bytes of one routed gate/up launch: each touched
+    expert's gate and up weights (e4m3) and scales once, the e4m3
+    activations and their scales once, the e4m3 h rows and scales out."""
+    T, H, I, k = c["T"], c["H"], c["I"], c["k"]
+    N = T * k
+    return (touched * (2 * I * H + 2 * (I // 128) * (H // 128) * 4)
+            + T * H + T * (H // 128) * 4 + N * I + N * (I // 128) * 4)
+
+
+def gemm2_bytes(c, touched):
+    T, H, I, k = c["T"], c["H"], c["I"], c["k"]
+    N = T * k
+    return (touched * (H * I + (H // 128) * (I // 128) * 4)
+            + N * I + N * (I // 128) * 4 + N * H * 2)
+
+
+def decode_bytes(c, B, touched):
+    H, E, I, Is = c["H"], c["E"], c["I"], c["Is"]
+    return (touched * (3 * H * I + 3 * (H // 128) * (I // 128) * 4)
+            + 3 * H * Is + E * H * 2 + H * 2 + 2 * B * H * 2)
+
+
+# --------------------------------------------------------------------------
+# CPU baseline: numpy restatement of the quantized layer, bounded sample
+# --------------------------------------------------------------------------
+def cpu_baseline(layer, x_host, ids, wts, sample_experts=64):
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import codecs, quant
+    c = layer.cfg
+    T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
+    cores = len(os.sched_getaffinity(0))
+    # weights dequantized to fp32 outside the timed region
+    deq = {}
+    for e in range(sample_experts):
+        deq[e] = tuple(codecs.dequant_fp8_block(*layer.host_expert(n, e, r, cc))
+                       for n, r, cc in (("wg", I, H), ("wu", I, H), ("wd", H, I)))
+    sh = tuple(codecs.dequant_fp8_block(*layer.host_expert(n, 0, r, cc))
+               for n, r, cc in (("sg", Is, H), ("su", Is, H), ("sd", H, Is)))
+    rw = codecs.round_bf16(layer.router_w_host)
+    sgl = codecs.round_bf16(layer.sgl_host)
+
+    def silu(v):
+        return v / (1.0 + np.exp(-v))
+
+    def expert(xr, g, u, d):
+        h = (silu(xr @ g.T) * (xr @ u.T)).astype(np.float32)
+        return quant.act_dequant(*quant.act_quant(h)) @ d.T
+
+    def run():
+        t0 = time.perf_counter()
+        # full router (all tokens): logits, softmax top-k
+        logits = x_host @ rw.T
+        p = np.exp(logits - logits.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        sel = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+        w = np.take_along_axis(p, sel, -1)
+        w /= w.sum(-1, keepdims=True) + np.float32(1e-20)
+        xd = quant.act_dequant(*quant.act_quant(x_host))
+        out = np.zeros((T, H), np.float32)
+        t_fixed = time.perf_counter()
+        # routed experts of the sample (using the device routing, identical)
+        for e in range(sample_experts):
+            t, j = np.nonzero(ids == e)
+            if t.size:
+                out[t] += wts[t, j][:, None] * expert(xd[t], *deq[e])
+        t_routed = time.perf_counter()
+        gate = 1.0 / (1.0 + np.exp(-(x_host @ sgl)))
+        out += gate[:, None] * expert(xd, *sh)
+        t_end = time.perf_counter()
+        return (t_fixed - t0) + (t_end - t_routed), t_routed - t_fixed
+
+    with threadpool_limits(limits=cores):
+        run()                                  # warm-up
+        runs = [run() for _ in range(3)]
+    fixed = statistics.median(r[0] for r in runs)
+    routed = statistics.median(r[1] for r in runs)
+    est = fixed + routed * (E / sample_experts)
+    return {
+        "value": round(T / est, 2), "unit": "tokens/s", "cores": cores,
+        "kind": "port",
+        "sample": (f"numpy restatement of the quantized C2 layer (oracle "
+                   f"act_quant + fp32 BLAS on pre-dequantized weights): router, "
+                   f"activation quant and shared expert over all {T} tokens, "
+                   f"routed experts 0-{sample_experts - 1} of {E} with all "
+                   f"their tokens, scaled x{E // sample_experts}; median of 3 "
+                   f"after a warm-up; {cores} BLAS threads"),
+        "seconds_per_layer_estimate": round(est, 3),
+    }
+
+
+# --------------------------------------------------------------------------
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-iters", type=int, default=20)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus "
+              f"{args.gpus}); the MoE layer's multi-GPU expert-parallel "
+              f"sharding is a design note, not a measured path.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    from sllm_amd import _lib
+    from sllm_amd.moe import STAGES, qwen_workspace_bytes
+    from sllm_amd.runtime import (DeviceBuffer, Event, memset, sync, to_bf16,
+                                  to_device_raw)
+    if not _lib.available():
+        raise RuntimeError(f"libsllm_moe.so unavailable: {_lib._lib_error}")
+
+    c = dict(C2)
+    T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
+    t_setup = time.perf_counter()
+    layer = DeviceLayer(c, seed=args.seed)
+    x_host = to_bf16_values(layer.rng.standard_normal((T, H)).astype(np.float32))
+    x = to_device_raw(to_bf16(x_host))
+    out = DeviceBuffer(T * H * 2)
+    ws = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, "prefill"))
+    dbg = {"ids_out": DeviceBuffer(T * k * 4), "w_out": DeviceBuffer(T * k * 4),
+           "counts_out": DeviceBuffer(E * 4)}
+    layer_call(layer, x, out, ws, T, "prefill", debug=dbg)
+    sync()
+    counts = dbg["counts_out"].copy_host_raw(np.int32, (E,))
+    touched = int((counts > 0).sum())
+    log(f"setup {time.perf_counter() - t_setup:.1f}s; touched experts {touched}")
+
+    # ---- headline: K steps of the full layer ---------------------------
+    for _ in range(args.warmup):
+        layer_call(layer, x, out, ws, T, "prefill")
+    sync()
+    e0, e1 = Event(), Event()
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        layer_call(layer, x, out, ws, T, "prefill")
+    e1.record()
+    e1.synchronize()
+    wall = time.perf_counter() - w0
+    sync()
+    ms = e0.elapsed_ms(e1) / args.steps
+    tok_s = T / (ms / 1e3)
+    log(f"prefill {ms:.3f} ms/layer ({tok_s:.4g} tok/s), wall {wall * 1e3 / args.steps:.3f} ms")
+
+    # ---- per-stage breakdown (roofline of the dominant kernel) ----------
+    evs = [Event() for _ in range(2 * len(STAGES))]
+    per_stage = {s: [] for s in STAGES}
+    for _ in range(max(5, min(args.steps, 20))):
+        layer_call(layer, x, out, ws, T, "prefill", stage_events=evs)
+        evs[-1].synchronize()
+        for i, s in enumerate(STAGES):
+            per_stage[s].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]))
+    stage_ms = {s: statistics.median(v) for s, v in per_stage.items()}
+    dom = max(("expert_up", "expert_down"), key=lambda s: stage_ms[s])
+    dom_bytes = gemm1_bytes(c, touched) if dom == "expert_up" else gemm2_bytes(c, touched)
+    dom_gbps = dom_bytes / (stage_ms[dom] / 1e3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"traffic_{dom}_c2.json")
+    if os.path.isfile(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    flops, bytes_ = prefill_work(c, touched)
+    t_s = ms / 1e3
+    layer_info = {
+        "ms": round(ms, 4), "flops": flops, "bytes": bytes_,
+        "mfma_frac": round(flops / t_s / (PEAK_FP8_TFLOPS * 1e12), 4),
+        "hbm_frac": round(bytes_ / t_s / (PEAK_HBM_GBPS * 1e9), 4),
+        "attainable_frac": round(max(flops / (PEAK_FP8_TFLOPS * 1e12),
+                                     bytes_ / (PEAK_HBM_GBPS * 1e9)) / t_s, 4),
+        "stage_ms": {s: round(v, 4) for s, v in stage_ms.items()},
+        "touched_experts": touched,
+    }
+
+    # ---- decode batches (C3) -------------------------------------------
+    decode = {}
+    if not args.no_decode:
+        flush = DeviceBuffer(512 << 20)
+        for B in (1, 8, 32, 64):
+            xb_host = to_bf16_values(layer.rng.standard_normal((B, H)).astype(np.float32))
+            xb = to_device_raw(to_bf16(xb_host))
+            ob = DeviceBuffer(B * H * 2)
+            wsb = DeviceBuffer(qwen_workspace_bytes(B, H, E, I, Is, k, "decode"))
+            cb = DeviceBuffer(E * 4)
+            layer_call(layer, xb, ob, wsb, B, "decode", debug={"counts_out": cb})
+            sync()
+            tb = int((cb.copy_host_raw(np.int32, (E,)) > 0).sum())
+            times = []
+            a0, a1 = Event(), Event()
+            for it in range(args.decode_iters + 3):
+                memset(flush, it & 0xFF, flush.nbytes)
+                a0.record()
+                layer_call(layer, xb, ob, wsb, B, "decode")
+                a1.record()
+                a1.synchronize()
+                if it >= 3:
+                    times.append(a0.elapsed_ms(a1) * 1e3)
+            us = statistics.median(times)
+            nb = decode_bytes(c, B, tb)
+            decode[str(B)] = {"us": round(us, 2), "touched_experts": tb,
+                              "bytes": nb, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                              "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+            log(f"decode B={B}: {us:.1f} us, touched {tb}, "
+                f"{decode[str(B)]['GBps']} GB/s")
+
+    # ---- CPU baseline -----------------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        ids = dbg["ids_out"].copy_host_raw(np.int32, (T, k))
+        wts = dbg["w_out"].copy_host().reshape(T, k)
+        tc = time.perf_counter()
+        cpu = cpu_baseline(layer, x_host, ids, wts)
+        log(f"cpu baseline {cpu['value']} tok/s ({time.perf_counter() - tc:.1f}s)")
+
+    res = {
+        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on device, bf16 N(0,1) activations)",
+        "config": {"workload": "C2 Qwen-style FP8 MoE layer, prefill",
+                   "tokens": T, "hidden": H, "experts": E, "top_k": k,
+                   "intermediate": I, "shared_intermediate": Is,
+                   "weights": "e4m3 + fp32 128x128 block scales",
+                   "activations": "bf16, e4m3 per 1x128 before each expert GEMM"},
+        "roofline": {"bound": "hbm", "kernel": f"moe_gemm{1 if dom == 'expert_up' else 2}_kernel<fp8>",
+                     "achieved": round(dom_gbps, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(dom_gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes": dom_bytes,
+                     "avg_ms": round(stage_ms[dom], 4)},
+        "layer": layer_info,
+        "decode": decode,
+        "decode_us_at_32": decode.get("32", {}).get("us"),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def to_bf16_values(a):
+    """float32 array rounded to bf16 values (kept as float32)."""
+    import numpy as np
+    u = a.astype(np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -184,6 +184,21 @@ int sllm_quantize_weight_mxfp4(const float* w, int N, int K, void* packed,
 #define SLLM_MOE_MODE_PREFILL 1 /* e4m3 activations, grouped MFMA GEMMs */
 #define SLLM_MOE_MODE_DECODE 2  /* fp32 activations, dequant GEMV */
 
+/* Optional per-stage timing: when `stage_events` is non-NULL it points to
+ * 2 * SLLM_MOE_STAGES hipEvent_t handles (from sllm_event_new); event 2s is
+ * recorded on the layer's stream before stage s and 2s+1 after it. Stages
+ * that do not run for a call record nothing. */
+#define SLLM_MOE_STAGES 9
+#define SLLM_MOE_STAGE_ROUTER_GEMM 0
+#define SLLM_MOE_STAGE_ROUTE 1
+#define SLLM_MOE_STAGE_PERMUTE 2
+#define SLLM_MOE_STAGE_ACT_QUANT 3 /* activation quant + shared gate */
+#define SLLM_MOE_STAGE_EXPERT_UP 4 /* routed gate/up (+SwiGLU) */
+#define SLLM_MOE_STAGE_EXPERT_DOWN 5
+#define SLLM_MOE_STAGE_SHARED_UP 6
+#define SLLM_MOE_STAGE_SHARED_DOWN 7
+#define SLLM_MOE_STAGE_COMBINE 8
+
 /* Qwen-style layer (ref/qwen4_exp.py:153-184): softmax top-k routing,
  * SwiGLU experts with FP8 e4m3 weights and fp32 128x128 block scales
  * (orientation (ceil(out/128), ceil(in/128)), loaders/fp8.py:98-135),
@@ -227,6 +242,7 @@ typedef struct sllm_moe_qwen_args {
   void* workspace;
   long workspace_bytes;
   void* stream;
+  void** stage_events;
 } sllm_moe_qwen_args;
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
@@ -270,6 +286,7 @@ typedef struct sllm_moe_ds_args {
   void* workspace;
   long workspace_bytes;
   void* stream;
+  void** stage_events;
 } sllm_moe_ds_args;
 
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a);

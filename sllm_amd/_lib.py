@@ -36,7 +36,7 @@ class QwenArgs(Structure):
         ("sg", P), ("sg_s", P), ("su", P), ("su_s", P), ("sd", P), ("sd_s", P),
         ("sgl", P), ("out", P), ("logits_out", P), ("w_out", P),
         ("ids_out", P), ("counts_out", P), ("workspace", P),
-        ("workspace_bytes", c_long), ("stream", P),
+        ("workspace_bytes", c_long), ("stream", P), ("stage_events", P),
     ]
 
 
@@ -53,7 +53,7 @@ class DeepseekArgs(Structure):
         ("s1", P), ("s1_s", P), ("s3", P), ("s3_s", P), ("s2", P), ("s2_s", P),
         ("out", P), ("logits_out", P), ("w_out", P), ("ids_out", P),
         ("counts_out", P), ("workspace", P), ("workspace_bytes", c_long),
-        ("stream", P),
+        ("stream", P), ("stage_events", P),
     ]
 
 

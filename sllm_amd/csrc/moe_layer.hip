@@ -87,6 +87,27 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   return p;
 }
 
+// Records the stage-boundary events when the caller asked for them.
+struct StageClock {
+  void** ev;
+  hipStream_t st;
+  int begin(int s) const {
+    if (ev) SLLM_HIP(hipEventRecord((hipEvent_t)ev[2 * s], st));
+    return 0;
+  }
+  int end(int s) const {
+    if (ev) SLLM_HIP(hipEventRecord((hipEvent_t)ev[2 * s + 1], st));
+    return 0;
+  }
+};
+
+#define STAGE(clk, s, call)                                                   \
+  do {                                                                        \
+    if ((clk).begin(s)) return -1;                                            \
+    if (call) return -1;                                                      \
+    if ((clk).end(s)) return -1;                                              \
+  } while (0)
+
 template <typename A>
 static int check_common(const A* a, const char* who) {
   SLLM_REQUIRE(a, "%s: null args", who);
@@ -175,80 +196,83 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   float* gate = (float*)(ws + p.gate);
   const float eps = a->renorm_eps;
 
-  if (!a->logits_given &&
-      launch_router_gemm((const uint16_t*)a->x, (const uint16_t*)a->router_w,
-                         logits, T, E, H, st))
-    return -1;
-  if (launch_route_softmax(logits, w, ids, T, E, k, eps, st)) return -1;
-  if (launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
-                     ntiles, p.max_tiles, ws + p.pscr, st))
-    return -1;
+  const StageClock clk{a->stage_events, st};
+  if (!a->logits_given)
+    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+          launch_router_gemm((const uint16_t*)a->x,
+                             (const uint16_t*)a->router_w, logits, T, E, H,
+                             st));
+  STAGE(clk, SLLM_MOE_STAGE_ROUTE,
+        launch_route_softmax(logits, w, ids, T, E, k, eps, st));
+  STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
+        launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
+                       ntiles, p.max_tiles, ws + p.pscr, st));
 
   if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);
-    if (sh && launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr, nullptr,
-                               (const uint16_t*)a->sgl, gate, st))
-      return -1;
-    if (launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
-                    p.max_tiles, offsets, (const uint8_t*)a->wg, a->wg_s,
-                    (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, h, st))
-      return -1;
-    if (launch_gemv(wf, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                    offsets, (const uint8_t*)a->wd, a->wd_s, nullptr, nullptr,
-                    H, I, w, 0.f, y, st))
-      return -1;
+    if (sh) STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
+          launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr, nullptr,
+          (const uint16_t*)a->sgl, gate, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+          launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
+          p.max_tiles, offsets, (const uint8_t*)a->wg, a->wg_s,
+          (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, h, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+          launch_gemv(wf, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->wd, a->wd_s, nullptr, nullptr,
+          H, I, w, 0.f, y, st));
     float* y_sh = nullptr;
     if (sh) {
       float* h_sh = (float*)(ws + p.hq_sh);
       y_sh = (float*)(ws + p.y_sh);
-      if (launch_gemv(wf, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
-                      nullptr, (const uint8_t*)a->sg, a->sg_s,
-                      (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
-                      h_sh, st))
-        return -1;
-      if (launch_gemv(wf, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
-                      nullptr, (const uint8_t*)a->sd, a->sd_s, nullptr,
-                      nullptr, H, Is, gate, 0.f, y_sh, st))
-        return -1;
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+            launch_gemv(wf, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
+            nullptr, (const uint8_t*)a->sg, a->sg_s,
+            (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
+            h_sh, st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+            launch_gemv(wf, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
+            nullptr, (const uint8_t*)a->sd, a->sd_s, nullptr,
+            nullptr, H, Is, gate, 0.f, y_sh, st));
     }
-    if (launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+          launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   } else {
     uint8_t* xq = (uint8_t*)(ws + p.xq);
     float* sx = (float*)(ws + p.sx);
     uint8_t* hq = (uint8_t*)(ws + p.hq);
     float* hs = (float*)(ws + p.hs);
     uint16_t* y = (uint16_t*)(ws + p.y);
-    if (launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
-                         sh ? (const uint16_t*)a->sgl : nullptr, gate, st))
-      return -1;
-    if (launch_gemm1_fp8(xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                         offsets, (const uint8_t*)a->wg, a->wg_s,
-                         (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, 0,
-                         hq, hs, st))
-      return -1;
-    if (launch_gemm2_fp8(hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                         offsets, (const uint8_t*)a->wd, a->wd_s, I, H, w, y,
-                         st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
+          launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
+          sh ? (const uint16_t*)a->sgl : nullptr, gate, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+          launch_gemm1_fp8(xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->wg, a->wg_s,
+          (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, 0,
+          hq, hs, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+          launch_gemm2_fp8(hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->wd, a->wd_s, I, H, w, y,
+          st));
     uint16_t* y_sh = nullptr;
     if (sh) {
       uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
       float* hs_sh = (float*)(ws + p.hs_sh);
       y_sh = (uint16_t*)(ws + p.y_sh);
-      if (launch_gemm1_fp8(xq, sx, nullptr, k, T, nullptr, nullptr, 0, nullptr,
-                           (const uint8_t*)a->sg, a->sg_s,
-                           (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
-                           0, hq_sh, hs_sh, st))
-        return -1;
-      if (launch_gemm2_fp8(hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
-                           nullptr, (const uint8_t*)a->sd, a->sd_s, Is, H, gate,
-                           y_sh, st))
-        return -1;
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+            launch_gemm1_fp8(xq, sx, nullptr, k, T, nullptr, nullptr, 0, nullptr,
+            (const uint8_t*)a->sg, a->sg_s,
+            (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
+            0, hq_sh, hs_sh, st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+            launch_gemm2_fp8(hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
+            nullptr, (const uint8_t*)a->sd, a->sd_s, Is, H, gate,
+            y_sh, st));
     }
-    if (launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+          launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
   return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
                     a->ids_out, a->counts_out, st);
@@ -295,77 +319,79 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   int* tiles = (int*)(ws + p.tiles);
   int* ntiles = (int*)(ws + p.ntiles);
 
-  if (!a->logits_given &&
-      launch_router_gemm((const uint16_t*)a->x, (const uint16_t*)a->router_w,
-                         logits, T, E, H, st))
-    return -1;
-  if (launch_route_grouped(logits, a->bias, w, ids, T, E, k, a->n_group,
-                           a->topk_group, a->scoring, a->route_scale, st))
-    return -1;
-  if (launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
-                     ntiles, p.max_tiles, ws + p.pscr, st))
-    return -1;
+  const StageClock clk{a->stage_events, st};
+  if (!a->logits_given)
+    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+          launch_router_gemm((const uint16_t*)a->x,
+                             (const uint16_t*)a->router_w, logits, T, E, H,
+                             st));
+  STAGE(clk, SLLM_MOE_STAGE_ROUTE,
+        launch_route_grouped(logits, a->bias, w, ids, T, E, k, a->n_group,
+                             a->topk_group, a->scoring, a->route_scale, st));
+  STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
+        launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
+                       ntiles, p.max_tiles, ws + p.pscr, st));
 
   if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);
-    if (launch_gemv(1, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
-                    p.max_tiles, offsets, (const uint8_t*)a->w1, a->w1_s,
-                    (const uint8_t*)a->w3, a->w3_s, I, H, nullptr, L, h, st))
-      return -1;
-    if (launch_gemv(1, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                    offsets, (const uint8_t*)a->w2, a->w2_s, nullptr, nullptr,
-                    H, I, w, 0.f, y, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+          launch_gemv(1, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
+          p.max_tiles, offsets, (const uint8_t*)a->w1, a->w1_s,
+          (const uint8_t*)a->w3, a->w3_s, I, H, nullptr, L, h, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+          launch_gemv(1, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->w2, a->w2_s, nullptr, nullptr,
+          H, I, w, 0.f, y, st));
     float* y_sh = nullptr;
     if (sh) {
       float* h_sh = (float*)(ws + p.hq_sh);
       y_sh = (float*)(ws + p.y_sh);
-      if (launch_gemv(0, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
-                      nullptr, (const uint8_t*)a->s1, a->s1_s,
-                      (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L, h_sh,
-                      st))
-        return -1;
-      if (launch_gemv(0, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
-                      nullptr, (const uint8_t*)a->s2, a->s2_s, nullptr,
-                      nullptr, H, Is, nullptr, 0.f, y_sh, st))
-        return -1;
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+            launch_gemv(0, 1, a->x, 1, 0, nullptr, k, T, nullptr, nullptr, 1,
+            nullptr, (const uint8_t*)a->s1, a->s1_s,
+            (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L, h_sh,
+            st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+            launch_gemv(0, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
+            nullptr, (const uint8_t*)a->s2, a->s2_s, nullptr,
+            nullptr, H, Is, nullptr, 0.f, y_sh, st));
     }
-    if (launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+          launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   } else {
     uint8_t* xq = (uint8_t*)(ws + p.xq);
     float* sx = (float*)(ws + p.sx);
     uint8_t* hq = (uint8_t*)(ws + p.hq);
     float* hs = (float*)(ws + p.hs);
     uint16_t* y = (uint16_t*)(ws + p.y);
-    if (launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx, nullptr,
-                         nullptr, st))
-      return -1;
-    if (launch_gemm1_mx(1, xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                        offsets, (const uint8_t*)a->w1, a->w1_s,
-                        (const uint8_t*)a->w3, a->w3_s, I, H, w, L, hq, hs, st))
-      return -1;
-    if (launch_gemm2_mx(1, hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-                        offsets, (const uint8_t*)a->w2, a->w2_s, I, H, y, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
+          launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx, nullptr,
+          nullptr, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+          launch_gemm1_mx(1, xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->w1, a->w1_s,
+          (const uint8_t*)a->w3, a->w3_s, I, H, w, L, hq, hs, st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+          launch_gemm2_mx(1, hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
+          offsets, (const uint8_t*)a->w2, a->w2_s, I, H, y, st));
     uint16_t* y_sh = nullptr;
     if (sh) {
       uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
       float* hs_sh = (float*)(ws + p.hs_sh);
       y_sh = (uint16_t*)(ws + p.y_sh);
-      if (launch_gemm1_mx(0, xq, sx, nullptr, k, T, nullptr, nullptr, 0,
-                          nullptr, (const uint8_t*)a->s1, a->s1_s,
-                          (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L,
-                          hq_sh, hs_sh, st))
-        return -1;
-      if (launch_gemm2_mx(0, hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
-                          nullptr, (const uint8_t*)a->s2, a->s2_s, Is, H, y_sh,
-                          st))
-        return -1;
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+            launch_gemm1_mx(0, xq, sx, nullptr, k, T, nullptr, nullptr, 0,
+            nullptr, (const uint8_t*)a->s1, a->s1_s,
+            (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L,
+            hq_sh, hs_sh, st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+            launch_gemm2_mx(0, hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
+            nullptr, (const uint8_t*)a->s2, a->s2_s, Is, H, y_sh,
+            st));
     }
-    if (launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st))
-      return -1;
+    STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+          launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
   return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
                     a->ids_out, a->counts_out, st);

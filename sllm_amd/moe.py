@@ -26,6 +26,20 @@ from .runtime import DeviceBuffer, ptr, stream_handle, to_bf16, to_device, to_de
 
 MODES = {"auto": 0, "prefill": 1, "decode": 2}
 SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+# stage order of the optional per-stage events (include/sllm_moe.h)
+STAGES = ("router_gemm", "route", "permute", "act_quant", "expert_up",
+          "expert_down", "shared_up", "shared_down", "combine")
+
+
+def _event_array(events):
+    """ctypes void*[2 * len(STAGES)] from a list of runtime.Event (or None)."""
+    if events is None:
+        return None
+    if len(events) != 2 * len(STAGES):
+        raise ValueError(f"need {2 * len(STAGES)} events")
+    import ctypes
+    arr = (ctypes.c_void_p * len(events))(*[e._ev for e in events])
+    return arr
 
 
 def _mode(m) -> int:
@@ -77,7 +91,7 @@ def qwen_workspace_bytes(T, H, E, I, Is, topk, mode="auto", has_shared=True,
 def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
                      mode="auto", out_f32=False, wdtype=0, eps=1e-20,
                      logits=None, workspace=None, workspace_bytes=None,
-                     stream=None, debug=None) -> None:
+                     stream=None, debug=None, stage_events=None) -> None:
     """One Qwen-style MoE layer on device buffers (see include/sllm_moe.h
     sllm_moe_qwen_args for shapes). `weights` maps router_w, wg, wg_s, wu,
     wu_s, wd, wd_s [, sg, sg_s, su, su_s, sd, sd_s, sgl] to device buffers;
@@ -88,6 +102,10 @@ def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
             workspace_bytes = workspace.numel() * workspace.element_size()
     a = _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
                    weights, out, debug, workspace, workspace_bytes, stream)
+    evs = _event_array(stage_events)
+    if evs is not None:
+        import ctypes
+        a.stage_events = ctypes.cast(evs, ctypes.c_void_p)
     _lib.check(_lib.lib().sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
 
 
@@ -138,7 +156,7 @@ def deepseek_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
                          mode="auto", out_f32=False, n_group=1, topk_group=1,
                          scoring="sigmoid", route_scale=1.0, swiglu_limit=0.0,
                          logits=None, workspace=None, workspace_bytes=None,
-                         stream=None, debug=None) -> None:
+                         stream=None, debug=None, stage_events=None) -> None:
     """One DeepSeek-style MoE layer on device buffers (shapes in
     include/sllm_moe.h sllm_moe_ds_args). `weights` maps router_w, bias, w1,
     w1_s, w3, w3_s, w2, w2_s [, s1, s1_s, s3, s3_s, s2, s2_s]."""
@@ -149,6 +167,10 @@ def deepseek_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
     a = _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
                  scoring, route_scale, swiglu_limit, x, logits, weights, out,
                  debug, workspace, workspace_bytes, stream)
+    evs = _event_array(stage_events)
+    if evs is not None:
+        import ctypes
+        a.stage_events = ctypes.cast(evs, ctypes.c_void_p)
     _lib.check(_lib.lib().sllm_moe_ds_forward(a), "sllm_moe_ds_forward")
 
 
