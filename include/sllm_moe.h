@@ -151,7 +151,8 @@ int sllm_moe_route_grouped(const float* logits, const float* bias,
                            int n_group, int topk_group, int scoring,
                            float route_scale, void* stream);
 /* Stable expert-major permutation of ids (N = T*k int32) with a ragged tile
- * table of ceil(count/bm) row tiles per expert. new (the reference has no
+ * table of ceil(count/bm) row tiles per expert: tile_info holds max_tiles
+ * int4 {expert, first permuted row, rows, 0}. new (the reference has no
  * permute; replaces the np.where grouping of ref/deepseek_v4.py:1080-1086).
  * scratch >= sllm_moe_permute_scratch_bytes(N, E). */
 long sllm_moe_permute_scratch_bytes(int N, int E);
@@ -169,6 +170,18 @@ int sllm_moe_act_quant(const void* x_bf16, int T, int H, int pow2,
 int sllm_moe_combine(const void* y, int y_f32, const int* inv_pos, int topk,
                      const void* y_shared, int T, int H, int out_f32,
                      void* out, void* stream);
+/* Streaming weight layout (gemm_stream.hip): a one-time repack of expert
+ * weights into MFMA operand order so the prefill GEMMs read contiguous HBM.
+ * fp4 = 0: w0 [, w1] are (E, N, K) e4m3; fp4 = 1: (E, N, K/2) packed e2m1
+ * with (E, N, K/32) e8m0 scales s0 [, s1], whose packed copy goes to
+ * out_scales. up = 1 packs a gate/up pair (N = intermediate, K = hidden,
+ * N % 128 == 0), up = 0 a down weight (N = hidden, K = intermediate,
+ * N % 256 == 0); K % 128 == 0. new: no reference counterpart. */
+long sllm_moe_packed_bytes(int fp4, int up, int E, int N, int K);
+long sllm_moe_packed_scale_bytes(int up, int E, int N, int K);
+int sllm_moe_pack_weights(int fp4, int up, const void* w0, const void* w1,
+                          const void* s0, const void* s1, int E, int N, int K,
+                          void* out, void* out_scales, void* stream);
 /* Synthetic-weight quantizers (data preparation): FP8 128x128 block
  * (s = amax/448, optionally its power-of-two ceiling) and MXFP4 per 32. */
 int sllm_quantize_weight_fp8(const float* w, int N, int K, int pow2,
@@ -243,6 +256,14 @@ typedef struct sllm_moe_qwen_args {
   long workspace_bytes;
   void* stream;
   void** stage_events;
+  /* Optional packed weights (sllm_moe_pack_weights, fp8): when wgu_packed is
+   * set the prefill path streams them (wd_packed, and for a shared expert
+   * sgu_packed / sd_packed, must then be set too); the fp32 scale tensors
+   * above are still read. */
+  const void* wgu_packed; /* pack(up=1, wg, wu, E, I, H) */
+  const void* wd_packed;  /* pack(up=0, wd, E, H, I) */
+  const void* sgu_packed; /* pack(up=1, sg, su, 1, Is, H) */
+  const void* sd_packed;  /* pack(up=0, sd, 1, H, Is) */
 } sllm_moe_qwen_args;
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
@@ -287,6 +308,14 @@ typedef struct sllm_moe_ds_args {
   long workspace_bytes;
   void* stream;
   void** stage_events;
+  /* Optional packed weights (sllm_moe_pack_weights) for the prefill path:
+   * routed fp4 w1/w3 and w2 with their packed e8m0 scales, shared fp8. */
+  const void* w13_packed;
+  const void* w13_s_packed;
+  const void* w2_packed;
+  const void* w2_s_packed;
+  const void* s13_packed;
+  const void* s2_packed;
 } sllm_moe_ds_args;
 
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a);

@@ -37,6 +37,7 @@ class QwenArgs(Structure):
         ("sgl", P), ("out", P), ("logits_out", P), ("w_out", P),
         ("ids_out", P), ("counts_out", P), ("workspace", P),
         ("workspace_bytes", c_long), ("stream", P), ("stage_events", P),
+        ("wgu_packed", P), ("wd_packed", P), ("sgu_packed", P), ("sd_packed", P),
     ]
 
 
@@ -54,6 +55,8 @@ class DeepseekArgs(Structure):
         ("out", P), ("logits_out", P), ("w_out", P), ("ids_out", P),
         ("counts_out", P), ("workspace", P), ("workspace_bytes", c_long),
         ("stream", P), ("stage_events", P),
+        ("w13_packed", P), ("w13_s_packed", P), ("w2_packed", P),
+        ("w2_s_packed", P), ("s13_packed", P), ("s2_packed", P),
     ]
 
 
@@ -108,6 +111,10 @@ SIGNATURES = {
     "sllm_moe_act_quant": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P]),
     "sllm_moe_combine": (c_int, [P, c_int, P, c_int, P, c_int, c_int, c_int,
                                  P, P]),
+    "sllm_moe_packed_bytes": (c_long, [c_int, c_int, c_int, c_int, c_int]),
+    "sllm_moe_packed_scale_bytes": (c_long, [c_int, c_int, c_int, c_int]),
+    "sllm_moe_pack_weights": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int,
+                                      c_int, P, P, P]),
     "sllm_quantize_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P, P]),
     "sllm_quantize_weight_mxfp4": (c_int, [P, c_int, c_int, P, P, P]),
     "sllm_moe_qwen_workspace_bytes": (c_long, [POINTER(QwenArgs)]),

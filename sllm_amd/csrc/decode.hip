@@ -129,9 +129,10 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(
   if (tile_info) {
     const int tile = blockIdx.y;
     if (tile >= *num_tiles) return;
-    e = tile_info[2 * tile];
-    row_begin = offsets[e];
-    rows = offsets[e + 1] - row_begin;
+    const int4 d = *(const int4*)(tile_info + 4 * tile);
+    e = d.x;
+    row_begin = d.y;
+    rows = d.z;
   } else {
     e = 0;
     row_begin = 0;

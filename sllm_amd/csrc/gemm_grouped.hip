@@ -105,9 +105,10 @@ __device__ __forceinline__ bool resolve_tile(int tile, const int* tile_info,
                                              TileRows& tr) {
   if (tile_info) {
     if (tile >= *num_tiles) return false;
-    tr.e = tile_info[2 * tile];
-    tr.row_begin = offsets[tr.e] + tile_info[2 * tile + 1];
-    tr.rows = min(G_BM, offsets[tr.e + 1] - tr.row_begin);
+    const int4 d = *(const int4*)(tile_info + 4 * tile);
+    tr.e = d.x;
+    tr.row_begin = d.y;
+    tr.rows = min(G_BM, d.z);
   } else {
     tr.e = 0;
     tr.row_begin = tile * G_BM;

@@ -1,0 +1,583 @@
+// Persistent, weight-streaming grouped expert GEMMs (prefill) and the packed
+// weight layouts they read.
+//
+// Same arithmetic and epilogues as gemm_grouped.hip (see there for the
+// reference semantics); this file changes how the expert weights move:
+//
+// * Packed weights. A one-time repack (sllm_moe_pack_weights) stores each
+//   expert's weights in MFMA operand order: for every (expert, column slab,
+//   128-wide K step) one contiguous block holds, wave by wave and subtile by
+//   subtile, exactly the bytes each lane feeds the MFMA, so every wave load
+//   instruction reads 1 KB of consecutive HBM and a workgroup streams one
+//   contiguous 32 KB (fp8) / 16 KB (fp4) block per K step.
+// * Persistent workgroups, one per CU (up to 512 registers per lane). Each
+//   owns a contiguous run of work items (row tile x column slab, routed
+//   items first, then the shared expert's) and walks the flat sequence of
+//   (item, K step); the weight operands of step s+2 are in flight while
+//   step s computes, across item boundaries, so the weight stream does not
+//   drain between tiles. The activation tile of step s+1 is fetched into
+//   registers during step s and double-buffered in LDS.
+// * Item descriptors and gathered row indices for the whole run are loaded
+//   into LDS once at the start.
+#include "launch.h"
+
+namespace sllm {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { SF_FP8_F32S = 0, SF_FP8_POW2 = 1, SF_FP4 = 2 };
+
+constexpr int ST_BM = 128;
+constexpr int ST_LDS = 144;          // A row stride in LDS (128 + 16 pad)
+constexpr int ST_MAX_ITEMS = 32;     // work items per workgroup
+
+// ---------------------------------------------------------------------------
+// packed layouts
+// ---------------------------------------------------------------------------
+// up   (MODE 0): W1, W3 (E, N, K), N = intermediate, K = hidden; slab = 128
+//       h columns, subtile s of wave w = rows 128 nt + 32 w + 16 (s & 1) +
+//       (l % 16) of W1 (s < 2) or W3 (s >= 2).
+// down (MODE 1): W2 (E, N, K), N = hidden, K = intermediate; slab = 256
+//       columns, subtile s of wave w = rows 256 nt + 64 w + 16 s + (l % 16).
+// fp8: block (e, nt, kb) = 32 KB at ((e NT + nt) KB + kb) * 32768, inside
+//       [w 4][s 4][h 2][lane 64][16 B]: the lane's 32 bytes are K
+//       [128 kb + 32 (l / 16), +32), half h = bytes [16 h, 16 h + 16).
+// fp4: block = 16 KB, [w][s][lane][16 B]: K [128 kb + 32 (l / 16), +32) =
+//       packed bytes [64 kb + 16 (l / 16), +16); e8m0 scales packed as one
+//       dword per lane per block: 1 KB blocks [w][lane][s], byte s = scale of
+//       (row of subtile s, K block 4 kb + l / 16).
+__device__ __forceinline__ int slab_row(int up, int nt, int w, int s, int l) {
+  return up ? nt * 128 + w * 32 + (s & 1) * 16 + (l & 15)
+            : nt * 256 + w * 64 + s * 16 + (l & 15);
+}
+
+__global__ void pack_fp8_kernel(const uint8_t* __restrict__ w0,
+                                const uint8_t* __restrict__ w1,
+                                uint8_t* __restrict__ out, int E, int N, int K,
+                                int up) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int NT = up ? N / 128 : N / 256, KB = K / 128;
+  const long nchunks = (long)E * NT * KB * 2048;
+  if (c >= nchunks) return;
+  const int l = c & 63, h = (c >> 6) & 1, s = (c >> 7) & 3, w = (c >> 9) & 3;
+  const long blk = c >> 11;
+  const int kb = (int)(blk % KB);
+  const long t = blk / KB;
+  const int nt = (int)(t % NT), e = (int)(t / NT);
+  const int row = slab_row(up, nt, w, s, l);
+  const uint8_t* src = (up && s >= 2) ? w1 : w0;
+  const size_t col = (size_t)kb * 128 + (l >> 4) * 32 + h * 16;
+  *(uint4*)(out + c * 16) = *(const uint4*)(src + ((size_t)e * N + row) * K + col);
+}
+
+__global__ void pack_fp4_kernel(const uint8_t* __restrict__ w0,
+                                const uint8_t* __restrict__ w1,
+                                const uint8_t* __restrict__ s0,
+                                const uint8_t* __restrict__ s1,
+                                uint8_t* __restrict__ out,
+                                uint32_t* __restrict__ out_s, int E, int N,
+                                int K, int up) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int NT = up ? N / 128 : N / 256, KB = K / 128;
+  const long nchunks = (long)E * NT * KB * 1024;
+  if (c >= nchunks) return;
+  const int l = c & 63, s = (c >> 6) & 3, w = (c >> 8) & 3;
+  const long blk = c >> 10;
+  const int kb = (int)(blk % KB);
+  const long t = blk / KB;
+  const int nt = (int)(t % NT), e = (int)(t / NT);
+  const int row = slab_row(up, nt, w, s, l);
+  const uint8_t* src = (up && s >= 2) ? w1 : w0;
+  const size_t col = (size_t)kb * 64 + (l >> 4) * 16;
+  *(uint4*)(out + c * 16) =
+      *(const uint4*)(src + ((size_t)e * N + row) * (K / 2) + col);
+  if (s == 0) {  // one thread per (block, w, lane) writes the scale dword
+    uint32_t v = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rq = slab_row(up, nt, w, q, l);
+      const uint8_t* sp = (up && q >= 2) ? s1 : s0;
+      v |= (uint32_t)sp[((size_t)e * N + rq) * (K / 32) + kb * 4 + (l >> 4)]
+           << (8 * q);
+    }
+    out_s[blk * 256 + w * 64 + l] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming kernel
+// ---------------------------------------------------------------------------
+
+
+template <int BF>
+struct BSet {
+  v8i v[4];
+  uint32_t sc;
+};
+
+template <int MODE>
+__device__ __forceinline__ int seg_items(const SegDesc& s) {
+  const int ntn = MODE == 0 ? s.N / 128 : s.N / 256;
+  const int rt = s.tile_info ? *s.num_tiles : (s.total_rows + ST_BM - 1) / ST_BM;
+  return rt * ntn;
+}
+
+__device__ __forceinline__ uint32_t e8m0_bits(float pow2) {
+  return (__float_as_uint(pow2) >> 23) & 0xFF;
+}
+
+template <int BF>
+__device__ __forceinline__ f32x4 st_mma(const v8i& a, const v8i& b, f32x4 c,
+                                        uint32_t sa, uint32_t sb) {
+  if constexpr (BF == SF_FP8_F32S) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0,
+                                                            0, 0, 0);
+  } else if constexpr (BF == SF_FP8_POW2) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+        a, b, c, 0, 0, 0, (int)sa, 0, (int)sb);
+  } else {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+        a, b, c, 0, 4, 0, (int)sa, 0, (int)sb);
+  }
+}
+
+template <int BF, int MODE>
+struct Stream {
+  static constexpr int NTW = MODE == 0 ? 128 : 256;
+  static constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
+};
+
+// item descriptor in LDS: x = seg | nt << 1, y = e, z = row_begin, w = rows
+template <int BF, int MODE>
+__global__ __launch_bounds__(256, 1) void moe_stream_kernel(
+    SegDesc S0, SegDesc S1, int nseg, int topk, float limit, int pow2) {
+  __shared__ int4 desc[ST_MAX_ITEMS];
+  __shared__ int rsrc[ST_MAX_ITEMS][ST_BM];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][ST_BM * ST_LDS];
+  __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM];
+  __shared__ float red[4][ST_BM];
+
+  constexpr int NTW = Stream<BF, MODE>::NTW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, lc = lane & 15;
+
+  const int n0 = seg_items<MODE>(S0);
+  const int n1 = nseg > 1 ? seg_items<MODE>(S1) : 0;
+  const int total = n0 + n1;
+  const int chunk = (total + gridDim.x - 1) / gridDim.x;
+  const int lo = blockIdx.x * chunk;
+  const int hi = min(total, lo + chunk);
+  if (lo >= hi || chunk > ST_MAX_ITEMS) return;  // host sizes grid so chunk fits
+  const int nitems = hi - lo;
+
+  // ---- phase 0: descriptors and gathered row indices -> LDS ---------------
+  if (tid < nitems) {
+    const int it = lo + tid;
+    const int seg = it >= n0;
+    const SegDesc& S = seg ? S1 : S0;
+    const int li = seg ? it - n0 : it;
+    const int ntn = S.N / NTW;
+    const int rt = li / ntn, nt = li % ntn;
+    int e = 0, rb, rows;
+    if (S.tile_info) {
+      const int4 d = *(const int4*)(S.tile_info + 4 * rt);
+      e = d.x;
+      rb = d.y;
+      rows = min(ST_BM, d.z);
+    } else {
+      rb = rt * ST_BM;
+      rows = min(ST_BM, S.total_rows - rb);
+    }
+    desc[tid] = make_int4(seg | (nt << 1), e, rb, rows);
+  }
+  __syncthreads();
+  for (int q = tid; q < nitems * ST_BM; q += 256) {
+    const int i = q / ST_BM, r = q % ST_BM;
+    const int4 d = desc[i];
+    const SegDesc& S = (d.x & 1) ? S1 : S0;
+    int src = 0;
+    if (r < d.w) src = S.gather ? S.sorted_idx[d.z + r] / topk : d.z + r;
+    rsrc[i][r] = src;
+  }
+  __syncthreads();
+
+  // ---- per-step helpers ---------------------------------------------------
+  auto kb_of = [&](int i) {
+    const int4 d = desc[i];
+    return ((d.x & 1) ? S1.K : S0.K) / 128;
+  };
+  int total_steps = 0;
+  for (int i = 0; i < nitems; ++i) total_steps += kb_of(i);
+
+  auto load_b = [&](BSet<BF>& b, int i, int kb) {
+    const int4 d = desc[i];
+    const int seg = d.x & 1, nt = d.x >> 1;
+    const uint8_t* wp = seg ? S1.wp : S0.wp;
+    const int N = seg ? S1.N : S0.N, K = seg ? S1.K : S0.K;
+    const int NT = N / NTW, KB = K / 128;
+    const size_t blk = ((size_t)d.y * NT + nt) * KB + kb;
+    const uint8_t* base = wp + blk * Stream<BF, MODE>::BLK;
+    if constexpr (BF == SF_FP4) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 v = *(const uint4*)(base + (wave * 4 + s) * 1024 + lane * 16);
+        b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+      }
+      const uint32_t* sp = (const uint32_t*)(seg ? S1.s0 : S0.s0);
+      b.sc = sp[blk * 256 + wave * 64 + lane];
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 lo4 = *(const uint4*)(base + ((wave * 4 + s) * 2) * 1024 + lane * 16);
+        const uint4 hi4 = *(const uint4*)(base + ((wave * 4 + s) * 2 + 1) * 1024 + lane * 16);
+        b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
+                       (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
+      }
+      b.sc = 0;
+    }
+  };
+
+  const int my_row = tid >> 1, half = tid & 1;
+  uint4 af[4];
+  float sa_next = 0.f;
+  auto fetch_a = [&](int i, int kb) {
+    const int4 d = desc[i];
+    const SegDesc& S = (d.x & 1) ? S1 : S0;
+    const int K = S.K, KB = K / 128;
+    if (my_row < d.w) {
+      const uint4* p = (const uint4*)(S.a + (size_t)rsrc[i][my_row] * K + kb * 128 + half * 64);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) af[q] = p[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) af[q] = make_uint4(0, 0, 0, 0);
+    }
+    if (tid < ST_BM) sa_next = tid < d.w ? S.sa[(size_t)rsrc[i][tid] * KB + kb] : 0.f;
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // cursors: compute (ci, ckb), B prefetch (bi, bkb), A prefetch (ai, akb)
+  int ci = 0, ckb = 0, bi = 0, bkb = 0, ai = 0, akb = 0;
+  auto adv = [&](int& i, int& kb) {
+    if (++kb == kb_of(i)) {
+      kb = 0;
+      ++i;
+    }
+  };
+
+  // ---- epilogues ------------------------------------------------------------
+  auto epilogue = [&](int i, int ebuf) {
+    const int4 d = desc[i];
+    const int seg = d.x & 1, nt = d.x >> 1;
+    const SegDesc& S = seg ? S1 : S0;
+    const int rows = d.w, rb = d.z;
+    const int nmi = (rows + 15) >> 4;
+    if constexpr (MODE == 0) {
+      const int ntn = S.N / 128;
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) {
+        if (mi < nmi) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = mi * 16 + lg * 4 + v;
+            float rw = 1.f;
+            if (S.row_w && r < rows)
+              rw = S.row_w[S.row_w_by_idx ? S.sorted_idx[rb + r] : rb + r];
+            float amax = 0.f;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              float g = acc[mi][s][v], u = acc[mi][s + 2][v];
+              if (limit > 0.f) {
+                u = fminf(fmaxf(u, -limit), limit);
+                g = fminf(g, limit);
+              }
+              const float h = silu_f32(g) * u * rw;
+              acc[mi][s][v] = h;
+              amax = fmaxf(amax, fabsf(h));
+            }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1)
+              amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+            if (lc == 0) red[wave][r] = amax;
+          }
+        }
+      }
+      __syncthreads();
+      uint8_t* h_lds = a_lds[ebuf];
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) {
+        if (mi < nmi) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = mi * 16 + lg * 4 + v;
+            const float amax = fmaxf(fmaxf(red[0][r], red[1][r]),
+                                     fmaxf(red[2][r], red[3][r]));
+            float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+            if (pow2) {
+              const uint32_t bits = __float_as_uint(sc);
+              const int ex = (int)((bits >> 23) & 0xFF) - 127 +
+                             ((bits & 0x7FFFFF) ? 1 : 0);
+              sc = __uint_as_float((uint32_t)(ex + 127) << 23);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              const float y = fminf(fmaxf(acc[mi][s][v] / sc, -448.f), 448.f);
+              h_lds[r * ST_LDS + wave * 32 + s * 16 + lc] = (uint8_t)(
+                  __builtin_amdgcn_cvt_pk_fp8_f32(y, 0.f, 0, false) & 0xFF);
+            }
+            if (wave == 0 && lc == 0 && r < rows)
+              S.hs[(size_t)(rb + r) * ntn + nt] = sc;
+          }
+        }
+      }
+      __syncthreads();
+      if (my_row < rows) {
+        const uint4* p = (const uint4*)(h_lds + my_row * ST_LDS + half * 64);
+        uint4* dst = (uint4*)(S.hq + (size_t)(rb + my_row) * S.N + nt * 128 + half * 64);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[q] = p[q];
+      }
+      __syncthreads();  // h_lds is the next step's A buffer
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) {
+        if (mi < nmi) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = mi * 16 + lg * 4 + v;
+            if (r < rows) {
+              const int pos = rb + r;
+              float w = 1.f;
+              if (S.row_w) w = S.row_w[S.row_w_by_idx ? S.sorted_idx[pos] : pos];
+              uint16_t* dst = S.y + (size_t)pos * S.N + nt * 256 + wave * 64 + lc;
+#pragma unroll
+              for (int s = 0; s < 4; ++s) dst[s * 16] = f32_to_bf16(acc[mi][s][v] * w);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+
+  // ---- one pipeline step ----------------------------------------------------
+  auto step = [&](int st, BSet<BF>& bcur, BSet<BF>& bload) {
+    const int buf = st & 1;
+    {  // A(st) registers -> LDS
+      uint4* p = (uint4*)(a_lds[buf] + my_row * ST_LDS + half * 64);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p[q] = af[q];
+      if (tid < ST_BM) sa_lds[buf][tid] = sa_next;
+    }
+    __syncthreads();
+    if (st + 2 < total_steps) {
+      load_b(bload, bi, bkb);
+      adv(bi, bkb);
+    }
+    if (st + 1 < total_steps) {
+      fetch_a(ai, akb);
+      adv(ai, akb);
+    }
+    // compute step st
+    const int4 d = desc[ci];
+    const int seg = d.x & 1, nt = d.x >> 1;
+    const int nmi = (d.w + 15) >> 4;
+    const SegDesc& S = seg ? S1 : S0;
+    const int KB = S.K / 128;
+    float sbf[2] = {0.f, 0.f};
+    uint32_t sbe[4] = {0, 0, 0, 0};
+    if constexpr (BF == SF_FP4) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sbe[s] = (bcur.sc >> (8 * s)) & 0xFF;
+    } else if constexpr (MODE == 0) {
+      const int ntn = S.N / 128;
+      const size_t o = ((size_t)d.y * ntn + nt) * KB + ckb;
+      sbf[0] = ((const float*)S.s0)[o];
+      sbf[1] = ((const float*)S.s1)[o];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sbe[s] = e8m0_bits(sbf[s >> 1]);
+    } else {
+      const int nblk = (nt * 256 + wave * 64) / 128;
+      sbf[0] = sbf[1] = ((const float*)S.s0)[((size_t)d.y * (S.N / 128) + nblk) * KB + ckb];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sbe[s] = e8m0_bits(sbf[0]);
+    }
+    const uint8_t* lds = a_lds[buf];
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+      if (mi < nmi) {
+        const uint8_t* row = lds + (mi * 16 + lc) * ST_LDS;
+        const uint8_t* p0 = BF == SF_FP4 ? row + lg * 16 : row + lg * 32;
+        const uint8_t* p1 = BF == SF_FP4 ? row + 64 + lg * 16 : row + lg * 32 + 16;
+        const uint4 x0 = *(const uint4*)p0, x1 = *(const uint4*)p1;
+        const v8i a = (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                            (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        if constexpr (BF == SF_FP8_F32S) {
+          const float4 sav = *(const float4*)(sa_lds[buf] + mi * 16 + lg * 4);
+          const float sv[4] = {sav.x, sav.y, sav.z, sav.w};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const f32x4 p = st_mma<BF>(a, bcur.v[s], acc[mi][s], 0, 0);
+            const float sb = MODE == 0 ? sbf[s >> 1] : sbf[0];
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              acc[mi][s][v] = fmaf(p[v], sv[v] * sb, acc[mi][s][v]);
+          }
+        } else {
+          const uint32_t sae = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            acc[mi][s] = st_mma<BF>(a, bcur.v[s], acc[mi][s], sae, sbe[s]);
+        }
+      }
+    }
+    const bool last = ckb + 1 == KB;
+    const int cur_item = ci;
+    adv(ci, ckb);
+    if (last) epilogue(cur_item, buf ^ 1);
+  };
+
+  // ---- pipeline -------------------------------------------------------------
+  BSet<BF> b0, b1, b2;
+  load_b(b0, bi, bkb);
+  adv(bi, bkb);
+  if (total_steps > 1) {
+    load_b(b1, bi, bkb);
+    adv(bi, bkb);
+  }
+  fetch_a(ai, akb);
+  adv(ai, akb);
+  for (int st = 0; st < total_steps; st += 3) {
+    step(st, b0, b2);
+    if (st + 1 < total_steps) step(st + 1, b1, b0);
+    if (st + 2 < total_steps) step(st + 2, b2, b1);
+  }
+}
+
+static int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+// upper_items: an upper bound of the total item count (sizes the grid so
+// that no workgroup receives more than ST_MAX_ITEMS items).
+template <int BF, int MODE>
+static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
+                     float limit, int pow2, long upper_items, hipStream_t st) {
+  const long need = (upper_items + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
+  const long grid = need > num_cus() ? need : num_cus();
+  SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
+  SegDesc dummy = s0;
+  moe_stream_kernel<BF, MODE><<<(unsigned)grid, 256, 0, st>>>(
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
+                  int topk, float limit, int pow2, long upper_items,
+                  hipStream_t st) {
+  SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1),
+               "stream gemm: bad format");
+  const int ntw = mode == 0 ? 128 : 256;
+  for (const SegDesc* s : {&s0, s1}) {
+    if (!s) continue;
+    SLLM_REQUIRE(s->a && s->sa && s->wp && s->s0 && s->N % ntw == 0 &&
+                     s->K % 128 == 0 && s->K > 0,
+                 "stream gemm: bad segment (N=%d K=%d)", s->N, s->K);
+    SLLM_REQUIRE(mode == 1 ? s->y != nullptr : (s->hq && s->hs),
+                 "stream gemm: missing outputs");
+    SLLM_REQUIRE(bf == SF_FP4 || mode == 1 || s->s1,
+                 "stream gemm: missing W3 scales");
+    SLLM_REQUIRE((!s->gather && !s->row_w_by_idx) || s->sorted_idx,
+                 "stream gemm: gather / row_w_by_idx need sorted_idx");
+  }
+#define GO(B, M)                                                              \
+  return go_stream<B, M>(s0, s1, topk, limit, pow2, upper_items, st)
+  if (mode == 0) {
+    if (bf == SF_FP8_F32S) GO(SF_FP8_F32S, 0);
+    if (bf == SF_FP8_POW2) GO(SF_FP8_POW2, 0);
+    GO(SF_FP4, 0);
+  } else {
+    if (bf == SF_FP8_F32S) GO(SF_FP8_F32S, 1);
+    if (bf == SF_FP8_POW2) GO(SF_FP8_POW2, 1);
+    GO(SF_FP4, 1);
+  }
+#undef GO
+}
+
+long packed_bytes(int fp4, int up, int E, int N, int K) {
+  const long NT = up ? N / 128 : N / 256, KB = K / 128;
+  return (long)E * NT * KB * (fp4 ? 16384 : 32768);
+}
+
+long packed_scale_bytes(int up, int E, int N, int K) {
+  const long NT = up ? N / 128 : N / 256, KB = K / 128;
+  return (long)E * NT * KB * 1024;
+}
+
+}  // namespace sllm
+
+using namespace sllm;
+
+extern "C" {
+
+// Size in bytes of the packed weight (and, for fp4, of the packed scales).
+long sllm_moe_packed_bytes(int fp4, int up, int E, int N, int K) {
+  if (E <= 0 || N <= 0 || K <= 0 || K % 128 || N % (up ? 128 : 256)) {
+    set_error("sllm_moe_packed_bytes: need K %% 128 == 0 and N %% %d == 0",
+              up ? 128 : 256);
+    return -1;
+  }
+  return packed_bytes(fp4, up, E, N, K);
+}
+
+long sllm_moe_packed_scale_bytes(int up, int E, int N, int K) {
+  if (E <= 0 || N <= 0 || K <= 0 || K % 128 || N % (up ? 128 : 256)) {
+    set_error("sllm_moe_packed_scale_bytes: bad shape");
+    return -1;
+  }
+  return packed_scale_bytes(up, E, N, K);
+}
+
+// Repacks expert weights into the streaming layout. fp8: w0 (and w1 for the
+// gate/up pair) are (E, N, K) e4m3; fp4: (E, N, K/2) packed e2m1 with e8m0
+// scales s0/s1 (E, N, K/32), packed scales to out_scales.
+int sllm_moe_pack_weights(int fp4, int up, const void* w0, const void* w1,
+                          const void* s0, const void* s1, int E, int N, int K,
+                          void* out, void* out_scales, void* stream) {
+  SLLM_REQUIRE(w0 && out && (!up || w1), "sllm_moe_pack_weights: null pointer");
+  SLLM_REQUIRE(!fp4 || (s0 && out_scales && (!up || s1)),
+               "sllm_moe_pack_weights: fp4 needs scales");
+  if (sllm_moe_packed_bytes(fp4, up, E, N, K) < 0) return -1;
+  const long n = packed_bytes(fp4, up, E, N, K) / 16;
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  if (fp4)
+    pack_fp4_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+        (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)s0,
+        (const uint8_t*)s1, (uint8_t*)out, (uint32_t*)out_scales, E, N, K, up);
+  else
+    pack_fp8_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+        (const uint8_t*)w0, (const uint8_t*)w1, (uint8_t*)out, E, N, K, up);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+}  // extern "C"

@@ -46,6 +46,35 @@ int launch_gemm2_mx(int b_fp4, const uint8_t* hq, const float* hs,
                     const int* tile_info, const int* num_tiles, int max_tiles,
                     const int* offsets, const uint8_t* w2, const void* w2_s,
                     int I, int H, uint16_t* y, hipStream_t st);
+// Persistent weight-streaming grouped GEMM over packed weights
+// (gemm_stream.hip). bf: 0 fp8 + fp32 scales, 1 fp8 + power-of-two scales,
+// 2 MXFP4; mode 0: gate/up + SwiGLU + e4m3 re-quant, 1: down -> bf16 rows.
+struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
+  const uint8_t* a;        // A rows (row stride K bytes)
+  const float* sa;         // A scales (row stride K / 128)
+  const int* sorted_idx;   // flat assignment index of permuted row p
+  int gather;              // 1: A row of permuted row p is sorted_idx[p] / topk
+  const int* tile_info;    // int4 per tile: expert, first row, rows, 0;
+                           // null: identity rows [0, total_rows)
+  const int* num_tiles;
+  int total_rows;
+  const uint8_t* wp;       // packed weights
+  const void* s0;          // fp8: fp32 scales of W1 / W2 (reference layout);
+                           // fp4: packed e8m0 scales
+  const void* s1;          // fp8 gate/up: fp32 scales of W3
+  int N, K;
+  const float* row_w;      // optional per-row weight (see row_w_by_idx)
+  int row_w_by_idx;        // 1: row_w[sorted_idx[p]], 0: row_w[p]
+  uint8_t* hq;             // mode 0 outputs at permuted row p
+  float* hs;
+  uint16_t* y;             // mode 1 output at permuted row p
+};
+int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
+                  int topk, float limit, int pow2, long upper_items,
+                  hipStream_t st);
+long packed_bytes(int fp4, int up, int E, int N, int K);
+long packed_scale_bytes(int up, int E, int N, int K);
+
 int launch_gemv(int wf, int swiglu, const void* act, int act_bf16,
                 int gather_tokens, const int* sorted_idx, int topk,
                 int total_rows, const int* tile_info, const int* num_tiles,

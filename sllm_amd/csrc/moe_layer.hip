@@ -62,7 +62,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.offsets = take(c, (size_t)(E + 1) * 4);
   p.sorted = take(c, (size_t)p.N * 4);
   p.inv = take(c, (size_t)p.N * 4);
-  p.tiles = take(c, (size_t)p.max_tiles * 8);
+  p.tiles = take(c, (size_t)p.max_tiles * 16);
   p.ntiles = take(c, 4);
   p.pscr = take(c, permute_scratch_bytes(p.N, E));
   p.gate = take(c, (size_t)T * 4);
@@ -247,29 +247,64 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
           launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
           sh ? (const uint16_t*)a->sgl : nullptr, gate, st));
-    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-          launch_gemm1_fp8(xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-          offsets, (const uint8_t*)a->wg, a->wg_s,
-          (const uint8_t*)a->wu, a->wu_s, I, H, nullptr, 0.f, 0,
-          hq, hs, st));
-    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-          launch_gemm2_fp8(hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-          offsets, (const uint8_t*)a->wd, a->wd_s, I, H, w, y,
-          st));
     uint16_t* y_sh = nullptr;
+    uint8_t* hq_sh = nullptr;
+    float* hs_sh = nullptr;
     if (sh) {
-      uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
-      float* hs_sh = (float*)(ws + p.hs_sh);
+      hq_sh = (uint8_t*)(ws + p.hq_sh);
+      hs_sh = (float*)(ws + p.hs_sh);
       y_sh = (uint16_t*)(ws + p.y_sh);
-      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
-            launch_gemm1_fp8(xq, sx, nullptr, k, T, nullptr, nullptr, 0, nullptr,
-            (const uint8_t*)a->sg, a->sg_s,
-            (const uint8_t*)a->su, a->su_s, Is, H, nullptr, 0.f,
-            0, hq_sh, hs_sh, st));
-      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
-            launch_gemm2_fp8(hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
-            nullptr, (const uint8_t*)a->sd, a->sd_s, Is, H, gate,
-            y_sh, st));
+    }
+    if (a->wgu_packed) {
+      SLLM_REQUIRE(a->wd_packed && (!sh || (a->sgu_packed && a->sd_packed)),
+                   "sllm_moe_qwen_forward: packed weights incomplete");
+      const long sh_rt = sh ? (T + 127) / 128 : 0;
+      SegDesc r1{}, s1{};
+      r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
+      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
+      r1.N = I; r1.K = H; r1.hq = hq; r1.hs = hs;
+      s1.a = xq; s1.sa = sx; s1.total_rows = T;
+      s1.wp = (const uint8_t*)a->sgu_packed; s1.s0 = a->sg_s; s1.s1 = a->su_s;
+      s1.N = Is; s1.K = H; s1.hq = hq_sh; s1.hs = hs_sh;
+      const long up1 = (long)p.max_tiles * (I / 128) + sh_rt * (Is / 128);
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+            launch_stream(0, 0, r1, sh ? &s1 : nullptr, k, 0.f, 0, up1, st));
+      SegDesc r2{}, s2{};
+      r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
+      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
+      r2.row_w = w; r2.row_w_by_idx = 1; r2.y = y;
+      s2.a = hq_sh; s2.sa = hs_sh; s2.total_rows = T;
+      s2.wp = (const uint8_t*)a->sd_packed; s2.s0 = a->sd_s; s2.N = H;
+      s2.K = Is; s2.row_w = gate; s2.y = y_sh;
+      const long up2 = (long)p.max_tiles * (H / 256) + sh_rt * (H / 256);
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+            launch_stream(0, 1, r2, sh ? &s2 : nullptr, k, 0.f, 0, up2, st));
+      // the shared expert ran inside the two launches above
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
+    } else {
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+            launch_gemm1_fp8(xq, sx, sorted, k, p.N, tiles, ntiles,
+                             p.max_tiles, offsets, (const uint8_t*)a->wg,
+                             a->wg_s, (const uint8_t*)a->wu, a->wu_s, I, H,
+                             nullptr, 0.f, 0, hq, hs, st));
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+            launch_gemm2_fp8(hq, hs, sorted, k, p.N, tiles, ntiles,
+                             p.max_tiles, offsets, (const uint8_t*)a->wd,
+                             a->wd_s, I, H, w, y, st));
+      if (sh) {
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+              launch_gemm1_fp8(xq, sx, nullptr, k, T, nullptr, nullptr, 0,
+                               nullptr, (const uint8_t*)a->sg, a->sg_s,
+                               (const uint8_t*)a->su, a->su_s, Is, H, nullptr,
+                               0.f, 0, hq_sh, hs_sh, st));
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+              launch_gemm2_fp8(hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr,
+                               0, nullptr, (const uint8_t*)a->sd, a->sd_s, Is,
+                               H, gate, y_sh, st));
+      }
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
@@ -368,27 +403,73 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
           launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx, nullptr,
           nullptr, st));
-    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-          launch_gemm1_mx(1, xq, sx, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-          offsets, (const uint8_t*)a->w1, a->w1_s,
-          (const uint8_t*)a->w3, a->w3_s, I, H, w, L, hq, hs, st));
-    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-          launch_gemm2_mx(1, hq, hs, sorted, k, p.N, tiles, ntiles, p.max_tiles,
-          offsets, (const uint8_t*)a->w2, a->w2_s, I, H, y, st));
     uint16_t* y_sh = nullptr;
+    uint8_t* hq_sh = nullptr;
+    float* hs_sh = nullptr;
     if (sh) {
-      uint8_t* hq_sh = (uint8_t*)(ws + p.hq_sh);
-      float* hs_sh = (float*)(ws + p.hs_sh);
+      hq_sh = (uint8_t*)(ws + p.hq_sh);
+      hs_sh = (float*)(ws + p.hs_sh);
       y_sh = (uint16_t*)(ws + p.y_sh);
-      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
-            launch_gemm1_mx(0, xq, sx, nullptr, k, T, nullptr, nullptr, 0,
-            nullptr, (const uint8_t*)a->s1, a->s1_s,
-            (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr, L,
-            hq_sh, hs_sh, st));
-      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
-            launch_gemm2_mx(0, hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr, 0,
-            nullptr, (const uint8_t*)a->s2, a->s2_s, Is, H, y_sh,
-            st));
+    }
+    if (a->w13_packed) {
+      SLLM_REQUIRE(a->w13_s_packed && a->w2_packed && a->w2_s_packed &&
+                       (!sh || (a->s13_packed && a->s2_packed)),
+                   "sllm_moe_ds_forward: packed weights incomplete");
+      const long sh_rt = (T + 127) / 128;
+      SegDesc r1{};
+      r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
+      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
+      r1.N = I; r1.K = H; r1.row_w = w; r1.row_w_by_idx = 1;
+      r1.hq = hq; r1.hs = hs;
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+            launch_stream(2, 0, r1, nullptr, k, L, 1,
+                          (long)p.max_tiles * (I / 128), st));
+      SegDesc r2{};
+      r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
+      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
+      r2.N = H; r2.K = I; r2.y = y;
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+            launch_stream(2, 1, r2, nullptr, k, 0.f, 1,
+                          (long)p.max_tiles * (H / 256), st));
+      if (sh) {
+        SegDesc s1{};
+        s1.a = xq; s1.sa = sx; s1.total_rows = T;
+        s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
+        s1.N = Is; s1.K = H; s1.hq = hq_sh; s1.hs = hs_sh;
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+              launch_stream(1, 0, s1, nullptr, k, L, 1, sh_rt * (Is / 128),
+                            st));
+        SegDesc s2{};
+        s2.a = hq_sh; s2.sa = hs_sh; s2.total_rows = T;
+        s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
+        s2.N = H; s2.K = Is; s2.y = y_sh;
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+              launch_stream(1, 1, s2, nullptr, k, 0.f, 1, sh_rt * (H / 256),
+                            st));
+      }
+    } else {
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+            launch_gemm1_mx(1, xq, sx, sorted, k, p.N, tiles, ntiles,
+                            p.max_tiles, offsets, (const uint8_t*)a->w1,
+                            a->w1_s, (const uint8_t*)a->w3, a->w3_s, I, H, w,
+                            L, hq, hs, st));
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+            launch_gemm2_mx(1, hq, hs, sorted, k, p.N, tiles, ntiles,
+                            p.max_tiles, offsets, (const uint8_t*)a->w2,
+                            a->w2_s, I, H, y, st));
+      if (sh) {
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+              launch_gemm1_mx(0, xq, sx, nullptr, k, T, nullptr, nullptr, 0,
+                              nullptr, (const uint8_t*)a->s1, a->s1_s,
+                              (const uint8_t*)a->s3, a->s3_s, Is, H, nullptr,
+                              L, hq_sh, hs_sh, st));
+        STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+              launch_gemm2_mx(0, hq_sh, hs_sh, nullptr, k, T, nullptr, nullptr,
+                              0, nullptr, (const uint8_t*)a->s2, a->s2_s, Is,
+                              H, y_sh, st));
+      }
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));

@@ -15,7 +15,8 @@
 //  1. hist:    chunks of PERM_CHUNK assignments, LDS histogram per chunk.
 //  2. scan:    one workgroup; per-expert exclusive scan over chunks, then an
 //              exclusive scan over experts (offsets), chunk bases, and the
-//              tile table {expert, first row} of ceil(count/bm) tiles/expert.
+//              tile table: ceil(count/bm) tiles per expert, each an int4
+//              {expert, first permuted row, rows, 0}.
 //  3. scatter: one wave per chunk walks its assignments in order, 64 at a
 //              time; lanes holding the same expert are matched with one
 //              ballot per id bit, so the rank among equal ids is the popcount
@@ -90,8 +91,9 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
       offsets[e] = off;
       for (int c = 0; c < nchunks; ++c) chunk_hist[(size_t)c * E + e] += off;
       for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
-        tile_info[2 * (toff + i)] = e;
-        tile_info[2 * (toff + i) + 1] = i * bm;
+        const int r0 = i * bm;
+        *(int4*)(tile_info + 4 * (toff + i)) =
+            make_int4(e, off + r0, min(bm, cnt - r0), 0);
       }
     }
     __syncthreads();
@@ -147,7 +149,7 @@ size_t permute_scratch_bytes(int N, int E) {
 }
 
 // ids (N = T*k) int32 -> counts[E], offsets[E+1], sorted_idx[N], inv_pos[N],
-// tile_info[2*max_tiles] {expert, first row}, num_tiles[1].
+// tile_info[4*max_tiles] {expert, first row, rows, 0}, num_tiles[1].
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,
                    int* tile_info, int* num_tiles, int max_tiles,

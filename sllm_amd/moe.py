@@ -64,7 +64,8 @@ def _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
     w = weights
     a.router_w = ptr(w.get("router_w"))
     for k in ("wg", "wg_s", "wu", "wu_s", "wd", "wd_s", "sg", "sg_s", "su",
-              "su_s", "sd", "sd_s", "sgl"):
+              "su_s", "sd", "sd_s", "sgl", "wgu_packed", "wd_packed",
+              "sgu_packed", "sd_packed"):
         setattr(a, k, ptr(w.get(k)))
     a.out = ptr(out)
     debug = debug or {}
@@ -129,7 +130,9 @@ def _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
     a.logits = ptr(logits)
     w = weights
     for k in ("router_w", "bias", "w1", "w1_s", "w3", "w3_s", "w2", "w2_s",
-              "s1", "s1_s", "s3", "s3_s", "s2", "s2_s"):
+              "s1", "s1_s", "s3", "s3_s", "s2", "s2_s", "w13_packed",
+              "w13_s_packed", "w2_packed", "w2_s_packed", "s13_packed",
+              "s2_packed"):
         setattr(a, k, ptr(w.get(k)))
     a.out = ptr(out)
     debug = debug or {}
@@ -175,6 +178,29 @@ def deepseek_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
 
 
 # ---------------------------------------------------------------------------
+# weight packing (streaming layout of the prefill GEMMs)
+# ---------------------------------------------------------------------------
+
+def pack_weights(fp4, up, w0, w1, E, N, K, s0=None, s1=None, stream=None):
+    """Repack device weights into the streaming layout; returns
+    (packed DeviceBuffer, packed-scales DeviceBuffer or None)."""
+    L = _lib.lib()
+    nb = L.sllm_moe_packed_bytes(int(fp4), int(up), E, N, K)
+    if nb < 0:
+        raise RuntimeError(_lib.last_error())
+    out = DeviceBuffer(int(nb))
+    outs = None
+    if fp4:
+        ns = L.sllm_moe_packed_scale_bytes(int(up), E, N, K)
+        outs = DeviceBuffer(int(ns))
+    _lib.check(L.sllm_moe_pack_weights(int(fp4), int(up), ptr(w0), ptr(w1),
+                                       ptr(s0), ptr(s1), E, N, K, ptr(out),
+                                       ptr(outs), stream_handle(stream)),
+               "sllm_moe_pack_weights")
+    return out, outs
+
+
+# ---------------------------------------------------------------------------
 # device-resident layers with numpy in / out
 # ---------------------------------------------------------------------------
 
@@ -204,7 +230,7 @@ class QwenMoE:
 
     def __init__(self, router_w, wg, wu, wd, wg_s=None, wu_s=None, wd_s=None,
                  sg=None, su=None, sd=None, sg_s=None, su_s=None, sd_s=None,
-                 sgl=None, top_k=8, eps=1e-20):
+                 sgl=None, top_k=8, eps=1e-20, packed=True):
         self.wdtype = 0 if wg_s is not None else 1
         self.E, self.I, self.H = np.asarray(wg).shape
         self.Is = 0 if su is None else np.asarray(su).shape[0]
@@ -225,6 +251,13 @@ class QwenMoE:
                 b.update(sg_s=_up(np.asarray(sg_s, np.float32)),
                          su_s=_up(np.asarray(su_s, np.float32)),
                          sd_s=_up(np.asarray(sd_s, np.float32)))
+        if packed and self.wdtype == 0:
+            E, I, H, Is = self.E, self.I, self.H, self.Is
+            b["wgu_packed"], _ = pack_weights(0, 1, b["wg"], b["wu"], E, I, H)
+            b["wd_packed"], _ = pack_weights(0, 0, b["wd"], None, E, H, I)
+            if su is not None:
+                b["sgu_packed"], _ = pack_weights(0, 1, b["sg"], b["su"], 1, Is, H)
+                b["sd_packed"], _ = pack_weights(0, 0, b["sd"], None, 1, H, Is)
         self._w = b
         self._ws = None
 
@@ -271,7 +304,7 @@ class DeepseekMoE:
     def __init__(self, router_w, bias, w1, w1_s, w3, w3_s, w2, w2_s, s1=None,
                  s1_s=None, s3=None, s3_s=None, s2=None, s2_s=None, top_k=8,
                  n_group=1, topk_group=1, scoring="sigmoid", route_scale=1.0,
-                 swiglu_limit=0.0):
+                 swiglu_limit=0.0, packed=True):
         self.E, self.I = np.asarray(w1).shape[:2]
         self.H = np.asarray(w2).shape[1]
         self.Is = 0 if s1 is None else np.asarray(s1).shape[0]
@@ -288,6 +321,15 @@ class DeepseekMoE:
                 b[k] = _up(np.ascontiguousarray(v, np.uint8))
             for k, v in (("s1_s", s1_s), ("s3_s", s3_s), ("s2_s", s2_s)):
                 b[k] = _up(np.asarray(v, np.float32))
+        if packed:
+            E, I, H, Is = self.E, self.I, self.H, self.Is
+            b["w13_packed"], b["w13_s_packed"] = pack_weights(
+                1, 1, b["w1"], b["w3"], E, I, H, b["w1_s"], b["w3_s"])
+            b["w2_packed"], b["w2_s_packed"] = pack_weights(
+                1, 0, b["w2"], None, E, H, I, b["w2_s"])
+            if s1 is not None:
+                b["s13_packed"], _ = pack_weights(0, 1, b["s1"], b["s3"], 1, Is, H)
+                b["s2_packed"], _ = pack_weights(0, 0, b["s2"], None, 1, H, Is)
         self._w = b
         self._ws = None
 

@@ -125,9 +125,9 @@ def deepseek_mxfp4_gpu(seed=0, T=64, H=7168, E=32, I=2048, Is=2048, shared=True)
     return x, W
 
 
-def qwen_layer(W, top_k):
+def qwen_layer(W, top_k, packed=True):
     from sllm_amd.moe import QwenMoE
-    kw = {}
+    kw = {"packed": packed}
     if W.has_shared:
         kw = dict(sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
                   sd_s=W.sd_s, sgl=W.sgl)
@@ -162,9 +162,9 @@ def deepseek_mxfp4(seed=0, T=64, H=512, E=16, I=256, Is=256, shared=True):
     return x, W
 
 
-def deepseek_layer(W, top_k, **route):
+def deepseek_layer(W, top_k, packed=True, **route):
     from sllm_amd.moe import DeepseekMoE
-    kw = {}
+    kw = {"packed": packed}
     if W.has_shared:
         kw = dict(s1=W.s1_q, s1_s=W.s1_s, s3=W.s3_q, s3_s=W.s3_s, s2=W.s2_q,
                   s2_s=W.s2_s)

@@ -211,7 +211,7 @@ def _run_permute(L, ids, E, bm):
     max_tiles = -(-N // bm) + min(E, N)
     bufs = dict(counts=empty(E * 4), offsets=empty((E + 1) * 4),
                 sorted=empty(N * 4), inv=empty(N * 4),
-                tiles=empty(max_tiles * 8), nt=empty(4))
+                tiles=empty(max_tiles * 16), nt=empty(4))
     scr = empty(L.lib().sllm_moe_permute_scratch_bytes(N, E))
     L.check(L.lib().sllm_moe_permute(dev(ids.astype(np.int32)).ptr, N, E, bm,
                                      bufs["counts"].ptr, bufs["offsets"].ptr,
@@ -224,7 +224,7 @@ def _run_permute(L, ids, E, bm):
                 offsets=host(bufs["offsets"], np.int32, (E + 1,)),
                 sorted_idx=host(bufs["sorted"], np.int32, (N,)),
                 inv_pos=host(bufs["inv"], np.int32, (N,)),
-                tiles=host(bufs["tiles"], np.int32, (max_tiles, 2))[:nt])
+                tiles=host(bufs["tiles"], np.int32, (max_tiles, 4))[:nt])
 
 
 @pytest.mark.parametrize("T,E,k,skew", [(4096, 512, 10, False), (16384, 512, 10, True),
@@ -244,9 +244,12 @@ def test_permute_bit_exact(L, T, E, k, skew):
     want = oracle_permute(ids, E)
     for key in ("counts", "offsets", "sorted_idx", "inv_pos"):
         np.testing.assert_array_equal(got[key], want[key], err_msg=key)
-    # tile table: every non-empty expert in order, ceil(count/128) tiles
-    exp_tiles = [(e, r) for e in range(E) for r in range(0, want["counts"][e], 128)]
-    np.testing.assert_array_equal(got["tiles"], np.array(exp_tiles, np.int32).reshape(-1, 2))
+    # tile table: every non-empty expert in order, ceil(count/128) tiles of
+    # {expert, first permuted row, rows, 0}
+    c, o = want["counts"], want["offsets"]
+    exp_tiles = [(e, o[e] + r, min(128, c[e] - r), 0)
+                 for e in range(E) for r in range(0, c[e], 128)]
+    np.testing.assert_array_equal(got["tiles"], np.array(exp_tiles, np.int32).reshape(-1, 4))
 
 
 def test_fill_normal_deterministic_and_normal(L):
@@ -259,3 +262,78 @@ def test_fill_normal_deterministic_and_normal(L):
     np.testing.assert_array_equal(x, host(b, np.float32, (n,)))
     assert abs(x.mean()) < 0.01 and abs(x.std() - 2.0) < 0.01
     assert abs((np.abs(x) < 2.0).mean() - 0.6827) < 0.003
+
+
+def _np_pack_fp8(w0, w1, up):
+    """numpy statement of the fp8 streaming layout (gemm_stream.hip)."""
+    E, N, K = w0.shape
+    NT, KB = (N // 128 if up else N // 256), K // 128
+    out = np.empty(E * NT * KB * 32768, np.uint8)
+    c = np.arange(out.size // 16)
+    l, h, s, w = c & 63, (c >> 6) & 1, (c >> 7) & 3, (c >> 9) & 3
+    blk = c >> 11
+    kb, t = blk % KB, blk // KB
+    nt, e = t % NT, t // NT
+    row = (nt * 128 + w * 32 + (s & 1) * 16 + (l & 15)) if up else \
+        (nt * 256 + w * 64 + s * 16 + (l & 15))
+    col = kb * 128 + (l >> 4) * 32 + h * 16
+    src = np.where((s >= 2) & bool(up), 1, 0)
+    both = np.stack([w0, w1 if w1 is not None else w0])
+    for b in range(16):
+        out[c * 16 + b] = both[src, e, row, col + b]
+    return out
+
+
+def _np_pack_fp4(w0, w1, s0, s1, up):
+    E, N, Kh = w0.shape
+    K = Kh * 2
+    NT, KB = (N // 128 if up else N // 256), K // 128
+    out = np.empty(E * NT * KB * 16384, np.uint8)
+    outs = np.empty(E * NT * KB * 256, np.uint32)
+    c = np.arange(out.size // 16)
+    l, s, w = c & 63, (c >> 6) & 3, (c >> 8) & 3
+    blk = c >> 10
+    kb, t = blk % KB, blk // KB
+    nt, e = t % NT, t // NT
+
+    def rowf(sv):
+        return (nt * 128 + w * 32 + (sv & 1) * 16 + (l & 15)) if up else \
+            (nt * 256 + w * 64 + sv * 16 + (l & 15))
+    row = rowf(s)
+    col = kb * 64 + (l >> 4) * 16
+    src = np.where((s >= 2) & bool(up), 1, 0)
+    both = np.stack([w0, w1 if w1 is not None else w0])
+    sboth = np.stack([s0, s1 if s1 is not None else s0])
+    for b in range(16):
+        out[c * 16 + b] = both[src, e, row, col + b]
+    sel = s == 0
+    v = np.zeros(sel.sum(), np.uint32)
+    for q in range(4):
+        rq = rowf(np.full_like(s, q))[sel]
+        sq = np.where((q >= 2) & bool(up), 1, 0)
+        v |= sboth[sq, e[sel], rq, kb[sel] * 4 + (l[sel] >> 4)].astype(np.uint32) << (8 * q)
+    outs[blk[sel] * 256 + w[sel] * 64 + l[sel]] = v
+    return out, outs
+
+
+@pytest.mark.parametrize("up", [1, 0])
+def test_pack_weights_layout(L, up):
+    from sllm_amd.moe import pack_weights
+    rng = np.random.default_rng(11 + up)
+    E, N, K = 3, 256, 384
+    w0 = rng.integers(0, 256, (E, N, K), dtype=np.uint8)
+    w1 = rng.integers(0, 256, (E, N, K), dtype=np.uint8) if up else None
+    d0, d1 = dev(w0), (dev(w1) if up else None)
+    p, _ = pack_weights(0, up, d0, d1, E, N, K)
+    _KEEP.append(p)
+    np.testing.assert_array_equal(host(p, np.uint8, (p.nbytes,)), _np_pack_fp8(w0, w1, up))
+    f0 = rng.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    f1 = rng.integers(0, 256, (E, N, K // 2), dtype=np.uint8) if up else None
+    s0 = rng.integers(0, 256, (E, N, K // 32), dtype=np.uint8)
+    s1 = rng.integers(0, 256, (E, N, K // 32), dtype=np.uint8) if up else None
+    p4, ps = pack_weights(1, up, dev(f0), dev(f1) if up else None, E, N, K,
+                          dev(s0), dev(s1) if up else None)
+    _KEEP.extend([p4, ps])
+    want, wants = _np_pack_fp4(f0, f1, s0, s1, up)
+    np.testing.assert_array_equal(host(p4, np.uint8, (p4.nbytes,)), want)
+    np.testing.assert_array_equal(host(ps, np.uint32, (ps.nbytes // 4,)), wants)

@@ -48,11 +48,12 @@ def _report(name, got, want):
     return rel, mabs, scale
 
 
+@pytest.mark.parametrize("packed", [True, False])
 @pytest.mark.parametrize("T,E,k,shared", [(256, 8, 2, True), (130, 16, 4, False),
                                           (512, 64, 6, True)])
-def test_qwen_prefill_small(T, E, k, shared):
+def test_qwen_prefill_small(T, E, k, shared, packed):
     x, W = qwen_fp8(seed=T, T=T, H=512, E=E, I=256, Is=256, shared=shared)
-    layer = qwen_layer(W, k)
+    layer = qwen_layer(W, k, packed=packed)
     y, r = layer.forward(x, mode="prefill", return_routing=True)
     _check_routing(r, E, k)
     want = qm.moe_layer_fp8(x, r["logits"], W, k)
@@ -138,12 +139,13 @@ def test_qwen_skewed_with_empty_experts():
     assert rel < 3e-3
 
 
+@pytest.mark.parametrize("packed", [True, False])
 @pytest.mark.parametrize("T,G,kg,L", [(200, 4, 2, 10.0), (256, 1, 1, 0.0)])
-def test_deepseek_prefill_small(T, G, kg, L):
+def test_deepseek_prefill_small(T, G, kg, L, packed):
     x, W = deepseek_mxfp4(seed=T, T=T, H=512, E=16, I=256, Is=256)
     route = dict(n_group=G, topk_group=kg, scoring="sigmoid", route_scale=2.5,
                  swiglu_limit=L)
-    layer = deepseek_layer(W, 4, **route)
+    layer = deepseek_layer(W, 4, packed=packed, **route)
     y, r = layer.forward(x, mode="prefill", return_routing=True)
     w_ref, ids_ref = dm.moe_route(r["logits"], W.bias, 4, "sigmoid", 2.5, G, kg)
     np.testing.assert_array_equal(r["ids"], ids_ref.astype(np.int32))
