@@ -15,8 +15,10 @@
 //   items first, then the shared expert's) and walks the flat sequence of
 //   (item, K step); the weight operands of step s+2 are in flight while
 //   step s computes, across item boundaries, so the weight stream does not
-//   drain between tiles. The activation tile of step s+1 is fetched into
-//   registers during step s and double-buffered in LDS.
+//   drain between tiles. The gathered activation tile of step s+2 is
+//   fetched into registers during step s as well and double-buffered in LDS
+//   (it comes from L2 / the Infinity Cache, whose latency under this load is
+//   microseconds, so one step of lead is not enough).
 // * Item descriptors and gathered row indices for the whole run are loaded
 //   into LDS once at the start.
 #include "launch.h"
@@ -110,10 +112,16 @@ __global__ void pack_fp4_kernel(const uint8_t* __restrict__ w0,
 // ---------------------------------------------------------------------------
 
 
+// Weight operands of one K step plus their scales (prefetched together so
+// that nothing loaded for the current step is issued after the prefetches:
+// vmcnt counts loads and stores in order on gfx9, so a late load would make
+// the wait for it drain every prefetch behind it).
 template <int BF>
 struct BSet {
   v8i v[4];
-  uint32_t sc;
+  uint32_t sc;   // fp4: packed e8m0 scale bytes of the 4 subtiles
+  float sb0;     // fp8: W1 / W2 block scale
+  float sb1;     // fp8 gate/up: W3 block scale
 };
 
 template <int MODE>
@@ -153,11 +161,14 @@ struct Stream {
 template <int BF, int MODE>
 __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, int pow2) {
+  constexpr int YS = 264;  // bf16 row stride of the down-projection staging
   __shared__ int4 desc[ST_MAX_ITEMS];
   __shared__ int rsrc[ST_MAX_ITEMS][ST_BM];
+  __shared__ float rwl[ST_MAX_ITEMS][ST_BM];
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][ST_BM * ST_LDS];
   __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM];
   __shared__ float red[4][ST_BM];
+  __shared__ __attribute__((aligned(16))) uint16_t ystage[MODE == 1 ? ST_BM * YS : 8];
 
   constexpr int NTW = Stream<BF, MODE>::NTW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -198,8 +209,14 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
     int src = 0;
-    if (r < d.w) src = S.gather ? S.sorted_idx[d.z + r] / topk : d.z + r;
+    float rw = 1.f;
+    if (r < d.w) {
+      const int p = d.z + r;
+      src = S.gather ? S.sorted_idx[p] / topk : p;
+      if (S.row_w) rw = S.row_w[S.row_w_by_idx ? S.sorted_idx[p] : p];
+    }
     rsrc[i][r] = src;
+    rwl[i][r] = rw;
   }
   __syncthreads();
 
@@ -227,6 +244,7 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       }
       const uint32_t* sp = (const uint32_t*)(seg ? S1.s0 : S0.s0);
       b.sc = sp[blk * 256 + wave * 64 + lane];
+      b.sb0 = b.sb1 = 0.f;
     } else {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -236,25 +254,42 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
       b.sc = 0;
+      const float* s0p = (const float*)(seg ? S1.s0 : S0.s0);
+      if constexpr (MODE == 0) {
+        const float* s1p = (const float*)(seg ? S1.s1 : S0.s1);
+        const size_t o = ((size_t)d.y * NT + nt) * KB + kb;  // NT = N / 128
+        b.sb0 = s0p[o];
+        b.sb1 = s1p[o];
+      } else {
+        const int nblk = (nt * 256 + wave * 64) / 128;
+        b.sb0 = b.sb1 = s0p[((size_t)d.y * (N / 128) + nblk) * KB + kb];
+      }
     }
   };
 
   const int my_row = tid >> 1, half = tid & 1;
-  uint4 af[4];
-  float sa_next = 0.f;
-  auto fetch_a = [&](int i, int kb) {
+  struct ASet {
+    uint4 v[4];
+    float s;
+  };
+  // Every prefetch load is issued unconditionally (rows past the tile read
+  // the valid row 0 of rsrc and are zeroed by a select): a load under a
+  // branch would leave the compiler no guaranteed count of younger loads and
+  // force a vmcnt(0) wait that drains the pipeline.
+  auto fetch_a = [&](ASet& af, int i, int kb) {
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
     const int K = S.K, KB = K / 128;
-    if (my_row < d.w) {
-      const uint4* p = (const uint4*)(S.a + (size_t)rsrc[i][my_row] * K + kb * 128 + half * 64);
+    const uint4* p = (const uint4*)(S.a + (size_t)rsrc[i][my_row] * K + kb * 128 + half * 64);
+    const bool ok = my_row < d.w;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) af[q] = p[q];
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) af[q] = make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = p[q];
+      af.v[q] = ok ? v : make_uint4(0, 0, 0, 0);
     }
-    if (tid < ST_BM) sa_next = tid < d.w ? S.sa[(size_t)rsrc[i][tid] * KB + kb] : 0.f;
+    const int sr = tid & (ST_BM - 1);
+    const float sv = S.sa[(size_t)rsrc[i][sr] * KB + kb];
+    af.s = sr < d.w ? sv : 0.f;
   };
 
   f32x4 acc[8][4];
@@ -267,6 +302,16 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   int ci = 0, ckb = 0, bi = 0, bkb = 0, ai = 0, akb = 0;
   auto adv = [&](int& i, int& kb) {
     if (++kb == kb_of(i)) {
+      kb = 0;
+      ++i;
+    }
+  };
+  // prefetch cursors saturate at the last step (the surplus loads at the end
+  // of the run re-read the last block and are never consumed)
+  auto adv_sat = [&](int& i, int& kb) {
+    if (kb + 1 < kb_of(i)) {
+      ++kb;
+    } else if (i + 1 < nitems) {
       kb = 0;
       ++i;
     }
@@ -287,9 +332,7 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int r = mi * 16 + lg * 4 + v;
-            float rw = 1.f;
-            if (S.row_w && r < rows)
-              rw = S.row_w[S.row_w_by_idx ? S.sorted_idx[rb + r] : rb + r];
+            const float rw = rwl[i][r];
             float amax = 0.f;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
@@ -346,23 +389,28 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       }
       __syncthreads();  // h_lds is the next step's A buffer
     } else {
+      // stage the bf16 tile in LDS, then write it with 16-byte row stores
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         if (mi < nmi) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int r = mi * 16 + lg * 4 + v;
-            if (r < rows) {
-              const int pos = rb + r;
-              float w = 1.f;
-              if (S.row_w) w = S.row_w[S.row_w_by_idx ? S.sorted_idx[pos] : pos];
-              uint16_t* dst = S.y + (size_t)pos * S.N + nt * 256 + wave * 64 + lc;
+            const float w = rwl[i][r];
 #pragma unroll
-              for (int s = 0; s < 4; ++s) dst[s * 16] = f32_to_bf16(acc[mi][s][v] * w);
-            }
+            for (int s = 0; s < 4; ++s)
+              ystage[r * YS + wave * 64 + s * 16 + lc] =
+                  f32_to_bf16(acc[mi][s][v] * w);
           }
         }
       }
+      __syncthreads();
+      for (int c = tid; c < rows * 32; c += 256) {
+        const int r = c >> 5, c8 = c & 31;
+        *(uint4*)(S.y + (size_t)(rb + r) * S.N + nt * 256 + c8 * 8) =
+            *(const uint4*)(ystage + r * YS + c8 * 8);
+      }
+      __syncthreads();
     }
 #pragma unroll
     for (int mi = 0; mi < 8; ++mi)
@@ -371,47 +419,35 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   };
 
   // ---- one pipeline step ----------------------------------------------------
-  auto step = [&](int st, BSet<BF>& bcur, BSet<BF>& bload) {
+  auto step = [&](int st, ASet& acur, ASet& aload, BSet<BF>& bcur,
+                  BSet<BF>& bload) {
     const int buf = st & 1;
     {  // A(st) registers -> LDS
       uint4* p = (uint4*)(a_lds[buf] + my_row * ST_LDS + half * 64);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p[q] = af[q];
-      if (tid < ST_BM) sa_lds[buf][tid] = sa_next;
+      for (int q = 0; q < 4; ++q) p[q] = acur.v[q];
+      if (tid < ST_BM) sa_lds[buf][tid] = acur.s;
     }
     __syncthreads();
-    if (st + 2 < total_steps) {
-      load_b(bload, bi, bkb);
-      adv(bi, bkb);
-    }
-    if (st + 1 < total_steps) {
-      fetch_a(ai, akb);
-      adv(ai, akb);
-    }
+    // both operands are prefetched two steps ahead; the activations of a step
+    // are consumed before its weights, so they are issued first
+    fetch_a(aload, ai, akb);
+    adv_sat(ai, akb);
+    load_b(bload, bi, bkb);
+    adv_sat(bi, bkb);
     // compute step st
     const int4 d = desc[ci];
     const int seg = d.x & 1, nt = d.x >> 1;
     const int nmi = (d.w + 15) >> 4;
     const SegDesc& S = seg ? S1 : S0;
     const int KB = S.K / 128;
-    float sbf[2] = {0.f, 0.f};
-    uint32_t sbe[4] = {0, 0, 0, 0};
-    if constexpr (BF == SF_FP4) {
+    (void)nt;
+    const float sbf[2] = {bcur.sb0, bcur.sb1};
+    uint32_t sbe[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) sbe[s] = (bcur.sc >> (8 * s)) & 0xFF;
-    } else if constexpr (MODE == 0) {
-      const int ntn = S.N / 128;
-      const size_t o = ((size_t)d.y * ntn + nt) * KB + ckb;
-      sbf[0] = ((const float*)S.s0)[o];
-      sbf[1] = ((const float*)S.s1)[o];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sbe[s] = e8m0_bits(sbf[s >> 1]);
-    } else {
-      const int nblk = (nt * 256 + wave * 64) / 128;
-      sbf[0] = sbf[1] = ((const float*)S.s0)[((size_t)d.y * (S.N / 128) + nblk) * KB + ckb];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sbe[s] = e8m0_bits(sbf[0]);
-    }
+    for (int s = 0; s < 4; ++s)
+      sbe[s] = BF == SF_FP4 ? (bcur.sc >> (8 * s)) & 0xFF
+                            : e8m0_bits(sbf[MODE == 0 ? (s >> 1) : 0]);
     const uint8_t* lds = a_lds[buf];
 #pragma unroll
     for (int mi = 0; mi < 8; ++mi) {
@@ -449,18 +485,19 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
 
   // ---- pipeline -------------------------------------------------------------
   BSet<BF> b0, b1, b2;
+  ASet a0, a1, a2;
+  fetch_a(a0, ai, akb);
+  adv_sat(ai, akb);
   load_b(b0, bi, bkb);
-  adv(bi, bkb);
-  if (total_steps > 1) {
-    load_b(b1, bi, bkb);
-    adv(bi, bkb);
-  }
-  fetch_a(ai, akb);
-  adv(ai, akb);
+  adv_sat(bi, bkb);
+  fetch_a(a1, ai, akb);
+  adv_sat(ai, akb);
+  load_b(b1, bi, bkb);
+  adv_sat(bi, bkb);
   for (int st = 0; st < total_steps; st += 3) {
-    step(st, b0, b2);
-    if (st + 1 < total_steps) step(st + 1, b1, b0);
-    if (st + 2 < total_steps) step(st + 2, b2, b1);
+    step(st, a0, a2, b0, b2);
+    if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
+    if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
   }
 }
 
