@@ -119,6 +119,14 @@ __device__ __forceinline__ float silu_f32(float x) {
   return x / (1.0f + expf(-x));
 }
 
+// SiLU from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, about
+// 1 ulp each): x / (1 + 2^(-x log2 e)). Large negative x: the exponential
+// overflows to +inf and the result is -0; large positive x: x.
+__device__ __forceinline__ float silu_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) {
   return 1.0f / (1.0f + expf(-x));
 }

@@ -135,19 +135,24 @@ __device__ __forceinline__ uint32_t e8m0_bits(float pow2) {
   return (__float_as_uint(pow2) >> 23) & 0xFF;
 }
 
+// One 16x16x128 MFMA with the weights as operand A and the activations as
+// operand B: lane l then holds D[4 (l / 16) + v][l % 16], i.e. four
+// consecutive output columns (v) of token l % 16. sw / sx are the e8m0
+// scales of the weight row and of the token (ignored for SF_FP8_F32S, whose
+// block scales are applied to the unscaled partial by the caller).
 template <int BF>
-__device__ __forceinline__ f32x4 st_mma(const v8i& a, const v8i& b, f32x4 c,
-                                        uint32_t sa, uint32_t sb) {
+__device__ __forceinline__ f32x4 st_mma(const v8i& w, const v8i& x, f32x4 c,
+                                        uint32_t sw, uint32_t sx) {
   if constexpr (BF == SF_FP8_F32S) {
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0,
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, z, 0, 0, 0,
                                                             0, 0, 0);
   } else if constexpr (BF == SF_FP8_POW2) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-        a, b, c, 0, 0, 0, (int)sa, 0, (int)sb);
+        w, x, c, 0, 0, 0, (int)sw, 0, (int)sx);
   } else {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-        a, b, c, 0, 4, 0, (int)sa, 0, (int)sb);
+        w, x, c, 4, 0, 0, (int)sw, 0, (int)sx);
   }
 }
 
@@ -167,7 +172,7 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   __shared__ float rwl[ST_MAX_ITEMS][ST_BM];
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][ST_BM * ST_LDS];
   __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM];
-  __shared__ float red[4][ST_BM];
+  __shared__ __attribute__((aligned(16))) float red[ST_BM][4];
   __shared__ __attribute__((aligned(16))) uint16_t ystage[MODE == 1 ? ST_BM * YS : 8];
 
   constexpr int NTW = Stream<BF, MODE>::NTW;
@@ -273,23 +278,18 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     float s;
   };
   // Every prefetch load is issued unconditionally (rows past the tile read
-  // the valid row 0 of rsrc and are zeroed by a select): a load under a
-  // branch would leave the compiler no guaranteed count of younger loads and
-  // force a vmcnt(0) wait that drains the pipeline.
+  // the valid row 0 of rsrc; they are zeroed when the registers are stored to
+  // LDS, after the wait): a load under a branch, which is what the compiler
+  // makes of a select applied right after the load, leaves it no guaranteed
+  // count of younger loads and forces a wait that drains the pipeline.
   auto fetch_a = [&](ASet& af, int i, int kb) {
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
     const int K = S.K, KB = K / 128;
     const uint4* p = (const uint4*)(S.a + (size_t)rsrc[i][my_row] * K + kb * 128 + half * 64);
-    const bool ok = my_row < d.w;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint4 v = p[q];
-      af.v[q] = ok ? v : make_uint4(0, 0, 0, 0);
-    }
-    const int sr = tid & (ST_BM - 1);
-    const float sv = S.sa[(size_t)rsrc[i][sr] * KB + kb];
-    af.s = sr < d.w ? sv : 0.f;
+    for (int q = 0; q < 4; ++q) af.v[q] = p[q];
+    af.s = S.sa[(size_t)rsrc[i][tid & (ST_BM - 1)] * KB + kb];
   };
 
   f32x4 acc[8][4];
@@ -318,6 +318,8 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   };
 
   // ---- epilogues ------------------------------------------------------------
+  // acc[mi][s][v] holds token mi * 16 + lc (tile row) and output column
+  // 16 s + 4 lg + v of the wave's subtiles.
   auto epilogue = [&](int i, int ebuf) {
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = d.x >> 1;
@@ -325,31 +327,33 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     const int rows = d.w, rb = d.z;
     const int nmi = (rows + 15) >> 4;
     if constexpr (MODE == 0) {
+      // h = silu(g) * u * route weight over the wave's 32 columns (gate
+      // subtiles 0, 1; up subtiles 2, 3), row amax across lane groups and
+      // then across the four waves, requantised per row to e4m3.
       const int ntn = S.N / 128;
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         if (mi < nmi) {
+          const int t = mi * 16 + lc;
+          const float rw = rwl[i][t];
+          float amax = 0.f;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = mi * 16 + lg * 4 + v;
-            const float rw = rwl[i][r];
-            float amax = 0.f;
+          for (int s = 0; s < 2; ++s) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
+            for (int v = 0; v < 4; ++v) {
               float g = acc[mi][s][v], u = acc[mi][s + 2][v];
               if (limit > 0.f) {
                 u = fminf(fmaxf(u, -limit), limit);
                 g = fminf(g, limit);
               }
-              const float h = silu_f32(g) * u * rw;
+              const float h = silu_fast(g) * u * rw;
               acc[mi][s][v] = h;
               amax = fmaxf(amax, fabsf(h));
             }
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1)
-              amax = fmaxf(amax, __shfl_xor(amax, o, 16));
-            if (lc == 0) red[wave][r] = amax;
           }
+          amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+          if (lg == 0) red[t][wave] = amax;
         }
       }
       __syncthreads();
@@ -357,27 +361,28 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         if (mi < nmi) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = mi * 16 + lg * 4 + v;
-            const float amax = fmaxf(fmaxf(red[0][r], red[1][r]),
-                                     fmaxf(red[2][r], red[3][r]));
-            float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
-            if (pow2) {
-              const uint32_t bits = __float_as_uint(sc);
-              const int ex = (int)((bits >> 23) & 0xFF) - 127 +
-                             ((bits & 0x7FFFFF) ? 1 : 0);
-              sc = __uint_as_float((uint32_t)(ex + 127) << 23);
-            }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-              const float y = fminf(fmaxf(acc[mi][s][v] / sc, -448.f), 448.f);
-              h_lds[r * ST_LDS + wave * 32 + s * 16 + lc] = (uint8_t)(
-                  __builtin_amdgcn_cvt_pk_fp8_f32(y, 0.f, 0, false) & 0xFF);
-            }
-            if (wave == 0 && lc == 0 && r < rows)
-              S.hs[(size_t)(rb + r) * ntn + nt] = sc;
+          const int t = mi * 16 + lc;
+          const float4 r4 = *(const float4*)red[t];
+          const float amax = fmaxf(fmaxf(r4.x, r4.y), fmaxf(r4.z, r4.w));
+          float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+          if (pow2) {
+            const uint32_t bits = __float_as_uint(sc);
+            const int ex = (int)((bits >> 23) & 0xFF) - 127 +
+                           ((bits & 0x7FFFFF) ? 1 : 0);
+            sc = __uint_as_float((uint32_t)(ex + 127) << 23);
           }
+          const float inv = 1.0f / sc;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            float y[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              y[v] = fminf(fmaxf(acc[mi][s][v] * inv, -448.f), 448.f);
+            *(uint32_t*)(h_lds + t * ST_LDS + wave * 32 + s * 16 + lg * 4) =
+                f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
+          }
+          if (wave == 0 && lg == 0 && t < rows)
+            S.hs[(size_t)(rb + t) * ntn + nt] = sc;
         }
       }
       __syncthreads();
@@ -389,18 +394,21 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       }
       __syncthreads();  // h_lds is the next step's A buffer
     } else {
-      // stage the bf16 tile in LDS, then write it with 16-byte row stores
+      // y = acc * row weight as bf16, staged in LDS (four consecutive
+      // columns per lane = one 8-byte write), then 16-byte row stores
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         if (mi < nmi) {
+          const int t = mi * 16 + lc;
+          const float w = rwl[i][t];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = mi * 16 + lg * 4 + v;
-            const float w = rwl[i][r];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-              ystage[r * YS + wave * 64 + s * 16 + lc] =
-                  f32_to_bf16(acc[mi][s][v] * w);
+          for (int s = 0; s < 4; ++s) {
+            const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][s][0] * w) |
+                                ((uint32_t)f32_to_bf16(acc[mi][s][1] * w) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][s][2] * w) |
+                                ((uint32_t)f32_to_bf16(acc[mi][s][3] * w) << 16);
+            *(uint2*)(ystage + t * YS + wave * 64 + s * 16 + lg * 4) =
+                make_uint2(lo, hi);
           }
         }
       }
@@ -422,11 +430,17 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   auto step = [&](int st, ASet& acur, ASet& aload, BSet<BF>& bcur,
                   BSet<BF>& bload) {
     const int buf = st & 1;
-    {  // A(st) registers -> LDS
+    const int4 d = desc[ci];
+    {  // A(st) registers -> LDS, rows past the tile zeroed
       uint4* p = (uint4*)(a_lds[buf] + my_row * ST_LDS + half * 64);
+      const uint32_t m = my_row < d.w ? ~0u : 0u;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p[q] = acur.v[q];
-      if (tid < ST_BM) sa_lds[buf][tid] = acur.s;
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = acur.v[q];
+        p[q] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+      }
+      const uint32_t ms = tid < d.w ? ~0u : 0u;
+      if (tid < ST_BM) sa_lds[buf][tid] = __uint_as_float(__float_as_uint(acur.s) & ms);
     }
     __syncthreads();
     // both operands are prefetched two steps ahead; the activations of a step
@@ -435,45 +449,68 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     adv_sat(ai, akb);
     load_b(bload, bi, bkb);
     adv_sat(bi, bkb);
-    // compute step st
-    const int4 d = desc[ci];
-    const int seg = d.x & 1, nt = d.x >> 1;
+    // compute step st. Every item has at least one row, so the first 16-row
+    // group is computed unconditionally: all registers of the step's operands
+    // are then consumed on every path, which keeps the compiler's wait for
+    // them at this point instead of at a later reuse of the registers.
+    const int seg = d.x & 1;
     const int nmi = (d.w + 15) >> 4;
     const SegDesc& S = seg ? S1 : S0;
     const int KB = S.K / 128;
-    (void)nt;
-    const float sbf[2] = {bcur.sb0, bcur.sb1};
-    uint32_t sbe[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      sbe[s] = BF == SF_FP4 ? (bcur.sc >> (8 * s)) & 0xFF
-                            : e8m0_bits(sbf[MODE == 0 ? (s >> 1) : 0]);
     const uint8_t* lds = a_lds[buf];
+    auto a_frag = [&](int mi) {
+      const uint8_t* row = lds + (mi * 16 + lc) * ST_LDS;
+      const uint8_t* p0 = BF == SF_FP4 ? row + lg * 16 : row + lg * 32;
+      const uint8_t* p1 = BF == SF_FP4 ? row + 64 + lg * 16 : row + lg * 32 + 16;
+      const uint4 x0 = *(const uint4*)p0, x1 = *(const uint4*)p1;
+      return (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                   (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    };
+    if constexpr (BF == SF_FP8_F32S) {
+      // fp32 block scales: each MFMA yields the unscaled partial of one
+      // 128-wide K block, added as acc += partial * (s_x[token] * s_w); the
+      // lane's four values share one token, so one scale product per
+      // subtile pair. The MFMAs of row group mi run while the partials of
+      // group mi - 1 are rescaled, from a second set of partial registers.
+      const float sb0 = bcur.sb0, sb1 = MODE == 0 ? bcur.sb1 : bcur.sb0;
+      f32x4 part[2][4];
+      auto rescale = [&](int m) {
+        const float sx = sa_lds[buf][m * 16 + lc];
+        const float f0 = sx * sb0, f1 = sx * sb1;
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      if (mi < nmi) {
-        const uint8_t* row = lds + (mi * 16 + lc) * ST_LDS;
-        const uint8_t* p0 = BF == SF_FP4 ? row + lg * 16 : row + lg * 32;
-        const uint8_t* p1 = BF == SF_FP4 ? row + 64 + lg * 16 : row + lg * 32 + 16;
-        const uint4 x0 = *(const uint4*)p0, x1 = *(const uint4*)p1;
-        const v8i a = (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
-                            (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-        if constexpr (BF == SF_FP8_F32S) {
-          const float4 sav = *(const float4*)(sa_lds[buf] + mi * 16 + lg * 4);
-          const float sv[4] = {sav.x, sav.y, sav.z, sav.w};
+        for (int s = 0; s < 4; ++s) {
+          const float f = s < 2 ? f0 : f1;
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const f32x4 p = st_mma<BF>(a, bcur.v[s], acc[mi][s], 0, 0);
-            const float sb = MODE == 0 ? sbf[s >> 1] : sbf[0];
+          for (int v = 0; v < 4; ++v)
+            acc[m][s][v] = fmaf(part[m & 1][s][v], f, acc[m][s][v]);
+        }
+      };
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              acc[mi][s][v] = fmaf(p[v], sv[v] * sb, acc[mi][s][v]);
-          }
-        } else {
-          const uint32_t sae = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
+      for (int mi = 0; mi < 8; ++mi) {
+        if (mi == 0 || mi < nmi) {
+          const v8i x = a_frag(mi);
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            acc[mi][s] = st_mma<BF>(a, bcur.v[s], acc[mi][s], sae, sbe[s]);
+            part[mi & 1][s] = st_mma<BF>(bcur.v[s], x, part[mi & 1][s], 0, 0);
+        }
+        if (mi > 0 && (mi == 1 || mi - 1 < nmi)) rescale(mi - 1);
+      }
+      if (nmi == 8) rescale(7);
+    } else {
+      const float sbf[2] = {bcur.sb0, bcur.sb1};
+      uint32_t sbe[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        sbe[s] = BF == SF_FP4 ? (bcur.sc >> (8 * s)) & 0xFF
+                              : e8m0_bits(sbf[MODE == 0 ? (s >> 1) : 0]);
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) {
+        if (mi == 0 || mi < nmi) {
+          const v8i x = a_frag(mi);
+          const uint32_t sxe = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
         }
       }
     }
@@ -494,11 +531,17 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   adv_sat(ai, akb);
   load_b(b1, bi, bkb);
   adv_sat(bi, bkb);
-  for (int st = 0; st < total_steps; st += 3) {
+  // The loop body runs its three steps unconditionally: a conditional step
+  // would make the compiler's wait analysis at the back-edge merge a path
+  // whose most recent loads are two steps older, and wait for everything.
+  int st = 0;
+  for (; st + 3 <= total_steps; st += 3) {
     step(st, a0, a2, b0, b2);
-    if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
-    if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+    step(st + 1, a1, a0, b1, b0);
+    step(st + 2, a2, a1, b2, b1);
   }
+  if (st < total_steps) step(st, a0, a2, b0, b2);
+  if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
 }
 
 static int num_cus() {
