@@ -124,6 +124,15 @@ struct BSet {
   float sb1;     // fp8 gate/up: W3 block scale
 };
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Streaming (nontemporal) 16-byte load: expert weights are read once per
+// layer and should not evict the gathered activation rows from L2.
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+  const v4u t = __builtin_nontemporal_load((const v4u*)p);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 template <int MODE>
 __device__ __forceinline__ int seg_items(const SegDesc& s) {
   const int ntn = MODE == 0 ? s.N / 128 : s.N / 256;
@@ -244,17 +253,17 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     if constexpr (BF == SF_FP4) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint4 v = *(const uint4*)(base + (wave * 4 + s) * 1024 + lane * 16);
+        const uint4 v = ld_stream(base + (wave * 4 + s) * 1024 + lane * 16);
         b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
       const uint32_t* sp = (const uint32_t*)(seg ? S1.s0 : S0.s0);
-      b.sc = sp[blk * 256 + wave * 64 + lane];
+      b.sc = __builtin_nontemporal_load(sp + blk * 256 + wave * 64 + lane);
       b.sb0 = b.sb1 = 0.f;
     } else {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint4 lo4 = *(const uint4*)(base + ((wave * 4 + s) * 2) * 1024 + lane * 16);
-        const uint4 hi4 = *(const uint4*)(base + ((wave * 4 + s) * 2 + 1) * 1024 + lane * 16);
+        const uint4 lo4 = ld_stream(base + ((wave * 4 + s) * 2) * 1024 + lane * 16);
+        const uint4 hi4 = ld_stream(base + ((wave * 4 + s) * 2 + 1) * 1024 + lane * 16);
         b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
@@ -282,13 +291,17 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   // LDS, after the wait): a load under a branch, which is what the compiler
   // makes of a select applied right after the load, leaves it no guaranteed
   // count of younger loads and forces a wait that drains the pipeline.
+  // Thread tid gathers 16-byte chunk (tid & 7) of tile rows 32 q + tid / 8:
+  // each load instruction of a wave reads eight whole 128-byte row segments.
+  const int a_chunk = tid & 7, a_row0 = tid >> 3;
   auto fetch_a = [&](ASet& af, int i, int kb) {
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
     const int K = S.K, KB = K / 128;
-    const uint4* p = (const uint4*)(S.a + (size_t)rsrc[i][my_row] * K + kb * 128 + half * 64);
+    const uint8_t* base = S.a + kb * 128 + a_chunk * 16;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) af.v[q] = p[q];
+    for (int q = 0; q < 4; ++q)
+      af.v[q] = *(const uint4*)(base + (size_t)rsrc[i][q * 32 + a_row0] * K);
     af.s = S.sa[(size_t)rsrc[i][tid & (ST_BM - 1)] * KB + kb];
   };
 
@@ -432,29 +445,28 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     const int buf = st & 1;
     const int4 d = desc[ci];
     {  // A(st) registers -> LDS, rows past the tile zeroed
-      uint4* p = (uint4*)(a_lds[buf] + my_row * ST_LDS + half * 64);
-      const uint32_t m = my_row < d.w ? ~0u : 0u;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        const int r = q * 32 + a_row0;
+        const uint32_t m = r < d.w ? ~0u : 0u;
         const uint4 v = acur.v[q];
-        p[q] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+        *(uint4*)(a_lds[buf] + r * ST_LDS + a_chunk * 16) =
+            make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
       }
       const uint32_t ms = tid < d.w ? ~0u : 0u;
       if (tid < ST_BM) sa_lds[buf][tid] = __uint_as_float(__float_as_uint(acur.s) & ms);
     }
     __syncthreads();
-    // both operands are prefetched two steps ahead; the activations of a step
-    // are consumed before its weights, so they are issued first
+    // both operands are prefetched three steps ahead; the activations of a
+    // step are consumed before its weights, so they are issued first
     fetch_a(aload, ai, akb);
     adv_sat(ai, akb);
     load_b(bload, bi, bkb);
     adv_sat(bi, bkb);
-    // compute step st. Every item has at least one row, so the first 16-row
-    // group is computed unconditionally: all registers of the step's operands
-    // are then consumed on every path, which keeps the compiler's wait for
-    // them at this point instead of at a later reuse of the registers.
+    // compute step st over all eight 16-row groups: rows past the tile are
+    // zero in LDS, and a branch-free step lets the compiler issue the LDS
+    // reads of the next groups ahead of the MFMAs of the current one.
     const int seg = d.x & 1;
-    const int nmi = (d.w + 15) >> 4;
     const SegDesc& S = seg ? S1 : S0;
     const int KB = S.K / 128;
     const uint8_t* lds = a_lds[buf];
@@ -487,15 +499,13 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       };
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
-        if (mi == 0 || mi < nmi) {
-          const v8i x = a_frag(mi);
+        const v8i x = a_frag(mi);
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            part[mi & 1][s] = st_mma<BF>(bcur.v[s], x, part[mi & 1][s], 0, 0);
-        }
-        if (mi > 0 && (mi == 1 || mi - 1 < nmi)) rescale(mi - 1);
+        for (int s = 0; s < 4; ++s)
+          part[mi & 1][s] = st_mma<BF>(bcur.v[s], x, part[mi & 1][s], 0, 0);
+        if (mi > 0) rescale(mi - 1);
       }
-      if (nmi == 8) rescale(7);
+      rescale(7);
     } else {
       const float sbf[2] = {bcur.sb0, bcur.sb1};
       uint32_t sbe[4];
@@ -505,13 +515,11 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
                               : e8m0_bits(sbf[MODE == 0 ? (s >> 1) : 0]);
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
-        if (mi == 0 || mi < nmi) {
-          const v8i x = a_frag(mi);
-          const uint32_t sxe = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
+        const v8i x = a_frag(mi);
+        const uint32_t sxe = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
-        }
+        for (int s = 0; s < 4; ++s)
+          acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
       }
     }
     const bool last = ckb + 1 == KB;
@@ -521,8 +529,12 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   };
 
   // ---- pipeline -------------------------------------------------------------
-  BSet<BF> b0, b1, b2;
-  ASet a0, a1, a2;
+  // Four register sets per operand, prefetch distance 3. The loop body runs
+  // its four steps unconditionally: a conditional step would make the
+  // compiler's wait analysis at the back-edge merge a path whose most recent
+  // loads are older, and wait for everything.
+  BSet<BF> b0, b1, b2, b3;
+  ASet a0, a1, a2, a3;
   fetch_a(a0, ai, akb);
   adv_sat(ai, akb);
   load_b(b0, bi, bkb);
@@ -531,17 +543,20 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   adv_sat(ai, akb);
   load_b(b1, bi, bkb);
   adv_sat(bi, bkb);
-  // The loop body runs its three steps unconditionally: a conditional step
-  // would make the compiler's wait analysis at the back-edge merge a path
-  // whose most recent loads are two steps older, and wait for everything.
+  fetch_a(a2, ai, akb);
+  adv_sat(ai, akb);
+  load_b(b2, bi, bkb);
+  adv_sat(bi, bkb);
   int st = 0;
-  for (; st + 3 <= total_steps; st += 3) {
-    step(st, a0, a2, b0, b2);
+  for (; st + 4 <= total_steps; st += 4) {
+    step(st, a0, a3, b0, b3);
     step(st + 1, a1, a0, b1, b0);
     step(st + 2, a2, a1, b2, b1);
+    step(st + 3, a3, a2, b3, b2);
   }
-  if (st < total_steps) step(st, a0, a2, b0, b2);
+  if (st < total_steps) step(st, a0, a3, b0, b3);
   if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
+  if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
 }
 
 static int num_cus() {
