@@ -229,6 +229,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run the library's copy kernel over MIB MiB five "
+                         "times (the known-size reference for scaling HBM "
+                         "byte counters) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus "
@@ -245,6 +249,17 @@ def main(argv=None) -> int:
                                   to_device_raw)
     if not _lib.available():
         raise RuntimeError(f"libsllm_moe.so unavailable: {_lib._lib_error}")
+
+    if args.copy_calib:
+        from sllm_amd.runtime import copy
+        nb = args.copy_calib << 20
+        src, dst = DeviceBuffer(nb), DeviceBuffer(nb)
+        memset(src, 1, nb)
+        for _ in range(5):
+            copy(dst, src, nb)
+        sync()
+        print(json.dumps({"copy_calib_bytes": nb, "launches": 5}))
+        return 0
 
     c = dict(C2)
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]

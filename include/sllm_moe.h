@@ -71,6 +71,10 @@ int sllm_event_sync(void* ev);
 float sllm_event_elapsed_ms(void* start, void* stop);
 /* stream-ordered byte fill (cache flushing between timed decode calls) */
 int sllm_memset(void* dst, int value, long nbytes, void* stream);
+/* stream-ordered device-to-device copy by a plain read/write kernel (the
+ * reference copy of known size against which HBM byte counters are scaled);
+ * dst, src 16-byte aligned */
+int sllm_buf_copy(void* dst, const void* src, long nbytes, void* stream);
 /* dst[i] ~ N(0, std^2), a pure function of (seed, i) */
 int sllm_fill_normal(float* dst, long n, unsigned long long seed, float stdv,
                      void* stream);

@@ -82,6 +82,7 @@ SIGNATURES = {
     "sllm_event_sync": (c_int, [P]),
     "sllm_event_elapsed_ms": (c_float, [P, P]),
     "sllm_memset": (c_int, [P, c_int, c_long, P]),
+    "sllm_buf_copy": (c_int, [P, P, c_long, P]),
     "sllm_fill_normal": (c_int, [P, c_long, ctypes.c_ulonglong, c_float, P]),
     "sllm_q4_moe_router": (c_int, [F, F, I, c_int, c_int, c_int]),
     "sllm_q4_moe_router_dev": (c_int, [P, P, P, c_int, c_int, c_int]),

@@ -8,6 +8,8 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace sllm {
@@ -31,6 +33,17 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
   x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
   return x ^ (x >> 31);
+}
+
+// grid-stride copy: 16-byte vectors, then the byte tail
+__global__ void copy_kernel(const uint8_t* __restrict__ src,
+                            uint8_t* __restrict__ dst, long nbytes) {
+  const long n16 = nbytes / 16;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    ((uint4*)dst)[i] = ((const uint4*)src)[i];
+  const long t = n16 * 16 + (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < nbytes) dst[t] = src[t];
 }
 
 __global__ void fill_normal_kernel(float* __restrict__ dst, long n,
@@ -172,6 +185,20 @@ float sllm_event_elapsed_ms(void* start, void* stop) {
 int sllm_memset(void* dst, int value, long nbytes, void* stream) {
   SLLM_REQUIRE(dst && nbytes >= 0, "sllm_memset: bad args");
   SLLM_HIP(hipMemsetAsync(dst, value, (size_t)nbytes, (hipStream_t)stream));
+  return 0;
+}
+
+int sllm_buf_copy(void* dst, const void* src, long nbytes, void* stream) {
+  SLLM_REQUIRE(dst && src && nbytes >= 0 && ((uintptr_t)dst % 16) == 0 &&
+                   ((uintptr_t)src % 16) == 0,
+               "sllm_buf_copy: need 16-byte aligned non-null buffers");
+  if (nbytes == 0) return 0;
+  const long n16 = nbytes / 16;
+  const int dev_cus = 256;
+  const long blocks = n16 > 0 ? std::min<long>((n16 + 255) / 256, 8L * dev_cus) : 1;
+  copy_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)src, (uint8_t*)dst, nbytes);
+  SLLM_LAUNCHED();
   return 0;
 }
 

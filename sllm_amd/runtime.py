@@ -210,6 +210,12 @@ def fill_normal(buf, n: int, seed: int, std: float = 1.0, stream=None) -> None:
                "sllm_fill_normal")
 
 
+def copy(dst, src, nbytes: int, stream=None) -> None:
+    """Device-to-device copy of ``nbytes`` by the library's copy kernel."""
+    _lib.check(_lib.lib().sllm_buf_copy(ptr(dst), ptr(src), int(nbytes),
+                                        stream_handle(stream)), "sllm_buf_copy")
+
+
 def memset(buf, value: int, nbytes: int, stream=None) -> None:
     _lib.check(_lib.lib().sllm_memset(ptr(buf), int(value), int(nbytes),
                                       stream_handle(stream)), "sllm_memset")

@@ -130,3 +130,19 @@ def test_gemm_ex_f32_and_bf16():
     sync()
     ab, wb = codecs.round_bf16(a), codecs.round_bf16(w)
     np.testing.assert_allclose(c.copy_host().reshape(m, n), ab @ wb.T, rtol=1e-4, atol=1e-4)
+
+
+def test_buf_copy_exact_with_tail():
+    """sllm_buf_copy (the calibration copy kernel): byte-exact over a size
+    with a non-multiple-of-16 tail and over an empty copy."""
+    from sllm_amd.runtime import DeviceBuffer, copy, sync
+    rng = np.random.default_rng(5)
+    n = (1 << 20) + 13
+    src_h = rng.integers(0, 256, n, dtype=np.uint8)
+    src = DeviceBuffer(n)
+    src.upload_raw(src_h)
+    dst = DeviceBuffer(n)
+    copy(dst, src, n)
+    copy(dst, src, 0)
+    sync()
+    np.testing.assert_array_equal(dst.copy_host_raw(np.uint8, (n,)), src_h)
