@@ -2,7 +2,8 @@
 // weight layouts they read.
 //
 // Same arithmetic and epilogues as gemm_grouped.hip (see there for the
-// reference semantics); this file changes how the expert weights move:
+// reference semantics); this file changes how the expert weights move and
+// how the work is spread over the chip:
 //
 // * Packed weights. A one-time repack (sllm_moe_pack_weights) stores each
 //   expert's weights in MFMA operand order: for every (expert, column slab,
@@ -10,17 +11,19 @@
 //   subtile, exactly the bytes each lane feeds the MFMA, so every wave load
 //   instruction reads 1 KB of consecutive HBM and a workgroup streams one
 //   contiguous 32 KB (fp8) / 16 KB (fp4) block per K step.
-// * Persistent workgroups, one per CU (up to 512 registers per lane). Each
-//   owns a contiguous run of work items (row tile x column slab, routed
-//   items first, then the shared expert's) and walks the flat sequence of
-//   (item, K step); the weight operands of step s+2 are in flight while
-//   step s computes, across item boundaries, so the weight stream does not
-//   drain between tiles. The gathered activation tile of step s+2 is
-//   fetched into registers during step s as well and double-buffered in LDS
-//   (it comes from L2 / the Infinity Cache, whose latency under this load is
-//   microseconds, so one step of lead is not enough).
-// * Item descriptors and gathered row indices for the whole run are loaded
-//   into LDS once at the start.
+// * Persistent workgroups of eight waves (two per SIMD, so that one wave's
+//   LDS, dependency and barrier stalls are covered by the other's MFMA and
+//   VALU work), one workgroup per CU. Each walks the flat sequence of
+//   (item, K step) of its items, an item being a 128-row tile x column slab
+//   of the routed segment or of the shared expert's; operands of step s+3
+//   are in flight while step s computes, across item boundaries.
+// * XCD-aware item order. Workgroups are dealt to the eight XCDs round-robin
+//   (blockIdx % 8); each XCD owns a contiguous range of items and its
+//   workgroups take that range's items round-robin, so the column slabs of
+//   one row tile run at the same time on one XCD and gather the same
+//   activation rows through that XCD's L2.
+// * Item descriptors and gathered row indices of a workgroup's items are
+//   loaded into LDS once at the start.
 #include "launch.h"
 
 namespace sllm {
@@ -33,25 +36,27 @@ enum { SF_FP8_F32S = 0, SF_FP8_POW2 = 1, SF_FP4 = 2 };
 constexpr int ST_BM = 128;
 constexpr int ST_LDS = 144;          // A row stride in LDS (128 + 16 pad)
 constexpr int ST_MAX_ITEMS = 32;     // work items per workgroup
+constexpr int ST_WAVES = 8;          // waves per workgroup
+constexpr int ST_THREADS = 64 * ST_WAVES;
 
 // ---------------------------------------------------------------------------
 // packed layouts
 // ---------------------------------------------------------------------------
 // up   (MODE 0): W1, W3 (E, N, K), N = intermediate, K = hidden; slab = 128
-//       h columns, subtile s of wave w = rows 128 nt + 32 w + 16 (s & 1) +
-//       (l % 16) of W1 (s < 2) or W3 (s >= 2).
+//       h columns; wave w owns h columns 128 nt + 16 w + (l % 16): subtile 0
+//       holds those rows of W1 (gate), subtile 1 the same rows of W3 (up).
 // down (MODE 1): W2 (E, N, K), N = hidden, K = intermediate; slab = 256
-//       columns, subtile s of wave w = rows 256 nt + 64 w + 16 s + (l % 16).
+//       columns; subtile s of wave w = rows 256 nt + 32 w + 16 s + (l % 16).
 // fp8: block (e, nt, kb) = 32 KB at ((e NT + nt) KB + kb) * 32768, inside
-//       [w 4][s 4][h 2][lane 64][16 B]: the lane's 32 bytes are K
+//       [w 8][s 2][h 2][lane 64][16 B]: the lane's 32 bytes are K
 //       [128 kb + 32 (l / 16), +32), half h = bytes [16 h, 16 h + 16).
-// fp4: block = 16 KB, [w][s][lane][16 B]: K [128 kb + 32 (l / 16), +32) =
-//       packed bytes [64 kb + 16 (l / 16), +16); e8m0 scales packed as one
-//       dword per lane per block: 1 KB blocks [w][lane][s], byte s = scale of
-//       (row of subtile s, K block 4 kb + l / 16).
+// fp4: block = 16 KB, [w 8][s 2][lane 64][16 B]: K [128 kb + 32 (l / 16),
+//       +32) = packed bytes [64 kb + 16 (l / 16), +16); e8m0 scales packed as
+//       1 KB blocks [w 8][lane 64][s 2], byte s = scale of (row of subtile s,
+//       K block 4 kb + l / 16).
 __device__ __forceinline__ int slab_row(int up, int nt, int w, int s, int l) {
-  return up ? nt * 128 + w * 32 + (s & 1) * 16 + (l & 15)
-            : nt * 256 + w * 64 + s * 16 + (l & 15);
+  return up ? nt * 128 + w * 16 + (l & 15)
+            : nt * 256 + w * 32 + s * 16 + (l & 15);
 }
 
 __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w0,
@@ -62,13 +67,13 @@ __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w0,
   const int NT = up ? N / 128 : N / 256, KB = K / 128;
   const long nchunks = (long)E * NT * KB * 2048;
   if (c >= nchunks) return;
-  const int l = c & 63, h = (c >> 6) & 1, s = (c >> 7) & 3, w = (c >> 9) & 3;
+  const int l = c & 63, h = (c >> 6) & 1, s = (c >> 7) & 1, w = (c >> 8) & 7;
   const long blk = c >> 11;
   const int kb = (int)(blk % KB);
   const long t = blk / KB;
   const int nt = (int)(t % NT), e = (int)(t / NT);
   const int row = slab_row(up, nt, w, s, l);
-  const uint8_t* src = (up && s >= 2) ? w1 : w0;
+  const uint8_t* src = (up && s == 1) ? w1 : w0;
   const size_t col = (size_t)kb * 128 + (l >> 4) * 32 + h * 16;
   *(uint4*)(out + c * 16) = *(const uint4*)(src + ((size_t)e * N + row) * K + col);
 }
@@ -78,32 +83,32 @@ __global__ void pack_fp4_kernel(const uint8_t* __restrict__ w0,
                                 const uint8_t* __restrict__ s0,
                                 const uint8_t* __restrict__ s1,
                                 uint8_t* __restrict__ out,
-                                uint32_t* __restrict__ out_s, int E, int N,
+                                uint16_t* __restrict__ out_s, int E, int N,
                                 int K, int up) {
   const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int NT = up ? N / 128 : N / 256, KB = K / 128;
   const long nchunks = (long)E * NT * KB * 1024;
   if (c >= nchunks) return;
-  const int l = c & 63, s = (c >> 6) & 3, w = (c >> 8) & 3;
+  const int l = c & 63, s = (c >> 6) & 1, w = (c >> 7) & 7;
   const long blk = c >> 10;
   const int kb = (int)(blk % KB);
   const long t = blk / KB;
   const int nt = (int)(t % NT), e = (int)(t / NT);
   const int row = slab_row(up, nt, w, s, l);
-  const uint8_t* src = (up && s >= 2) ? w1 : w0;
+  const uint8_t* src = (up && s == 1) ? w1 : w0;
   const size_t col = (size_t)kb * 64 + (l >> 4) * 16;
   *(uint4*)(out + c * 16) =
       *(const uint4*)(src + ((size_t)e * N + row) * (K / 2) + col);
-  if (s == 0) {  // one thread per (block, w, lane) writes the scale dword
+  if (s == 0) {  // one thread per (block, w, lane) writes the two scale bytes
     uint32_t v = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       const int rq = slab_row(up, nt, w, q, l);
-      const uint8_t* sp = (up && q >= 2) ? s1 : s0;
+      const uint8_t* sp = (up && q == 1) ? s1 : s0;
       v |= (uint32_t)sp[((size_t)e * N + rq) * (K / 32) + kb * 4 + (l >> 4)]
            << (8 * q);
     }
-    out_s[blk * 256 + w * 64 + l] = v;
+    out_s[blk * 512 + w * 64 + l] = (uint16_t)v;
   }
 }
 
@@ -118,8 +123,8 @@ __global__ void pack_fp4_kernel(const uint8_t* __restrict__ w0,
 // the wait for it drain every prefetch behind it).
 template <int BF>
 struct BSet {
-  v8i v[4];
-  uint32_t sc;   // fp4: packed e8m0 scale bytes of the 4 subtiles
+  v8i v[2];
+  uint32_t sc;   // fp4: packed e8m0 scale bytes of the 2 subtiles
   float sb0;     // fp8: W1 / W2 block scale
   float sb1;     // fp8 gate/up: W3 block scale
 };
@@ -173,7 +178,7 @@ struct Stream {
 
 // item descriptor in LDS: x = seg | nt << 1, y = e, z = row_begin, w = rows
 template <int BF, int MODE>
-__global__ __launch_bounds__(256, 1) void moe_stream_kernel(
+__global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, int pow2) {
   constexpr int YS = 264;  // bf16 row stride of the down-projection staging
   __shared__ int4 desc[ST_MAX_ITEMS];
@@ -181,25 +186,28 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   __shared__ float rwl[ST_MAX_ITEMS][ST_BM];
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][ST_BM * ST_LDS];
   __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM];
-  __shared__ __attribute__((aligned(16))) float red[ST_BM][4];
+  __shared__ __attribute__((aligned(16))) float red[ST_BM][ST_WAVES];
   __shared__ __attribute__((aligned(16))) uint16_t ystage[MODE == 1 ? ST_BM * YS : 8];
 
   constexpr int NTW = Stream<BF, MODE>::NTW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, lc = lane & 15;
 
+  // ---- this workgroup's items (XCD-aware round-robin) ----------------------
   const int n0 = seg_items<MODE>(S0);
   const int n1 = nseg > 1 ? seg_items<MODE>(S1) : 0;
   const int total = n0 + n1;
-  const int chunk = (total + gridDim.x - 1) / gridDim.x;
-  const int lo = blockIdx.x * chunk;
-  const int hi = min(total, lo + chunk);
-  if (lo >= hi || chunk > ST_MAX_ITEMS) return;  // host sizes grid so chunk fits
-  const int nitems = hi - lo;
+  const int nx = gridDim.x / 8;  // workgroups per XCD (grid is a multiple of 8)
+  const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
+  const int xbeg = (int)((long)total * xcd / 8);
+  const int xend = (int)((long)total * (xcd + 1) / 8);
+  const int nitems = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
+  if (nitems == 0 || nitems > ST_MAX_ITEMS) return;  // host sizes the grid
+  auto item_at = [&](int m) { return xbeg + jx + m * nx; };
 
   // ---- phase 0: descriptors and gathered row indices -> LDS ---------------
   if (tid < nitems) {
-    const int it = lo + tid;
+    const int it = item_at(tid);
     const int seg = it >= n0;
     const SegDesc& S = seg ? S1 : S0;
     const int li = seg ? it - n0 : it;
@@ -218,7 +226,7 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     desc[tid] = make_int4(seg | (nt << 1), e, rb, rows);
   }
   __syncthreads();
-  for (int q = tid; q < nitems * ST_BM; q += 256) {
+  for (int q = tid; q < nitems * ST_BM; q += ST_THREADS) {
     const int i = q / ST_BM, r = q % ST_BM;
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
@@ -242,97 +250,106 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   int total_steps = 0;
   for (int i = 0; i < nitems; ++i) total_steps += kb_of(i);
 
-  auto load_b = [&](BSet<BF>& b, int i, int kb) {
+  struct ASet {
+    uint4 v[2];
+    float s;
+  };
+
+  // ---- prefetch cursor ------------------------------------------------------
+  // Addresses of the prefetch cursor's item are kept in registers and
+  // rebuilt from LDS only when the cursor enters a new item, so a step's
+  // loads issue without a chain of dependent LDS reads.
+  // Thread tid gathers 16-byte chunk (tid & 7) of tile rows 64 q + tid / 8:
+  // each load instruction of a wave reads eight whole 128-byte row segments.
+  // Rows past the tile read the valid row 0 of rsrc; they are zeroed when
+  // the registers are stored to LDS, after the wait (a load under a branch,
+  // which is what the compiler makes of a select applied right after the
+  // load, leaves it no guaranteed count of younger loads and forces a wait
+  // that drains the pipeline).
+  const int a_chunk = tid & 7, a_row0 = tid >> 3;
+  int pi = 0, pkb = 0, pKB = 1;
+  const uint8_t *pa0 = nullptr, *pa1 = nullptr, *pb = nullptr;
+  const float *psa = nullptr, *ps0 = nullptr, *ps1 = nullptr;
+  const uint16_t* ps4 = nullptr;
+  auto p_enter = [&](int i) {
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = d.x >> 1;
-    const uint8_t* wp = seg ? S1.wp : S0.wp;
-    const int N = seg ? S1.N : S0.N, K = seg ? S1.K : S0.K;
-    const int NT = N / NTW, KB = K / 128;
-    const size_t blk = ((size_t)d.y * NT + nt) * KB + kb;
-    const uint8_t* base = wp + blk * Stream<BF, MODE>::BLK;
+    const SegDesc& S = seg ? S1 : S0;
+    const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
+    pKB = KB;
+    pa0 = S.a + (size_t)rsrc[i][a_row0] * K + a_chunk * 16;
+    pa1 = S.a + (size_t)rsrc[i][64 + a_row0] * K + a_chunk * 16;
+    psa = S.sa + (size_t)rsrc[i][tid & (ST_BM - 1)] * KB;
+    const size_t blk0 = ((size_t)d.y * NT + nt) * KB;
+    if constexpr (BF == SF_FP4) {
+      pb = S.wp + blk0 * Stream<BF, MODE>::BLK + (wave * 2) * 1024 + lane * 16;
+      ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
+    } else {
+      pb = S.wp + blk0 * Stream<BF, MODE>::BLK + (wave * 4) * 1024 + lane * 16;
+      if constexpr (MODE == 0) {
+        ps0 = (const float*)S.s0 + blk0;  // NT = N / 128: scale row (e, nt)
+        ps1 = (const float*)S.s1 + blk0;
+      } else {
+        const int nblk = nt * 2 + wave / 4;  // the wave's 32 columns' block
+        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB;
+      }
+    }
+  };
+  auto p_advance = [&]() {  // saturates at the last step of the last item
+    if (pkb + 1 < pKB) {
+      ++pkb;
+    } else if (pi + 1 < nitems) {
+      ++pi;
+      pkb = 0;
+      p_enter(pi);
+    }
+  };
+  auto fetch_a = [&](ASet& af) {
+    af.v[0] = *(const uint4*)(pa0 + pkb * 128);
+    af.v[1] = *(const uint4*)(pa1 + pkb * 128);
+    af.s = psa[pkb];
+  };
+  auto load_b = [&](BSet<BF>& b) {
+    const uint8_t* base = pb + (size_t)pkb * Stream<BF, MODE>::BLK;
     if constexpr (BF == SF_FP4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 v = ld_stream(base + (wave * 4 + s) * 1024 + lane * 16);
+      for (int s = 0; s < 2; ++s) {
+        const uint4 v = ld_stream(base + s * 1024);
         b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
-      const uint32_t* sp = (const uint32_t*)(seg ? S1.s0 : S0.s0);
-      b.sc = __builtin_nontemporal_load(sp + blk * 256 + wave * 64 + lane);
+      b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
       b.sb0 = b.sb1 = 0.f;
     } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 lo4 = ld_stream(base + ((wave * 4 + s) * 2) * 1024 + lane * 16);
-        const uint4 hi4 = ld_stream(base + ((wave * 4 + s) * 2 + 1) * 1024 + lane * 16);
+      for (int s = 0; s < 2; ++s) {
+        const uint4 lo4 = ld_stream(base + (2 * s) * 1024);
+        const uint4 hi4 = ld_stream(base + (2 * s + 1) * 1024);
         b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
       b.sc = 0;
-      const float* s0p = (const float*)(seg ? S1.s0 : S0.s0);
-      if constexpr (MODE == 0) {
-        const float* s1p = (const float*)(seg ? S1.s1 : S0.s1);
-        const size_t o = ((size_t)d.y * NT + nt) * KB + kb;  // NT = N / 128
-        b.sb0 = s0p[o];
-        b.sb1 = s1p[o];
-      } else {
-        const int nblk = (nt * 256 + wave * 64) / 128;
-        b.sb0 = b.sb1 = s0p[((size_t)d.y * (N / 128) + nblk) * KB + kb];
-      }
+      b.sb0 = ps0[pkb];
+      b.sb1 = MODE == 0 ? ps1[pkb] : b.sb0;
     }
   };
 
-  const int my_row = tid >> 1, half = tid & 1;
-  struct ASet {
-    uint4 v[4];
-    float s;
-  };
-  // Every prefetch load is issued unconditionally (rows past the tile read
-  // the valid row 0 of rsrc; they are zeroed when the registers are stored to
-  // LDS, after the wait): a load under a branch, which is what the compiler
-  // makes of a select applied right after the load, leaves it no guaranteed
-  // count of younger loads and forces a wait that drains the pipeline.
-  // Thread tid gathers 16-byte chunk (tid & 7) of tile rows 32 q + tid / 8:
-  // each load instruction of a wave reads eight whole 128-byte row segments.
-  const int a_chunk = tid & 7, a_row0 = tid >> 3;
-  auto fetch_a = [&](ASet& af, int i, int kb) {
-    const int4 d = desc[i];
-    const SegDesc& S = (d.x & 1) ? S1 : S0;
-    const int K = S.K, KB = K / 128;
-    const uint8_t* base = S.a + kb * 128 + a_chunk * 16;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      af.v[q] = *(const uint4*)(base + (size_t)rsrc[i][q * 32 + a_row0] * K);
-    af.s = S.sa[(size_t)rsrc[i][tid & (ST_BM - 1)] * KB + kb];
-  };
-
-  f32x4 acc[8][4];
+  f32x4 acc[8][2];
 #pragma unroll
   for (int mi = 0; mi < 8; ++mi)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < 2; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // cursors: compute (ci, ckb), B prefetch (bi, bkb), A prefetch (ai, akb)
-  int ci = 0, ckb = 0, bi = 0, bkb = 0, ai = 0, akb = 0;
-  auto adv = [&](int& i, int& kb) {
-    if (++kb == kb_of(i)) {
-      kb = 0;
-      ++i;
-    }
-  };
-  // prefetch cursors saturate at the last step (the surplus loads at the end
-  // of the run re-read the last block and are never consumed)
-  auto adv_sat = [&](int& i, int& kb) {
-    if (kb + 1 < kb_of(i)) {
-      ++kb;
-    } else if (i + 1 < nitems) {
-      kb = 0;
-      ++i;
-    }
+  // ---- compute cursor -------------------------------------------------------
+  int ci = 0, ckb = 0, cKB = 1, crows = 0;
+  auto c_enter = [&](int i) {
+    const int4 d = desc[i];
+    cKB = ((d.x & 1) ? S1.K : S0.K) / 128;
+    crows = d.w;
   };
 
   // ---- epilogues ------------------------------------------------------------
   // acc[mi][s][v] holds token mi * 16 + lc (tile row) and output column
-  // 16 s + 4 lg + v of the wave's subtiles.
+  // 4 lg + v of the wave's subtile s.
   auto epilogue = [&](int i, int ebuf) {
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = d.x >> 1;
@@ -340,9 +357,9 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     const int rows = d.w, rb = d.z;
     const int nmi = (rows + 15) >> 4;
     if constexpr (MODE == 0) {
-      // h = silu(g) * u * route weight over the wave's 32 columns (gate
-      // subtiles 0, 1; up subtiles 2, 3), row amax across lane groups and
-      // then across the four waves, requantised per row to e4m3.
+      // h = silu(g) * u * route weight over the wave's 16 columns, row amax
+      // across lane groups and then across the eight waves, requantised per
+      // row (one 128-column block) to e4m3.
       const int ntn = S.N / 128;
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
@@ -351,18 +368,15 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
           const float rw = rwl[i][t];
           float amax = 0.f;
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              float g = acc[mi][s][v], u = acc[mi][s + 2][v];
-              if (limit > 0.f) {
-                u = fminf(fmaxf(u, -limit), limit);
-                g = fminf(g, limit);
-              }
-              const float h = silu_fast(g) * u * rw;
-              acc[mi][s][v] = h;
-              amax = fmaxf(amax, fabsf(h));
+          for (int v = 0; v < 4; ++v) {
+            float g = acc[mi][0][v], u = acc[mi][1][v];
+            if (limit > 0.f) {
+              u = fminf(fmaxf(u, -limit), limit);
+              g = fminf(g, limit);
             }
+            const float h = silu_fast(g) * u * rw;
+            acc[mi][0][v] = h;
+            amax = fmaxf(amax, fabsf(h));
           }
           amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
           amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
@@ -375,8 +389,10 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       for (int mi = 0; mi < 8; ++mi) {
         if (mi < nmi) {
           const int t = mi * 16 + lc;
-          const float4 r4 = *(const float4*)red[t];
-          const float amax = fmaxf(fmaxf(r4.x, r4.y), fmaxf(r4.z, r4.w));
+          const float4 r0 = *(const float4*)&red[t][0];
+          const float4 r1 = *(const float4*)&red[t][4];
+          const float amax = fmaxf(fmaxf(fmaxf(r0.x, r0.y), fmaxf(r0.z, r0.w)),
+                                   fmaxf(fmaxf(r1.x, r1.y), fmaxf(r1.z, r1.w)));
           float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
           if (pow2) {
             const uint32_t bits = __float_as_uint(sc);
@@ -385,25 +401,21 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
             sc = __uint_as_float((uint32_t)(ex + 127) << 23);
           }
           const float inv = 1.0f / sc;
+          float y[4];
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            float y[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              y[v] = fminf(fmaxf(acc[mi][s][v] * inv, -448.f), 448.f);
-            *(uint32_t*)(h_lds + t * ST_LDS + wave * 32 + s * 16 + lg * 4) =
-                f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
-          }
+          for (int v = 0; v < 4; ++v)
+            y[v] = fminf(fmaxf(acc[mi][0][v] * inv, -448.f), 448.f);
+          *(uint32_t*)(h_lds + t * ST_LDS + wave * 16 + lg * 4) =
+              f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
           if (wave == 0 && lg == 0 && t < rows)
             S.hs[(size_t)(rb + t) * ntn + nt] = sc;
         }
       }
       __syncthreads();
-      if (my_row < rows) {
-        const uint4* p = (const uint4*)(h_lds + my_row * ST_LDS + half * 64);
-        uint4* dst = (uint4*)(S.hq + (size_t)(rb + my_row) * S.N + nt * 128 + half * 64);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) dst[q] = p[q];
+      for (int c = tid; c < rows * 8; c += ST_THREADS) {
+        const int r = c >> 3, c16 = c & 7;
+        *(uint4*)(S.hq + (size_t)(rb + r) * S.N + nt * 128 + c16 * 16) =
+            *(const uint4*)(h_lds + r * ST_LDS + c16 * 16);
       }
       __syncthreads();  // h_lds is the next step's A buffer
     } else {
@@ -415,18 +427,18 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
           const int t = mi * 16 + lc;
           const float w = rwl[i][t];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
+          for (int s = 0; s < 2; ++s) {
             const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][s][0] * w) |
                                 ((uint32_t)f32_to_bf16(acc[mi][s][1] * w) << 16);
             const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][s][2] * w) |
                                 ((uint32_t)f32_to_bf16(acc[mi][s][3] * w) << 16);
-            *(uint2*)(ystage + t * YS + wave * 64 + s * 16 + lg * 4) =
+            *(uint2*)(ystage + t * YS + wave * 32 + s * 16 + lg * 4) =
                 make_uint2(lo, hi);
           }
         }
       }
       __syncthreads();
-      for (int c = tid; c < rows * 32; c += 256) {
+      for (int c = tid; c < rows * 32; c += ST_THREADS) {
         const int r = c >> 5, c8 = c & 31;
         *(uint4*)(S.y + (size_t)(rb + r) * S.N + nt * 256 + c8 * 8) =
             *(const uint4*)(ystage + r * YS + c8 * 8);
@@ -436,39 +448,41 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
 #pragma unroll
     for (int mi = 0; mi < 8; ++mi)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < 2; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+
+  auto prefetch = [&](ASet& af, BSet<BF>& bf) {
+    fetch_a(af);
+    load_b(bf);
+    p_advance();
   };
 
   // ---- one pipeline step ----------------------------------------------------
   auto step = [&](int st, ASet& acur, ASet& aload, BSet<BF>& bcur,
                   BSet<BF>& bload) {
     const int buf = st & 1;
-    const int4 d = desc[ci];
     {  // A(st) registers -> LDS, rows past the tile zeroed
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = q * 32 + a_row0;
-        const uint32_t m = r < d.w ? ~0u : 0u;
+      for (int q = 0; q < 2; ++q) {
+        const int r = q * 64 + a_row0;
+        const uint32_t m = r < crows ? ~0u : 0u;
         const uint4 v = acur.v[q];
         *(uint4*)(a_lds[buf] + r * ST_LDS + a_chunk * 16) =
             make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
       }
-      const uint32_t ms = tid < d.w ? ~0u : 0u;
+      const uint32_t ms = tid < crows ? ~0u : 0u;
       if (tid < ST_BM) sa_lds[buf][tid] = __uint_as_float(__float_as_uint(acur.s) & ms);
     }
     __syncthreads();
     // both operands are prefetched three steps ahead; the activations of a
-    // step are consumed before its weights, so they are issued first
-    fetch_a(aload, ai, akb);
-    adv_sat(ai, akb);
-    load_b(bload, bi, bkb);
-    adv_sat(bi, bkb);
+    // step are consumed before its weights, so they are issued first. The
+    // batch is kept in one piece and in the same order in every step and in
+    // the prologue, so the compiler's count of younger loads at each wait is
+    // the same on every path into it.
+    prefetch(aload, bload);
     // compute step st over all eight 16-row groups: rows past the tile are
     // zero in LDS, and a branch-free step lets the compiler issue the LDS
     // reads of the next groups ahead of the MFMAs of the current one.
-    const int seg = d.x & 1;
-    const SegDesc& S = seg ? S1 : S0;
-    const int KB = S.K / 128;
     const uint8_t* lds = a_lds[buf];
     auto a_frag = [&](int mi) {
       const uint8_t* row = lds + (mi * 16 + lc) * ST_LDS;
@@ -481,17 +495,17 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
     if constexpr (BF == SF_FP8_F32S) {
       // fp32 block scales: each MFMA yields the unscaled partial of one
       // 128-wide K block, added as acc += partial * (s_x[token] * s_w); the
-      // lane's four values share one token, so one scale product per
-      // subtile pair. The MFMAs of row group mi run while the partials of
-      // group mi - 1 are rescaled, from a second set of partial registers.
+      // lane's four values share one token. The MFMAs of row group mi run
+      // while the partials of group mi - 1 are rescaled, from a second set
+      // of partial registers.
       const float sb0 = bcur.sb0, sb1 = MODE == 0 ? bcur.sb1 : bcur.sb0;
-      f32x4 part[2][4];
+      f32x4 part[2][2];
       auto rescale = [&](int m) {
         const float sx = sa_lds[buf][m * 16 + lc];
         const float f0 = sx * sb0, f1 = sx * sb1;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float f = s < 2 ? f0 : f1;
+        for (int s = 0; s < 2; ++s) {
+          const float f = s == 0 ? f0 : f1;
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             acc[m][s][v] = fmaf(part[m & 1][s][v], f, acc[m][s][v]);
@@ -501,31 +515,34 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
       for (int mi = 0; mi < 8; ++mi) {
         const v8i x = a_frag(mi);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 2; ++s)
           part[mi & 1][s] = st_mma<BF>(bcur.v[s], x, part[mi & 1][s], 0, 0);
         if (mi > 0) rescale(mi - 1);
       }
       rescale(7);
     } else {
-      const float sbf[2] = {bcur.sb0, bcur.sb1};
-      uint32_t sbe[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        sbe[s] = BF == SF_FP4 ? (bcur.sc >> (8 * s)) & 0xFF
-                              : e8m0_bits(sbf[MODE == 0 ? (s >> 1) : 0]);
+      uint32_t sbe[2];
+      if constexpr (BF == SF_FP4) {
+        sbe[0] = bcur.sc & 0xFF;
+        sbe[1] = (bcur.sc >> 8) & 0xFF;
+      } else {
+        sbe[0] = e8m0_bits(bcur.sb0);
+        sbe[1] = e8m0_bits(MODE == 0 ? bcur.sb1 : bcur.sb0);
+      }
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         const v8i x = a_frag(mi);
         const uint32_t sxe = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 2; ++s)
           acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
       }
     }
-    const bool last = ckb + 1 == KB;
-    const int cur_item = ci;
-    adv(ci, ckb);
-    if (last) epilogue(cur_item, buf ^ 1);
+    if (++ckb == cKB) {
+      epilogue(ci, buf ^ 1);
+      ckb = 0;
+      if (ci + 1 < nitems) c_enter(++ci);
+    }
   };
 
   // ---- pipeline -------------------------------------------------------------
@@ -535,18 +552,11 @@ __global__ __launch_bounds__(256, 1) void moe_stream_kernel(
   // loads are older, and wait for everything.
   BSet<BF> b0, b1, b2, b3;
   ASet a0, a1, a2, a3;
-  fetch_a(a0, ai, akb);
-  adv_sat(ai, akb);
-  load_b(b0, bi, bkb);
-  adv_sat(bi, bkb);
-  fetch_a(a1, ai, akb);
-  adv_sat(ai, akb);
-  load_b(b1, bi, bkb);
-  adv_sat(bi, bkb);
-  fetch_a(a2, ai, akb);
-  adv_sat(ai, akb);
-  load_b(b2, bi, bkb);
-  adv_sat(bi, bkb);
+  p_enter(0);
+  c_enter(0);
+  prefetch(a0, b0);
+  prefetch(a1, b1);
+  prefetch(a2, b2);
   int st = 0;
   for (; st + 4 <= total_steps; st += 4) {
     step(st, a0, a3, b0, b3);
@@ -576,11 +586,17 @@ static int num_cus() {
 template <int BF, int MODE>
 static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
                      float limit, int pow2, long upper_items, hipStream_t st) {
-  const long need = (upper_items + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
-  const long grid = need > num_cus() ? need : num_cus();
+  // workgroups per XCD: at least one per CU, and enough that no workgroup
+  // receives more than ST_MAX_ITEMS items (an XCD's range holds at most
+  // ceil(upper / 8) items, dealt round-robin over its workgroups)
+  const long per_xcd = (upper_items + 7) / 8;
+  long nx = (num_cus() + 7) / 8;
+  const long need = (per_xcd + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
+  if (need > nx) nx = need;
+  const long grid = 8 * nx;
   SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
   SegDesc dummy = s0;
-  moe_stream_kernel<BF, MODE><<<(unsigned)grid, 256, 0, st>>>(
+  moe_stream_kernel<BF, MODE><<<(unsigned)grid, ST_THREADS, 0, st>>>(
       s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
   SLLM_LAUNCHED();
   return 0;
@@ -667,7 +683,7 @@ int sllm_moe_pack_weights(int fp4, int up, const void* w0, const void* w1,
   if (fp4)
     pack_fp4_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
         (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)s0,
-        (const uint8_t*)s1, (uint8_t*)out, (uint32_t*)out_scales, E, N, K, up);
+        (const uint8_t*)s1, (uint8_t*)out, (uint16_t*)out_scales, E, N, K, up);
   else
     pack_fp8_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
         (const uint8_t*)w0, (const uint8_t*)w1, (uint8_t*)out, E, N, K, up);

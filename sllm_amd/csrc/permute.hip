@@ -76,10 +76,18 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
     const int e = e0 + tid;
     int cnt = 0;
     if (e < E) {
-      for (int c = 0; c < nchunks; ++c) {
-        int v = chunk_hist[(size_t)c * E + e];
-        chunk_hist[(size_t)c * E + e] = cnt;  // exclusive within expert
-        cnt += v;
+      // eight chunk counts in flight at a time (a dependent load per chunk
+      // would expose the memory latency nchunks times)
+      for (int c0 = 0; c0 < nchunks; c0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (c0 + j < nchunks) chunk_hist[(size_t)(c0 + j) * E + e] = cnt;
+          cnt += v[j];  // exclusive within expert
+        }
       }
     }
     int ntile = (e < E && cnt > 0) ? (cnt + bm - 1) / bm : 0;
@@ -89,7 +97,15 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
     if (e < E) {
       counts[e] = cnt;
       offsets[e] = off;
-      for (int c = 0; c < nchunks; ++c) chunk_hist[(size_t)c * E + e] += off;
+      for (int c0 = 0; c0 < nchunks; c0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (c0 + j < nchunks) chunk_hist[(size_t)(c0 + j) * E + e] = v[j] + off;
+      }
       for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
         const int r0 = i * bm;
         *(int4*)(tile_info + 4 * (toff + i)) =
@@ -120,9 +136,17 @@ __global__ __launch_bounds__(64) void permute_scatter_kernel(
   __syncthreads();
   const int a0 = c * PERM_CHUNK, a1 = min(N, a0 + PERM_CHUNK);
   const uint64_t lt = (1ull << lane) - 1ull;
-  for (int base = a0; base < a1; base += 64) {
+  // the chunk's ids, all loads in flight at once (clamped in-bounds)
+  constexpr int G = PERM_CHUNK / 64;
+  int idv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) idv[g] = ids[min(a0 + g * 64 + lane, N - 1)];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int base = a0 + g * 64;
+    if (base >= a1) break;
     const int a = base + lane;
-    const int raw = a < a1 ? ids[a] : -1;
+    const int raw = a < a1 ? idv[g] : -1;
     const bool valid = raw >= 0 && raw < E;  // out-of-range ids are dropped
     const int e = valid ? raw : 0;
     uint64_t peers = __ballot(valid);

@@ -21,72 +21,155 @@
 namespace sllm {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // --------------------------------------------------------------------------
 // router GEMM: logits (T, E) fp32 = x (T, H) bf16 . W (E, H)^T bf16
 // --------------------------------------------------------------------------
-// WG = 4 waves, tile 64 tokens x 64 experts, each wave a 32x32 quadrant made
-// of 2x2 MFMA 16x16x32 bf16 subtiles. K advances 128 at a time; every lane
-// loads 64 contiguous bytes per row (4 MFMAs worth). The MFMA's K order is
-// irrelevant as long as both operands use the same lane->K assignment.
-constexpr int RG_TILE = 64;
+// MFMA 16x16x32 bf16; lane l feeds row l % 16 and the 8 K values
+// [8 (l / 16), +8) of each 32-wide K slice (the same lane->K assignment for
+// both operands, so the MFMA's internal K order does not matter). Output:
+// lane l, element v = row 4 (l / 16) + v, column l % 16.
+//
+// Prefill (T > 64): a workgroup owns a 64-token x 128-expert tile; both
+// operands go through LDS in 128-wide K chunks (row stride padded to
+// 272 B), with two chunks' global loads in flight (two register stages,
+// two LDS buffers) while one is multiplied. Wave (wm, we) of the 2 x 2
+// arrangement computes 32 tokens x 64 experts as 2 x 4 subtiles. x is read
+// E / 128 times and W T / 64 times, both mostly from L2.
+constexpr int RG_TT = 64, RG_TE = 128, RG_KC = 128, RG_LS = 136;  // LS in bf16
 
-__global__ __launch_bounds__(256) void router_gemm_kernel(
+__global__ __launch_bounds__(256, 1) void router_gemm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     float* __restrict__ logits, int T, int E, int H) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tile_e = blockIdx.x, tile_t = blockIdx.y;
-  const int r0 = tile_t * RG_TILE + (wave >> 1) * 32;
-  const int c0 = tile_e * RG_TILE + (wave & 1) * 32;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][RG_TT * RG_LS];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[2][RG_TE * RG_LS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-
-  const uint16_t* arow[2];
-  const uint16_t* brow[2];
+  const int wm = wave >> 1, we = wave & 1;
+  const int t0 = blockIdx.x * RG_TT, e0 = blockIdx.y * RG_TE;
+  // global -> register staging, 16 threads per 256-byte row segment:
+  // x 64 rows (4 x 16 B per thread), W 128 rows (8 x 16 B per thread)
+  const int srow = tid >> 4, scol = (tid & 15) * 8;  // scol in bf16
+  const uint16_t* xg = x + (size_t)min(t0 + srow, T - 1) * H + scol;
+  const uint16_t* wg = w + (size_t)min(e0 + srow, E - 1) * H + scol;
+  u32x4 r0[12], r1[12];  // the two register stages
+  auto gload = [&](u32x4 (&rg)[12], int k0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    int r = min(r0 + i * 16 + lr, T - 1);
-    int c = min(c0 + i * 16 + lr, E - 1);
-    arow[i] = x + (size_t)r * H + lg * 32;
-    brow[i] = w + (size_t)c * H + lg * 32;
-  }
-  f32x4 acc[2][2];
+    for (int q = 0; q < 4; ++q) {
+      const int row = min(t0 + srow + 16 * q, T - 1) - min(t0 + srow, T - 1);
+      rg[q] = *(const u32x4*)(xg + (size_t)row * H + k0);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int row = min(e0 + srow + 16 * q, E - 1) - min(e0 + srow, E - 1);
+      rg[4 + q] = *(const u32x4*)(wg + (size_t)row * H + k0);
+    }
+  };
+  auto sstore = [&](const u32x4 (&rg)[12], int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *(u32x4*)(xs[b] + (srow + 16 * q) * RG_LS + scol) = rg[q];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      *(u32x4*)(ws[b] + (srow + 16 * q) * RG_LS + scol) = rg[4 + q];
+  };
+  f32x4 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = 0; k0 < H; k0 += 128) {
-    bf16x8 a[2][4], b[2][4];
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 a[2], bb[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[i][q] = *(const bf16x8*)(arow[i] + k0 + q * 8);
-        b[i][q] = *(const bf16x8*)(brow[i] + k0 + q * 8);
-      }
+      for (int i = 0; i < 2; ++i)
+        a[i] = *(const bf16x8*)(xs[b] + (wm * 32 + i * 16 + lr) * RG_LS + q * 32 + lg * 8);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+      for (int j = 0; j < 4; ++j)
+        bb[j] = *(const bf16x8*)(ws[b] + (we * 64 + j * 16 + lr) * RG_LS + q * 32 + lg * 8);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  const int nk = H / RG_KC;
+  // chunk kc lives in register stage kc & 1 and LDS buffer kc & 1; the
+  // prefetch of chunk kc + 2 reuses the stage chunk kc just left
+  // prefetches past the last chunk re-read the last chunk (kept
+  // unconditional so the register stages stay in registers)
+  auto kof = [&](int kc) { return min(kc, nk - 1) * RG_KC; };
+  gload(r0, 0);
+  gload(r1, kof(1));
+  for (int kc = 0; kc < nk; kc += 2) {
+    sstore(r0, 0);
+    __syncthreads();
+    gload(r0, kof(kc + 2));
+    mma(0);
+    if (kc + 1 < nk) {
+      sstore(r1, 1);
+      __syncthreads();
+      gload(r1, kof(kc + 3));
+      mma(1);
+    }
   }
-  // output layout of a 16x16 MFMA tile: lane l, element v holds
-  // row 4*(l/16)+v, column l%16
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        int r = r0 + i * 16 + lg * 4 + v;
-        int c = c0 + j * 16 + lr;
-        if (r < T && c < E) logits[(size_t)r * E + c] = acc[i][j][v];
+        const int rr = t0 + wm * 32 + i * 16 + lg * 4 + v;
+        const int c = e0 + we * 64 + j * 16 + lr;
+        if (rr < T && c < E) logits[(size_t)rr * E + c] = acc[i][j][v];
       }
+}
+
+// Small T (decode, T <= 64): a workgroup owns 16 experts and all T tokens;
+// its 8 waves split K (wave w takes the 32-wide slices w, w + 8, ...) so the
+// router weights stream through many CUs at once; partial sums are reduced
+// through LDS.
+constexpr int RG_SMALL_T = 64;
+
+__global__ __launch_bounds__(512) void router_gemm_small_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    float* __restrict__ logits, int T, int E, int H) {
+  __shared__ float part[8][RG_SMALL_T][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int e0 = blockIdx.x * 16;
+  const int nti = (T + 15) / 16;
+  const uint16_t* brow = w + (size_t)min(e0 + lr, E - 1) * H + lg * 8;
+  f32x4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int k0 = wave * 32; k0 < H; k0 += 256) {
+    const bf16x8 b = *(const bf16x8*)(brow + k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < nti) {
+        const bf16x8 a = *(const bf16x8*)(
+            x + (size_t)min(i * 16 + lr, T - 1) * H + k0 + lg * 8);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[i], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wave][i * 16 + lg * 4 + v][lr] = acc[i][v];
+  __syncthreads();
+  for (int q = threadIdx.x; q < T * 16; q += 512) {
+    const int r = q >> 4, c = q & 15;
+    float s = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < 8; ++wv) s += part[wv][r][c];
+    if (e0 + c < E) logits[(size_t)r * E + e0 + c] = s;
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -306,8 +389,13 @@ int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
   SLLM_REQUIRE(T > 0 && E > 0 && H > 0 && H % 128 == 0,
                "router_gemm: need T,E>0 and H %% 128 == 0 (T=%d E=%d H=%d)",
                T, E, H);
-  dim3 grid(ceil_div(E, RG_TILE), ceil_div(T, RG_TILE));
-  router_gemm_kernel<<<grid, 256, 0, st>>>(x, w, logits, T, E, H);
+  if (T <= RG_SMALL_T) {
+    router_gemm_small_kernel<<<ceil_div(E, 16), 512, 0, st>>>(x, w, logits,
+                                                              T, E, H);
+  } else {
+    dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
+    router_gemm_kernel<<<grid, 256, 0, st>>>(x, w, logits, T, E, H);
+  }
   SLLM_LAUNCHED();
   return 0;
 }

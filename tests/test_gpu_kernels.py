@@ -189,7 +189,8 @@ def test_route_grouped_matches_oracle(L, G, kg, scoring):
 
 def test_router_gemm_matches_fp64(L):
     rng = np.random.default_rng(3)
-    for T, E, H in [(4096, 512, 2048), (64, 16, 1024), (33, 100, 256)]:
+    for T, E, H in [(4096, 512, 2048), (64, 16, 1024), (33, 100, 256),
+                    (100, 300, 256), (1, 512, 2048), (65, 40, 384)]:
         x = codecs.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
         wr = codecs.round_bf16((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
         out = empty(T * E * 4)
@@ -229,7 +230,8 @@ def _run_permute(L, ids, E, bm):
 
 @pytest.mark.parametrize("T,E,k,skew", [(4096, 512, 10, False), (16384, 512, 10, True),
                                         (1, 512, 10, False), (3, 7, 2, False),
-                                        (1000, 2048, 16, True)])
+                                        (1000, 2048, 16, True), (2000, 1024, 8, True),
+                                        (20000, 256, 8, False)])
 def test_permute_bit_exact(L, T, E, k, skew):
     rng = np.random.default_rng(T + E)
     if skew:
@@ -264,20 +266,27 @@ def test_fill_normal_deterministic_and_normal(L):
     assert abs((np.abs(x) < 2.0).mean() - 0.6827) < 0.003
 
 
+def _np_rows(up, nt, w, s, l):
+    """Weight row fed by lane l of wave w, subtile s, column slab nt."""
+    return (nt * 128 + w * 16 + (l & 15)) if up else \
+        (nt * 256 + w * 32 + s * 16 + (l & 15))
+
+
 def _np_pack_fp8(w0, w1, up):
-    """numpy statement of the fp8 streaming layout (gemm_stream.hip)."""
+    """numpy statement of the fp8 streaming layout (gemm_stream.hip):
+    32 KB blocks [wave 8][subtile 2][half 2][lane 64][16 B] per
+    (expert, slab, K step); gate/up subtile 1 is W3."""
     E, N, K = w0.shape
     NT, KB = (N // 128 if up else N // 256), K // 128
     out = np.empty(E * NT * KB * 32768, np.uint8)
     c = np.arange(out.size // 16)
-    l, h, s, w = c & 63, (c >> 6) & 1, (c >> 7) & 3, (c >> 9) & 3
+    l, h, s, w = c & 63, (c >> 6) & 1, (c >> 7) & 1, (c >> 8) & 7
     blk = c >> 11
     kb, t = blk % KB, blk // KB
     nt, e = t % NT, t // NT
-    row = (nt * 128 + w * 32 + (s & 1) * 16 + (l & 15)) if up else \
-        (nt * 256 + w * 64 + s * 16 + (l & 15))
+    row = _np_rows(up, nt, w, s, l)
     col = kb * 128 + (l >> 4) * 32 + h * 16
-    src = np.where((s >= 2) & bool(up), 1, 0)
+    src = np.where((s == 1) & bool(up), 1, 0)
     both = np.stack([w0, w1 if w1 is not None else w0])
     for b in range(16):
         out[c * 16 + b] = both[src, e, row, col + b]
@@ -285,34 +294,32 @@ def _np_pack_fp8(w0, w1, up):
 
 
 def _np_pack_fp4(w0, w1, s0, s1, up):
+    """fp4 streaming layout: 16 KB blocks [wave 8][subtile 2][lane 64][16 B]
+    and 1 KB scale blocks [wave 8][lane 64][subtile 2] of e8m0 bytes."""
     E, N, Kh = w0.shape
     K = Kh * 2
     NT, KB = (N // 128 if up else N // 256), K // 128
     out = np.empty(E * NT * KB * 16384, np.uint8)
-    outs = np.empty(E * NT * KB * 256, np.uint32)
+    outs = np.empty(E * NT * KB * 512, np.uint16)
     c = np.arange(out.size // 16)
-    l, s, w = c & 63, (c >> 6) & 3, (c >> 8) & 3
+    l, s, w = c & 63, (c >> 6) & 1, (c >> 7) & 7
     blk = c >> 10
     kb, t = blk % KB, blk // KB
     nt, e = t % NT, t // NT
-
-    def rowf(sv):
-        return (nt * 128 + w * 32 + (sv & 1) * 16 + (l & 15)) if up else \
-            (nt * 256 + w * 64 + sv * 16 + (l & 15))
-    row = rowf(s)
+    row = _np_rows(up, nt, w, s, l)
     col = kb * 64 + (l >> 4) * 16
-    src = np.where((s >= 2) & bool(up), 1, 0)
+    src = np.where((s == 1) & bool(up), 1, 0)
     both = np.stack([w0, w1 if w1 is not None else w0])
     sboth = np.stack([s0, s1 if s1 is not None else s0])
     for b in range(16):
         out[c * 16 + b] = both[src, e, row, col + b]
     sel = s == 0
-    v = np.zeros(sel.sum(), np.uint32)
-    for q in range(4):
-        rq = rowf(np.full_like(s, q))[sel]
-        sq = np.where((q >= 2) & bool(up), 1, 0)
-        v |= sboth[sq, e[sel], rq, kb[sel] * 4 + (l[sel] >> 4)].astype(np.uint32) << (8 * q)
-    outs[blk[sel] * 256 + w[sel] * 64 + l[sel]] = v
+    v = np.zeros(sel.sum(), np.uint16)
+    for q in range(2):
+        rq = _np_rows(up, nt[sel], w[sel], q, l[sel])
+        sq = 1 if (q == 1 and up) else 0
+        v |= sboth[sq, e[sel], rq, kb[sel] * 4 + (l[sel] >> 4)].astype(np.uint16) << (8 * q)
+    outs[blk[sel] * 512 + w[sel] * 64 + l[sel]] = v
     return out, outs
 
 
@@ -336,4 +343,4 @@ def test_pack_weights_layout(L, up):
     _KEEP.extend([p4, ps])
     want, wants = _np_pack_fp4(f0, f1, s0, s1, up)
     np.testing.assert_array_equal(host(p4, np.uint8, (p4.nbytes,)), want)
-    np.testing.assert_array_equal(host(ps, np.uint32, (ps.nbytes // 4,)), wants)
+    np.testing.assert_array_equal(host(ps, np.uint16, (ps.nbytes // 2,)), wants)
