@@ -24,6 +24,8 @@
 //   activation rows through that XCD's L2.
 // * Item descriptors and gathered row indices of a workgroup's items are
 //   loaded into LDS once at the start.
+#include <type_traits>
+
 #include "launch.h"
 
 namespace sllm {
@@ -569,6 +571,331 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
 }
 
+// ---------------------------------------------------------------------------
+// decode variant
+// ---------------------------------------------------------------------------
+// Same items, packed weights, persistent XCD-aware dealing and prefetch
+// pipeline as moe_stream_kernel, for the decode regime (a handful of rows
+// per expert): 16-row tiles, activations kept unquantized. Each lane's
+// weight bytes (32 consecutive K of its row) are converted to bf16 in
+// registers -- exact for e4m3 and for e2m1 times its e8m0 scale -- and fed to
+// four v_mfma_f32_16x16x32_bf16 per subtile and K step, slice m taking K
+// [32 g + 8 m, +8) of lane group g for both operands. x is bf16 already;
+// the fp32 h of the down projection is split into bf16 hi + lo halves (two
+// MFMAs), which keeps ~16 mantissa bits. fp8 block scales multiply the
+// step's fp32 partial.
+constexpr int SD_BM = 16;
+constexpr int SD_LS = 136;  // bf16 row stride of the LDS activation tile
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_bf16_hi(float a, float b) {
+  // fp32 values that are exact in bf16: keep the upper halves
+  return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
+}
+
+// 8 e4m3 bytes (two dwords) -> 8 bf16
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(d0, false);
+  const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(d0, true);
+  const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(d1, false);
+  const f32x2 e = __builtin_amdgcn_cvt_pk_f32_fp8(d1, true);
+  const u32x4v r = {pack_bf16_hi(a.x, a.y), pack_bf16_hi(b.x, b.y),
+                    pack_bf16_hi(c.x, c.y), pack_bf16_hi(e.x, e.y)};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// e2m1 nibble -> fp32 (exact)
+__device__ __forceinline__ float e2m1_f32(uint32_t n) {
+  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
+  const uint32_t bits = e ? ((e + 126u) << 23) | (m << 22) : (m ? 0x3F000000u : 0u);
+  return __uint_as_float(bits | ((n & 8u) << 28));
+}
+
+// 8 e2m1 values (one dword, low nibble first) times scale -> 8 bf16
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t d, float scale) {
+  float f[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = e2m1_f32((d >> (4 * j)) & 15u) * scale;
+  const u32x4v r = {pack_bf16_hi(f[0], f[1]), pack_bf16_hi(f[2], f[3]),
+                    pack_bf16_hi(f[4], f[5]), pack_bf16_hi(f[6], f[7])};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// e8m0 byte -> fp32 scale, loader convention (loaders/fp8.py:145-156):
+// 0x00 -> 0, 0xFF -> NaN
+__device__ __forceinline__ float e8m0_f32(uint32_t b) {
+  return b == 0 ? 0.f : (b == 255 ? __uint_as_float(0x7FC00000u)
+                                  : __uint_as_float(b << 23));
+}
+
+template <int BF, int MODE>
+__global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
+    SegDesc S0, SegDesc S1, int nseg, int topk, float limit) {
+  __shared__ int4 desc[ST_MAX_ITEMS];
+  __shared__ int rsrc[ST_MAX_ITEMS][SD_BM];
+  __shared__ float rwl[ST_MAX_ITEMS][SD_BM];
+  __shared__ __attribute__((aligned(16))) uint16_t a_hi[2][SD_BM * SD_LS];
+  __shared__ __attribute__((aligned(16))) uint16_t a_lo[MODE == 1 ? 2 : 1][MODE == 1 ? SD_BM * SD_LS : 8];
+
+  constexpr int NTW = MODE == 0 ? 128 : 256;
+  constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, lc = lane & 15;
+
+  auto seg_items_dec = [&](const SegDesc& S) {
+    const int rt = S.tile_info ? *S.num_tiles : (S.total_rows + SD_BM - 1) / SD_BM;
+    return rt * (S.N / NTW);
+  };
+  const int n0 = seg_items_dec(S0);
+  const int n1 = nseg > 1 ? seg_items_dec(S1) : 0;
+  const int total = n0 + n1;
+  const int nx = gridDim.x / 8;
+  const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
+  const int xbeg = (int)((long)total * xcd / 8);
+  const int xend = (int)((long)total * (xcd + 1) / 8);
+  const int nitems = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
+  if (nitems == 0 || nitems > ST_MAX_ITEMS) return;  // host sizes the grid
+
+  if (tid < nitems) {
+    const int it = xbeg + jx + tid * nx;
+    const int seg = it >= n0;
+    const SegDesc& S = seg ? S1 : S0;
+    const int li = seg ? it - n0 : it;
+    const int ntn = S.N / NTW;
+    const int rt = li / ntn, nt = li % ntn;
+    int e = 0, rb, rows;
+    if (S.tile_info) {
+      const int4 d = *(const int4*)(S.tile_info + 4 * rt);
+      e = d.x;
+      rb = d.y;
+      rows = min(SD_BM, d.z);
+    } else {
+      rb = rt * SD_BM;
+      rows = min(SD_BM, S.total_rows - rb);
+    }
+    desc[tid] = make_int4(seg | (nt << 1), e, rb, rows);
+  }
+  __syncthreads();
+  for (int q = tid; q < nitems * SD_BM; q += ST_THREADS) {
+    const int i = q / SD_BM, r = q % SD_BM;
+    const int4 d = desc[i];
+    const SegDesc& S = (d.x & 1) ? S1 : S0;
+    int src = 0;
+    float rw = 1.f;
+    if (r < d.w) {
+      const int p = d.z + r;
+      src = S.gather ? S.sorted_idx[p] / topk : p;
+      if (S.row_w) rw = S.row_w[S.row_w_by_idx ? S.sorted_idx[p] : p];
+    }
+    rsrc[i][r] = src;
+    rwl[i][r] = rw;
+  }
+  __syncthreads();
+
+  int total_steps = 0;
+  for (int i = 0; i < nitems; ++i) total_steps += ((desc[i].x & 1) ? S1.K : S0.K) / 128;
+
+  // activation tile of a K step: 16 rows x 128 values; thread tid takes row
+  // tid / 32 and values [4 (tid % 32), +4)
+  const int a_row = tid >> 5, a_col = (tid & 31) * 4;
+  typedef typename std::conditional<MODE == 0, u32x2, u32x4v>::type AVec;
+  struct ASet {
+    AVec v;
+  };
+  struct BSetD {
+    v8i v[2];
+    uint32_t sc;
+    float sb0, sb1;
+  };
+
+  int pi = 0, pkb = 0, pKB = 1;
+  const uint8_t* pa = nullptr;
+  const uint8_t* pb = nullptr;
+  const float *ps0 = nullptr, *ps1 = nullptr;
+  const uint16_t* ps4 = nullptr;
+  auto p_enter = [&](int i) {
+    const int4 d = desc[i];
+    const int seg = d.x & 1, nt = d.x >> 1;
+    const SegDesc& S = seg ? S1 : S0;
+    const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
+    pKB = KB;
+    pa = S.a + ((size_t)rsrc[i][a_row] * K + a_col) * (MODE == 0 ? 2 : 4);
+    const size_t blk0 = ((size_t)d.y * NT + nt) * KB;
+    if constexpr (BF == SF_FP4) {
+      pb = S.wp + blk0 * BLK + (wave * 2) * 1024 + lane * 16;
+      ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
+    } else {
+      pb = S.wp + blk0 * BLK + (wave * 4) * 1024 + lane * 16;
+      if constexpr (MODE == 0) {
+        ps0 = (const float*)S.s0 + blk0;
+        ps1 = (const float*)S.s1 + blk0;
+      } else {
+        const int nblk = nt * 2 + wave / 4;
+        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB;
+      }
+    }
+  };
+  auto p_advance = [&]() {
+    if (pkb + 1 < pKB) {
+      ++pkb;
+    } else if (pi + 1 < nitems) {
+      ++pi;
+      pkb = 0;
+      p_enter(pi);
+    }
+  };
+  auto prefetch = [&](ASet& af, BSetD& b) {
+    af.v = *(const AVec*)(pa + (size_t)pkb * 128 * (MODE == 0 ? 2 : 4));
+    const uint8_t* base = pb + (size_t)pkb * BLK;
+    if constexpr (BF == SF_FP4) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint4 v = ld_stream(base + s * 1024);
+        b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+      }
+      b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
+      b.sb0 = b.sb1 = 1.f;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint4 lo4 = ld_stream(base + (2 * s) * 1024);
+        const uint4 hi4 = ld_stream(base + (2 * s + 1) * 1024);
+        b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
+                       (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
+      }
+      b.sc = 0;
+      b.sb0 = ps0[pkb];
+      b.sb1 = MODE == 0 ? ps1[pkb] : b.sb0;
+    }
+    p_advance();
+  };
+
+  f32x4 acc[2];
+  acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  int ci = 0, ckb = 0, cKB = 1, crows = 0;
+  auto c_enter = [&](int i) {
+    const int4 d = desc[i];
+    cKB = ((d.x & 1) ? S1.K : S0.K) / 128;
+    crows = d.w;
+  };
+
+  // acc[s][v]: token lc of the tile, output column 4 lg + v of subtile s
+  auto epilogue = [&](int i) {
+    const int4 d = desc[i];
+    const int seg = d.x & 1, nt = d.x >> 1;
+    const SegDesc& S = seg ? S1 : S0;
+    if (lc < d.w) {
+      const float rw = rwl[i][lc];
+      if constexpr (MODE == 0) {
+        float h[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float g = acc[0][v], u = acc[1][v];
+          if (limit > 0.f) {
+            u = fminf(fmaxf(u, -limit), limit);
+            g = fminf(g, limit);
+          }
+          h[v] = silu_f32(g) * u * rw;
+        }
+        float* out = (float*)S.hq + (size_t)(d.z + lc) * S.N + nt * 128 + wave * 16 + lg * 4;
+        *(float4*)out = make_float4(h[0], h[1], h[2], h[3]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          float* out = (float*)S.y + (size_t)(d.z + lc) * S.N + nt * 256 + wave * 32 + s * 16 + lg * 4;
+          *(float4*)out = make_float4(acc[s][0] * rw, acc[s][1] * rw,
+                                      acc[s][2] * rw, acc[s][3] * rw);
+        }
+      }
+    }
+    acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+
+  auto step = [&](int st, ASet& acur, ASet& aload, BSetD& bcur, BSetD& bload) {
+    const int buf = st & 1;
+    {  // activations -> LDS as bf16 (mode 1: hi and lo halves), rows past
+       // the tile zeroed
+      const uint32_t m = a_row < crows ? ~0u : 0u;
+      if constexpr (MODE == 0) {
+        *(u32x2*)(a_hi[buf] + a_row * SD_LS + a_col) =
+            (u32x2){acur.v.x & m, acur.v.y & m};
+      } else {
+        float f[4] = {__uint_as_float(acur.v.x & m), __uint_as_float(acur.v.y & m),
+                      __uint_as_float(acur.v.z & m), __uint_as_float(acur.v.w & m)};
+        uint32_t hb[4], lb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hb[j] = f32_to_bf16(f[j]);
+          lb[j] = f32_to_bf16(f[j] - __uint_as_float(hb[j] << 16));
+        }
+        *(u32x2*)(a_hi[buf] + a_row * SD_LS + a_col) =
+            (u32x2){hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+        *(u32x2*)(a_lo[buf] + a_row * SD_LS + a_col) =
+            (u32x2){lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+      }
+    }
+    __syncthreads();
+    prefetch(aload, bload);
+    f32x4 part[2];
+    part[0] = part[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      const int ko = lg * 32 + mm * 8;
+      const bf16x8 xh = *(const bf16x8*)(a_hi[buf] + lc * SD_LS + ko);
+      bf16x8 xl;
+      if constexpr (MODE == 1) xl = *(const bf16x8*)(a_lo[buf] + lc * SD_LS + ko);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        bf16x8 wv;
+        if constexpr (BF == SF_FP4) {
+          wv = fp4x8_to_bf16((uint32_t)bcur.v[s][mm], e8m0_f32((bcur.sc >> (8 * s)) & 0xFF));
+        } else {
+          wv = fp8x8_to_bf16((uint32_t)bcur.v[s][2 * mm], (uint32_t)bcur.v[s][2 * mm + 1]);
+        }
+        f32x4& tgt = BF == SF_FP4 ? acc[s] : part[s];
+        tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xh, tgt, 0, 0, 0);
+        if constexpr (MODE == 1)
+          tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xl, tgt, 0, 0, 0);
+      }
+    }
+    if constexpr (BF != SF_FP4) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        acc[0][v] = fmaf(part[0][v], bcur.sb0, acc[0][v]);
+        acc[1][v] = fmaf(part[1][v], bcur.sb1, acc[1][v]);
+      }
+    }
+    if (++ckb == cKB) {
+      epilogue(ci);
+      ckb = 0;
+      if (ci + 1 < nitems) c_enter(++ci);
+    }
+  };
+
+  BSetD b0, b1, b2, b3;
+  ASet a0, a1, a2, a3;
+  p_enter(0);
+  c_enter(0);
+  prefetch(a0, b0);
+  prefetch(a1, b1);
+  prefetch(a2, b2);
+  int st = 0;
+  for (; st + 4 <= total_steps; st += 4) {
+    step(st, a0, a3, b0, b3);
+    step(st + 1, a1, a0, b1, b0);
+    step(st + 2, a2, a1, b2, b1);
+    step(st + 3, a3, a2, b3, b2);
+  }
+  if (st < total_steps) step(st, a0, a3, b0, b3);
+  if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
+  if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+}
+
 static int num_cus() {
   static int n = 0;
   if (n == 0) {
@@ -630,6 +957,51 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
     if (bf == SF_FP8_F32S) GO(SF_FP8_F32S, 1);
     if (bf == SF_FP8_POW2) GO(SF_FP8_POW2, 1);
     GO(SF_FP4, 1);
+  }
+#undef GO
+}
+
+template <int BF, int MODE>
+static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
+                         float limit, long upper_items, hipStream_t st) {
+  const long per_xcd = (upper_items + 7) / 8;
+  long nx = (num_cus() + 7) / 8;
+  const long need = (per_xcd + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
+  if (need > nx) nx = need;
+  const long grid = 8 * nx;
+  SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
+  SegDesc dummy = s0;
+  moe_stream_dec_kernel<BF, MODE><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
+                      int topk, float limit, long upper_items,
+                      hipStream_t st) {
+  SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1),
+               "stream decode gemm: bad format");
+  const int ntw = mode == 0 ? 128 : 256;
+  for (const SegDesc* s : {&s0, s1}) {
+    if (!s) continue;
+    SLLM_REQUIRE(s->a && s->wp && s->s0 && s->N % ntw == 0 &&
+                     s->K % 128 == 0 && s->K > 0,
+                 "stream decode gemm: bad segment (N=%d K=%d)", s->N, s->K);
+    SLLM_REQUIRE(mode == 1 ? s->y != nullptr : s->hq != nullptr,
+                 "stream decode gemm: missing outputs");
+    SLLM_REQUIRE(bf == SF_FP4 || mode == 1 || s->s1,
+                 "stream decode gemm: missing W3 scales");
+    SLLM_REQUIRE((!s->gather && !s->row_w_by_idx) || s->sorted_idx,
+                 "stream decode gemm: gather / row_w_by_idx need sorted_idx");
+  }
+#define GO(B, M) return go_stream_dec<B, M>(s0, s1, topk, limit, upper_items, st)
+  if (mode == 0) {
+    if (bf == SF_FP4) GO(SF_FP4, 0);
+    GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales
+  } else {
+    if (bf == SF_FP4) GO(SF_FP4, 1);
+    GO(SF_FP8_F32S, 1);
   }
 #undef GO
 }

@@ -72,6 +72,15 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
                   hipStream_t st);
+// Decode variant over the same packed weights: 16-row tiles, weights
+// converted to bf16 in registers and multiplied by unquantized activations
+// with bf16 MFMAs. mode 0 reads bf16 rows (a, row stride K elements) and
+// writes fp32 h rows to hq (as float*); mode 1 reads fp32 h rows (a as
+// float*, split into bf16 hi + lo) and writes fp32 rows to y (as float*).
+// bf: 0 / 1 fp8 (block scales applied in fp32), 2 MXFP4.
+int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
+                      int topk, float limit, long upper_items,
+                      hipStream_t st);
 long packed_bytes(int fp4, int up, int E, int N, int K);
 long packed_scale_bytes(int up, int E, int N, int K);
 

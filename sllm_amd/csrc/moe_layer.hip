@@ -21,6 +21,7 @@ namespace sllm {
 
 constexpr int PREFILL_BM = 128;
 constexpr int DECODE_MAX_T = 64;
+constexpr int DECODE_BM = 16;
 
 struct Plan {
   bool decode;
@@ -48,8 +49,8 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.decode = force_gemv || pick_decode(mode, T);
   p.N = T * topk;
   if (p.decode) {
-    p.bm = p.N;  // one tile per touched expert
-    p.max_tiles = E < p.N ? E : p.N;
+    p.bm = DECODE_BM;  // 16-row tiles: a touched expert's rows, mostly one tile
+    p.max_tiles = (p.N + DECODE_BM - 1) / DECODE_BM + (E < p.N ? E : p.N);
   } else {
     p.bm = PREFILL_BM;
     p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N);
@@ -214,6 +215,42 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
     if (sh) STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
           launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr, nullptr,
           (const uint16_t*)a->sgl, gate, st));
+    float* y_sh = nullptr;
+    if (a->wgu_packed) {
+      // streamed packed weights (routed and shared segments in one launch
+      // per projection), unquantized activations
+      SLLM_REQUIRE(a->wd_packed && (!sh || (a->sgu_packed && a->sd_packed)),
+                   "sllm_moe_qwen_forward: packed weights incomplete");
+      float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
+      y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
+      const long sh_rt = sh ? (T + DECODE_BM - 1) / DECODE_BM : 0;
+      SegDesc r1{}, s1{};
+      r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
+      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
+      r1.N = I; r1.K = H; r1.hq = (uint8_t*)h;
+      s1.a = (const uint8_t*)a->x; s1.total_rows = T;
+      s1.wp = (const uint8_t*)a->sgu_packed; s1.s0 = a->sg_s; s1.s1 = a->su_s;
+      s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+            launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k, 0.f,
+                              (long)p.max_tiles * (I / 128) + sh_rt * (Is / 128),
+                              st));
+      SegDesc r2{}, s2{};
+      r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
+      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
+      r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
+      s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
+      s2.wp = (const uint8_t*)a->sd_packed; s2.s0 = a->sd_s; s2.N = H;
+      s2.K = Is; s2.row_w = gate; s2.y = (uint16_t*)y_sh;
+      STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+            launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
+                              (long)p.max_tiles * (H / 256) + sh_rt * (H / 256),
+                              st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
+    } else {
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
           p.max_tiles, offsets, (const uint8_t*)a->wg, a->wg_s,
@@ -222,7 +259,6 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
           launch_gemv(wf, 0, h, 0, 0, sorted, k, p.N, tiles, ntiles, p.max_tiles,
           offsets, (const uint8_t*)a->wd, a->wd_s, nullptr, nullptr,
           H, I, w, 0.f, y, st));
-    float* y_sh = nullptr;
     if (sh) {
       float* h_sh = (float*)(ws + p.hq_sh);
       y_sh = (float*)(ws + p.y_sh);
@@ -235,6 +271,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
             launch_gemv(wf, 0, h_sh, 0, 0, nullptr, k, T, nullptr, nullptr, 1,
             nullptr, (const uint8_t*)a->sd, a->sd_s, nullptr,
             nullptr, H, Is, gate, 0.f, y_sh, st));
+    }
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
@@ -367,7 +404,50 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
         launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
                        ntiles, p.max_tiles, ws + p.pscr, st));
 
-  if (p.decode) {
+  if (p.decode && a->w13_packed) {
+    // streamed packed weights, unquantized activations; the route weight
+    // scales the down projection's rows as in the GEMV decode below
+    SLLM_REQUIRE(a->w13_s_packed && a->w2_packed && a->w2_s_packed &&
+                     (!sh || (a->s13_packed && a->s2_packed)),
+                 "sllm_moe_ds_forward: packed weights incomplete");
+    float* h = (float*)(ws + p.hq);
+    float* y = (float*)(ws + p.y);
+    float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
+    float* y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
+    const long sh_rt = (T + DECODE_BM - 1) / DECODE_BM;
+    SegDesc r1{};
+    r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
+    r1.tile_info = tiles; r1.num_tiles = ntiles;
+    r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
+    r1.N = I; r1.K = H; r1.hq = (uint8_t*)h;
+    SegDesc r2{};
+    r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
+    r2.tile_info = tiles; r2.num_tiles = ntiles;
+    r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
+    r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
+          launch_stream_dec(2, 0, r1, nullptr, k, L,
+                            (long)p.max_tiles * (I / 128), st));
+    STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
+          launch_stream_dec(2, 1, r2, nullptr, k, 0.f,
+                            (long)p.max_tiles * (H / 256), st));
+    if (sh) {
+      SegDesc s1{};
+      s1.a = (const uint8_t*)a->x; s1.total_rows = T;
+      s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
+      s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
+      SegDesc s2{};
+      s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
+      s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
+      s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
+            launch_stream_dec(1, 0, s1, nullptr, k, L, sh_rt * (Is / 128), st));
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
+            launch_stream_dec(1, 1, s2, nullptr, k, 0.f, sh_rt * (H / 256), st));
+    }
+    STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+          launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
+  } else if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
