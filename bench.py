@@ -39,6 +39,12 @@ PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E
 PEAK_FP8_TFLOPS = 5033.0        # MI355X dense FP8 MFMA (no sparsity)
 
 C2 = dict(T=4096, H=2048, E=512, I=512, Is=512, k=10)
+# DeepSeek-style MXFP4 prefill (routed e2m1 + e8m0/32, FP8 ue8m0-scaled shared
+# expert, sigmoid scoring with selection bias, group-limited top-k)
+C4 = dict(T=8192, H=7168, E=256, I=2048, Is=2048, k=8, n_group=8,
+          topk_group=4, route_scale=2.5, swiglu_limit=10.0)
+# C2 shapes at 16384 tokens with Zipf-skewed routing
+C5 = dict(C2, T=16384)
 
 
 def log(*a):
@@ -113,6 +119,215 @@ def layer_call(layer, x, out, ws, T, mode, debug=None, stage_events=None):
     qwen_forward_dev(x, out, layer.w, T=T, H=c["H"], E=c["E"], I=c["I"],
                      Is=c["Is"], topk=c["k"], mode=mode, out_f32=False,
                      workspace=ws, debug=debug, stage_events=stage_events)
+
+
+class DeviceLayerDS:
+    """Synthetic C4 layer on the device: routed N(0, 0.02) weights quantized
+    to MXFP4 (e2m1 + e8m0 per 32, s = 2^ceil(log2(amax/6))), shared expert
+    FP8 with power-of-two 128x128 scales, router bf16 N(0, 0.02), selection
+    bias N(0, 0.01); all packed into the streaming layout."""
+
+    def __init__(self, cfg, seed=0):
+        import numpy as np
+        from sllm_amd import _lib
+        from sllm_amd.moe import pack_weights
+        from sllm_amd.runtime import (DeviceBuffer, fill_normal, sync, to_bf16,
+                                      to_device_raw)
+        self.cfg = cfg
+        H, E, I, Is = cfg["H"], cfg["E"], cfg["I"], cfg["Is"]
+        L = _lib.lib()
+        tmp = DeviceBuffer(E * I * H * 4)
+        w = {}
+        sub = [0]
+
+        def q4(rows, cols):
+            n = rows * cols
+            fill_normal(tmp, n, seed * 1000 + 500 + sub[0], 0.02)
+            sub[0] += 1
+            q, sc = DeviceBuffer(n // 2), DeviceBuffer(n // 32)
+            _lib.check(L.sllm_quantize_weight_mxfp4(tmp.ptr, rows, cols, q.ptr,
+                                                    sc.ptr, None), "quantize")
+            return q, sc
+
+        def q8(rows, cols):
+            n = rows * cols
+            fill_normal(tmp, n, seed * 1000 + 500 + sub[0], 0.02)
+            sub[0] += 1
+            q, sc = DeviceBuffer(n), DeviceBuffer((rows // 128) * (cols // 128) * 4)
+            _lib.check(L.sllm_quantize_weight_fp8(tmp.ptr, rows, cols, 1, q.ptr,
+                                                  sc.ptr, None), "quantize")
+            return q, sc
+
+        w1, w1s = q4(E * I, H)
+        w3, w3s = q4(E * I, H)
+        w2, w2s = q4(E * H, I)
+        w["w13_packed"], w["w13_s_packed"] = pack_weights(1, 1, w1, w3, E, I, H, w1s, w3s)
+        w["w2_packed"], w["w2_s_packed"] = pack_weights(1, 0, w2, None, E, H, I, w2s)
+        sync()
+        w["w1"], w["w3"], w["w2"] = w1, w3, w2
+        w["w1_s"], w["w3_s"], w["w2_s"] = w1s, w3s, w2s
+        s1, w["s1_s"] = q8(Is, H)
+        s3, w["s3_s"] = q8(Is, H)
+        s2, w["s2_s"] = q8(H, Is)
+        w["s13_packed"], _ = pack_weights(0, 1, s1, s3, 1, Is, H)
+        w["s2_packed"], _ = pack_weights(0, 0, s2, None, 1, H, Is)
+        w["s1"], w["s3"], w["s2"] = s1, s3, s2
+        sync()
+        tmp.free()
+        rng = np.random.default_rng(seed)
+        w["router_w"] = to_device_raw(to_bf16((rng.standard_normal((E, H)) * 0.02)
+                                              .astype(np.float32)))
+        w["bias"] = to_device_raw((rng.standard_normal(E) * 0.01).astype(np.float32))
+        self.w = w
+        self.rng = rng
+
+
+def ds_call(layer, x, out, ws, T, mode, debug=None, stage_events=None):
+    from sllm_amd.moe import deepseek_forward_dev
+    c = layer.cfg
+    deepseek_forward_dev(x, out, layer.w, T=T, H=c["H"], E=c["E"], I=c["I"],
+                         Is=c["Is"], topk=c["k"], mode=mode, out_f32=False,
+                         n_group=c["n_group"], topk_group=c["topk_group"],
+                         scoring="sigmoid", route_scale=c["route_scale"],
+                         swiglu_limit=c["swiglu_limit"], workspace=ws,
+                         debug=debug, stage_events=stage_events)
+
+
+def _time_layer(call, steps, warmup):
+    from sllm_amd.runtime import Event, sync
+    for _ in range(warmup):
+        call()
+    sync()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / steps
+
+
+def _stage_times(call_with_events, nstages, reps=10):
+    from sllm_amd.moe import STAGES
+    from sllm_amd.runtime import Event
+    evs = [Event() for _ in range(2 * nstages)]
+    per = {s: [] for s in STAGES}
+    for _ in range(reps):
+        call_with_events(evs)
+        evs[-1].synchronize()
+        for i, s in enumerate(STAGES):
+            per[s].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]))
+    return {s: round(statistics.median(v), 4) for s, v in per.items()}
+
+
+def run_c4(args):
+    """C4 prefill: one JSON line for this configuration (not the headline)."""
+    import numpy as np
+    from sllm_amd.moe import STAGES, deepseek_workspace_bytes
+    from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
+    c = dict(C4)
+    T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
+    t0 = time.perf_counter()
+    layer = DeviceLayerDS(c, seed=args.seed)
+    x = to_device_raw(to_bf16(layer.rng.standard_normal((T, H)).astype(np.float32)))
+    out = DeviceBuffer(T * H * 2)
+    ws = DeviceBuffer(deepseek_workspace_bytes(T, H, E, I, Is, k, "prefill"))
+    cnt = DeviceBuffer(E * 4)
+    ds_call(layer, x, out, ws, T, "prefill", debug={"counts_out": cnt})
+    sync()
+    touched = int((cnt.copy_host_raw(np.int32, (E,)) > 0).sum())
+    log(f"C4 setup {time.perf_counter() - t0:.1f}s, touched {touched}")
+    ms = _time_layer(lambda: ds_call(layer, x, out, ws, T, "prefill"),
+                     args.steps, args.warmup)
+    st = _stage_times(lambda ev: ds_call(layer, x, out, ws, T, "prefill",
+                                         stage_events=ev), len(STAGES))
+    flops = 6 * H * I * T * k + 6 * H * Is * T
+    wbytes = touched * 3 * H * I // 2 + touched * 3 * H * I // 32
+    bytes_ = wbytes + 3 * H * Is + E * H * 2 + 2 * T * H * 2
+    up_bytes = touched * (2 * I * H // 2 + 2 * I * H // 32) + T * H + T * k * I
+    up_flops = 4 * H * I * T * k
+    t_up = st["expert_up"] / 1e3
+    res = {"metric": "C4 MoE layer tokens/s (prefill)", "value": round(T / (ms / 1e3), 1),
+           "unit": "tokens/s", "ms_per_step": round(ms, 4), "steps": args.steps,
+           "config": {"workload": "C4 DeepSeek-style MXFP4 MoE layer, prefill", **c},
+           "layer": {"flops": flops, "bytes": bytes_,
+                     "mfma_frac_fp8_rate": round(flops / (ms / 1e3) / (PEAK_FP8_TFLOPS * 1e12), 4),
+                     "hbm_frac": round(bytes_ / (ms / 1e3) / (PEAK_HBM_GBPS * 1e9), 4),
+                     "stage_ms": st, "touched_experts": touched},
+           "expert_up": {"algorithmic_bytes": up_bytes, "ms": st["expert_up"],
+                         "GBps": round(up_bytes / t_up / 1e9, 1),
+                         "TFLOPs": round(up_flops / t_up / 1e12, 1),
+                         "mfma_frac_fp8_rate": round(up_flops / t_up / (PEAK_FP8_TFLOPS * 1e12), 4)}}
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def run_c5(args):
+    """C5: C2 shapes at T=16384 with Zipf-skewed routing (logit bias
+    -beta ln(rank_e), ranks a seeded permutation of 1..E, beta calibrated so
+    the top 10% of experts take ~60% of assignments); logits are computed on
+    the host and passed in, so the timed layer excludes the router GEMM."""
+    import numpy as np
+    from sllm_amd.moe import STAGES, qwen_workspace_bytes
+    from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
+    c = dict(C5)
+    T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
+    t0 = time.perf_counter()
+    layer = DeviceLayer(c, seed=args.seed)
+    xh = to_bf16_values(layer.rng.standard_normal((T, H)).astype(np.float32))
+    rwh = to_bf16_values(layer.router_w_host)
+    logits0 = (xh @ rwh.T).astype(np.float32)
+    rank = layer.rng.permutation(E) + 1
+    top = E // 10
+
+    def share(beta, n=2048):
+        lg = logits0[:n] - beta * np.log(rank)[None, :]
+        ids = np.argpartition(-lg, k, axis=1)[:, :k]
+        cnt = np.bincount(ids.ravel(), minlength=E)
+        return np.sort(cnt)[::-1][:top].sum() / cnt.sum()
+
+    lo, hi = 0.0, 10.0
+    for _ in range(40):
+        mid = 0.5 * (lo + hi)
+        lo, hi = (mid, hi) if share(mid) < 0.6 else (lo, mid)
+    beta = 0.5 * (lo + hi)
+    logits = (logits0 - beta * np.log(rank)[None, :]).astype(np.float32)
+    x = to_device_raw(to_bf16(xh))
+    lg = to_device_raw(logits)
+    out = DeviceBuffer(T * H * 2)
+    ws = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, "prefill",
+                                           logits_given=True))
+    from sllm_amd.moe import qwen_forward_dev
+
+    def call(debug=None, ev=None):
+        qwen_forward_dev(x, out, layer.w, T=T, H=H, E=E, I=I, Is=Is, topk=k,
+                         mode="prefill", out_f32=False, logits=lg, workspace=ws,
+                         debug=debug, stage_events=ev)
+    cnt = DeviceBuffer(E * 4)
+    call(debug={"counts_out": cnt})
+    sync()
+    counts = cnt.copy_host_raw(np.int32, (E,))
+    touched = int((counts > 0).sum())
+    share_top = float(np.sort(counts)[::-1][:top].sum() / counts.sum())
+    log(f"C5 setup {time.perf_counter() - t0:.1f}s, beta {beta:.3f}, top-10% share "
+        f"{share_top:.3f}, empty experts {E - touched}")
+    ms = _time_layer(call, args.steps, args.warmup)
+    st = _stage_times(lambda ev: call(ev=ev), len(STAGES))
+    flops = 6 * H * I * T * k + 6 * H * Is * T
+    wbytes = touched * 3 * H * I + touched * 3 * (H // 128) * (I // 128) * 4
+    bytes_ = wbytes + 3 * H * Is + 2 * T * H * 2 + T * E * 4
+    res = {"metric": "C5 MoE layer tokens/s (prefill, skewed routing, logits given)",
+           "value": round(T / (ms / 1e3), 1), "unit": "tokens/s",
+           "ms_per_step": round(ms, 4), "steps": args.steps,
+           "config": {"workload": "C5 Qwen-style FP8 MoE layer, Zipf-skewed prefill", **c,
+                      "beta": round(beta, 4), "top10pct_share": round(share_top, 4),
+                      "empty_experts": E - touched},
+           "layer": {"flops": flops, "bytes": bytes_,
+                     "mfma_frac": round(flops / (ms / 1e3) / (PEAK_FP8_TFLOPS * 1e12), 4),
+                     "hbm_frac": round(bytes_ / (ms / 1e3) / (PEAK_HBM_GBPS * 1e9), 4),
+                     "stage_ms": st, "touched_experts": touched}}
+    print(json.dumps(res), flush=True)
+    return 0
 
 
 # --------------------------------------------------------------------------
@@ -229,6 +444,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--config", choices=("c2", "c4", "c5"), default="c2",
+                    help="c2 (default): the headline line; c4 / c5: one line "
+                         "for that configuration instead")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run the library's copy kernel over MIB MiB five "
                          "times (the known-size reference for scaling HBM "
@@ -260,6 +478,10 @@ def main(argv=None) -> int:
         sync()
         print(json.dumps({"copy_calib_bytes": nb, "launches": 5}))
         return 0
+    if args.config == "c4":
+        return run_c4(args)
+    if args.config == "c5":
+        return run_c5(args)
 
     c = dict(C2)
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]

@@ -198,11 +198,13 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const float eps = a->renorm_eps;
 
   const StageClock clk{a->stage_events, st};
-  if (!a->logits_given)
-    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
-          launch_router_gemm((const uint16_t*)a->x,
-                             (const uint16_t*)a->router_w, logits, T, E, H,
-                             st));
+  // with caller-provided logits the router stage is recorded with zero
+  // length, so every stage's events exist on every call
+  STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+        a->logits_given ? 0
+                        : launch_router_gemm((const uint16_t*)a->x,
+                                             (const uint16_t*)a->router_w,
+                                             logits, T, E, H, st));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
         launch_route_softmax(logits, w, ids, T, E, k, eps, st));
   STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
@@ -392,11 +394,13 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   int* ntiles = (int*)(ws + p.ntiles);
 
   const StageClock clk{a->stage_events, st};
-  if (!a->logits_given)
-    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
-          launch_router_gemm((const uint16_t*)a->x,
-                             (const uint16_t*)a->router_w, logits, T, E, H,
-                             st));
+  // with caller-provided logits the router stage is recorded with zero
+  // length, so every stage's events exist on every call
+  STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+        a->logits_given ? 0
+                        : launch_router_gemm((const uint16_t*)a->x,
+                                             (const uint16_t*)a->router_w,
+                                             logits, T, E, H, st));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
         launch_route_grouped(logits, a->bias, w, ids, T, E, k, a->n_group,
                              a->topk_group, a->scoring, a->route_scale, st));

@@ -129,7 +129,7 @@ def qwen_layer(W, top_k, packed=True):
     from sllm_amd.moe import QwenMoE
     kw = {"packed": packed}
     if W.has_shared:
-        kw = dict(sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
+        kw.update(sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
                   sd_s=W.sd_s, sgl=W.sgl)
     return QwenMoE(W.router_w, W.wg_q, W.wu_q, W.wd_q, W.wg_s, W.wu_s,
                    W.wd_s, top_k=top_k, **kw)
@@ -166,7 +166,7 @@ def deepseek_layer(W, top_k, packed=True, **route):
     from sllm_amd.moe import DeepseekMoE
     kw = {"packed": packed}
     if W.has_shared:
-        kw = dict(s1=W.s1_q, s1_s=W.s1_s, s3=W.s3_q, s3_s=W.s3_s, s2=W.s2_q,
+        kw.update(s1=W.s1_q, s1_s=W.s1_s, s3=W.s3_q, s3_s=W.s3_s, s2=W.s2_q,
                   s2_s=W.s2_s)
     return DeepseekMoE(W.router_w, W.bias, W.w1_p, W.w1_s, W.w3_p, W.w3_s,
                        W.w2_p, W.w2_s, top_k=top_k, **kw, **route)
