@@ -178,6 +178,31 @@ struct Stream {
   static constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
 };
 
+// Scheduling pattern of one prefill step: before each of the eight pairs of
+// MFMAs (one 16-row group), one or two of the step's prefetch loads. Spreading the loads keeps the workgroup's
+// burst of vector loads after the barrier from backing up the address unit
+// while the matrix cores idle.
+#define ST_SCHED_GROUP(nv)                                   \
+  do {                                                       \
+    if ((nv) > 0) __builtin_amdgcn_sched_group_barrier(0x0020, (nv), 0); \
+    __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);      \
+  } while (0)
+
+template <int NV>
+__device__ __forceinline__ void st_sched_pattern() {
+  // NV prefetch loads over eight groups: the first NV - 8 groups take two
+  constexpr int e = NV > 8 ? NV - 8 : 0;
+  constexpr int one = NV > 8 ? 1 : 0;
+  ST_SCHED_GROUP(e > 0 ? 2 : (0 < NV ? 1 : 0));
+  ST_SCHED_GROUP(e > 1 ? 2 : (1 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 2 ? 2 : (2 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 3 ? 2 : (3 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 4 ? 2 : (4 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 5 ? 2 : (5 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 6 ? 2 : (6 < NV || one ? 1 : 0));
+  ST_SCHED_GROUP(e > 7 ? 2 : (7 < NV || one ? 1 : 0));
+}
+
 // item descriptor in LDS: x = seg | nt << 1, y = e, z = row_begin, w = rows
 template <int BF, int MODE>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
@@ -453,11 +478,6 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
       for (int s = 0; s < 2; ++s) acc[mi][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
   };
 
-  auto prefetch = [&](ASet& af, BSet<BF>& bf) {
-    fetch_a(af);
-    load_b(bf);
-    p_advance();
-  };
 
   // ---- one pipeline step ----------------------------------------------------
   auto step = [&](int st, ASet& acur, ASet& aload, BSet<BF>& bcur,
@@ -478,10 +498,14 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     __syncthreads();
     // both operands are prefetched three steps ahead; the activations of a
     // step are consumed before its weights, so they are issued first. The
-    // batch is kept in one piece and in the same order in every step and in
-    // the prologue, so the compiler's count of younger loads at each wait is
-    // the same on every path into it.
-    prefetch(aload, bload);
+    // batch is issued in the same order in every step and in the prologue,
+    // so the compiler's count of younger loads at each wait is the same on
+    // every path into it; the cursor advances before the loads (its item
+    // change is a branch), keeping the loads, LDS reads and MFMAs in one
+    // scheduling region.
+    p_advance();
+    fetch_a(aload);
+    load_b(bload);
     // compute step st over all eight 16-row groups: rows past the tile are
     // zero in LDS, and a branch-free step lets the compiler issue the LDS
     // reads of the next groups ahead of the MFMAs of the current one.
@@ -540,6 +564,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
           acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
       }
     }
+    st_sched_pattern<BF == SF_FP4 ? 6 : 9>();
     if (++ckb == cKB) {
       epilogue(ci, buf ^ 1);
       ckb = 0;
@@ -556,9 +581,14 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   ASet a0, a1, a2, a3;
   p_enter(0);
   c_enter(0);
-  prefetch(a0, b0);
-  prefetch(a1, b1);
-  prefetch(a2, b2);
+  fetch_a(a0);
+  load_b(b0);
+  p_advance();
+  fetch_a(a1);
+  load_b(b1);
+  p_advance();
+  fetch_a(a2);
+  load_b(b2);
   int st = 0;
   for (; st + 4 <= total_steps; st += 4) {
     step(st, a0, a3, b0, b3);
