@@ -313,12 +313,17 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
       ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
     } else {
       pb = S.wp + blk0 * Stream<BF, MODE>::BLK + (wave * 4) * 1024 + lane * 16;
+      // the block scales are wave-uniform: read through the scalar cache
+      // (constant address space), off the vector memory path
+      const int ue = __builtin_amdgcn_readfirstlane(d.y);
+      const int unt = __builtin_amdgcn_readfirstlane(nt);
       if constexpr (MODE == 0) {
-        ps0 = (const float*)S.s0 + blk0;  // NT = N / 128: scale row (e, nt)
-        ps1 = (const float*)S.s1 + blk0;
+        const size_t ub0 = ((size_t)ue * NT + unt) * KB;  // NT = N / 128
+        ps0 = (const float*)S.s0 + ub0;
+        ps1 = (const float*)S.s1 + ub0;
       } else {
-        const int nblk = nt * 2 + wave / 4;  // the wave's 32 columns' block
-        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB;
+        const int nblk = unt * 2 + __builtin_amdgcn_readfirstlane(wave) / 4;
+        ps0 = ps1 = (const float*)S.s0 + ((size_t)ue * (N / 128) + nblk) * KB;
       }
     }
   };
@@ -355,8 +360,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
       b.sc = 0;
-      b.sb0 = ps0[pkb];
-      b.sb1 = MODE == 0 ? ps1[pkb] : b.sb0;
+      typedef const __attribute__((address_space(4))) float* cfp;
+      b.sb0 = ((cfp)ps0)[pkb];
+      b.sb1 = MODE == 0 ? ((cfp)ps1)[pkb] : b.sb0;
     }
   };
 
@@ -564,7 +570,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
           acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
       }
     }
-    st_sched_pattern<BF == SF_FP4 ? 6 : 9>();
+    st_sched_pattern<BF == SF_FP4 ? 6 : 7>();
     if (++ckb == cKB) {
       epilogue(ci, buf ^ 1);
       ckb = 0;
