@@ -573,6 +573,17 @@ def main(argv=None) -> int:
             decode[str(B)] = {"us": round(us, 2), "touched_experts": tb,
                               "bytes": nb, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
                               "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+            if B == 32:  # per-stage breakdown (flushed like the timed calls)
+                evs = [Event() for _ in range(2 * len(STAGES))]
+                per = {s_: [] for s_ in STAGES}
+                for it in range(10):
+                    memset(flush, it & 0xFF, flush.nbytes)
+                    layer_call(layer, xb, ob, wsb, B, "decode", stage_events=evs)
+                    evs[-1].synchronize()
+                    for i, s_ in enumerate(STAGES):
+                        per[s_].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3)
+                decode[str(B)]["stage_us"] = {s_: round(statistics.median(v), 2)
+                                              for s_, v in per.items()}
             log(f"decode B={B}: {us:.1f} us, touched {tb}, "
                 f"{decode[str(B)]['GBps']} GB/s")
 

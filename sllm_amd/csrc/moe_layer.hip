@@ -198,25 +198,49 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const float eps = a->renorm_eps;
 
   const StageClock clk{a->stage_events, st};
-  // with caller-provided logits the router stage is recorded with zero
-  // length, so every stage's events exist on every call
-  STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
-        a->logits_given ? 0
-                        : launch_router_gemm((const uint16_t*)a->x,
-                                             (const uint16_t*)a->router_w,
-                                             logits, T, E, H, st));
-  STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-        launch_route_softmax(logits, w, ids, T, E, k, eps, st));
-  STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
-        launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
-                       ntiles, p.max_tiles, ws + p.pscr, st));
+  // Decode-size routing: the router GEMM also computes the shared-expert
+  // gate, and softmax top-k runs fused with the permutation (two launches
+  // instead of four). Stages a call does not run are recorded with zero
+  // length, so every stage's events exist on every call.
+  const bool small_router = p.decode && !a->logits_given && T <= 64;
+  const bool small_route = p.decode && route_permute_small_fits(T, E, k);
+  bool gate_done = false;
+  if (small_router) {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+          launch_router_small_gate((const uint16_t*)a->x,
+                                   (const uint16_t*)a->router_w, logits, T, E,
+                                   H, sh ? (const uint16_t*)a->sgl : nullptr,
+                                   sh ? gate : nullptr, st));
+    gate_done = sh;
+  } else {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
+          a->logits_given ? 0
+                          : launch_router_gemm((const uint16_t*)a->x,
+                                               (const uint16_t*)a->router_w,
+                                               logits, T, E, H, st));
+  }
+  if (small_route) {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTE,
+          launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
+                                     counts, offsets, sorted, inv, tiles,
+                                     ntiles, p.max_tiles, st));
+    STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
+  } else {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTE,
+          launch_route_softmax(logits, w, ids, T, E, k, eps, st));
+    STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
+          launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
+                         tiles, ntiles, p.max_tiles, ws + p.pscr, st));
+  }
 
   if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);
-    if (sh) STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
-          launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr, nullptr,
-          (const uint16_t*)a->sgl, gate, st));
+    STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
+          (sh && !gate_done)
+              ? launch_act_quant((const uint16_t*)a->x, T, H, 0, nullptr,
+                                 nullptr, (const uint16_t*)a->sgl, gate, st)
+              : 0);
     float* y_sh = nullptr;
     if (a->wgu_packed) {
       // streamed packed weights (routed and shared segments in one launch

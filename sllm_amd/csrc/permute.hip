@@ -11,7 +11,8 @@
 // then ascending flat assignment index a = t*k + j, i.e.
 // np.argsort(ids.ravel(), kind="stable").
 //
-// Three kernels, all deterministic:
+// Small problems use one fused workgroup (permute_fused_kernel); otherwise
+// three kernels, all deterministic:
 //  1. hist:    chunks of PERM_CHUNK assignments, LDS histogram per chunk.
 //  2. scan:    one workgroup; per-expert exclusive scan over chunks, then an
 //              exclusive scan over experts (offsets), chunk bases, and the
@@ -22,6 +23,7 @@
 //              ballot per id bit, so the rank among equal ids is the popcount
 //              of lower matching lanes -- a stable, atomic-free scatter.
 #include "launch.h"
+#include "permute_fused.h"
 
 namespace sllm {
 
@@ -41,23 +43,6 @@ __global__ __launch_bounds__(256) void permute_hist_kernel(
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += blockDim.x)
     chunk_hist[(size_t)c * E + e] = h[e];
-}
-
-// Block-wide exclusive scan of one value per thread (1024 threads).
-__device__ int block_excl_scan(int v, int* sh, int& total) {
-  const int tid = threadIdx.x;
-  sh[tid] = v;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    int add = tid >= o ? sh[tid - o] : 0;
-    __syncthreads();
-    sh[tid] += add;
-    __syncthreads();
-  }
-  int incl = sh[tid];
-  total = sh[1023];
-  __syncthreads();
-  return incl - v;
 }
 
 __global__ __launch_bounds__(1024) void permute_scan_kernel(
@@ -167,6 +152,17 @@ __global__ __launch_bounds__(64) void permute_scatter_kernel(
   }
 }
 
+__global__ __launch_bounds__(1024) void permute_fused_kernel(
+    const int* __restrict__ ids, int N, int E, int nbits, int bm,
+    int* __restrict__ counts, int* __restrict__ offsets,
+    int* __restrict__ sorted_idx, int* __restrict__ inv_pos,
+    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles) {
+  __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
+  __shared__ int sh[1024];
+  permute_fused_body(ids, N, E, nbits, bm, counts, offsets, sorted_idx,
+                     inv_pos, tile_info, num_tiles, max_tiles, hist, sh);
+}
+
 size_t permute_scratch_bytes(int N, int E) {
   int nchunks = N > 0 ? (N + PERM_CHUNK - 1) / PERM_CHUNK : 1;
   return align_up((size_t)nchunks * E * sizeof(int), 256);
@@ -186,6 +182,13 @@ int launch_permute(const int* ids, int N, int E, int bm, int* counts,
   const int nchunks = (N + PERM_CHUNK - 1) / PERM_CHUNK;
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
+  if (N <= PERM_FUSED_MAX_N && E <= PERM_FUSED_MAX_E) {
+    permute_fused_kernel<<<1, 1024, 0, st>>>(ids, N, E, nbits, bm, counts,
+                                             offsets, sorted_idx, inv_pos,
+                                             tile_info, num_tiles, max_tiles);
+    SLLM_LAUNCHED();
+    return 0;
+  }
   int* chunk_hist = (int*)scratch;
   const size_t lds = (size_t)E * sizeof(int);
   permute_hist_kernel<<<nchunks, 256, lds, st>>>(ids, N, E, chunk_hist);

@@ -1,0 +1,122 @@
+// Single-workgroup pieces of the expert-major permutation, shared by the
+// permute launches (permute.hip) and the fused decode route + permute
+// kernel (router.hip). Canonical order: ascending expert id, then ascending
+// flat assignment index a = t * k + j.
+#pragma once
+#include "common.h"
+
+namespace sllm {
+
+// Block-wide exclusive scan of one value per thread (1024 threads).
+__device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
+  const int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    int add = tid >= o ? sh[tid - o] : 0;
+    __syncthreads();
+    sh[tid] += add;
+    __syncthreads();
+  }
+  int incl = sh[tid];
+  total = sh[1023];
+  __syncthreads();
+  return incl - v;
+}
+
+// One workgroup of 16 waves (1024 threads) permutes N <= PERM_FUSED_MAX_N
+// assignments over E <= PERM_FUSED_MAX_E experts. Wave w owns the contiguous
+// assignment range [w R, (w + 1) R) and keeps its ids in registers;
+// histogram per wave in LDS, one scan over (expert, wave) for counts,
+// offsets, the tile table and each wave's per-expert base, then every wave
+// scatters its range in order: lanes holding the same expert are matched
+// with one ballot per id bit, so the rank among equal ids is the popcount
+// of lower matching lanes (stable, atomic-free). `ids` may point to global
+// memory or LDS; hist / sh are the workgroup's LDS scratch.
+constexpr int PERM_FUSED_MAX_E = 1024;
+constexpr int PERM_FUSED_WAVES = 16;
+constexpr int PERM_FUSED_G = 4;  // 64-assignment groups per wave
+constexpr int PERM_FUSED_MAX_N = PERM_FUSED_WAVES * PERM_FUSED_G * 64;
+
+__device__ __forceinline__ void permute_fused_body(
+    const int* ids, int N, int E, int nbits, int bm, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted_idx,
+    int* __restrict__ inv_pos, int* __restrict__ tile_info,
+    int* __restrict__ num_tiles, int max_tiles,
+    int (*hist)[PERM_FUSED_MAX_E], int* sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = ((N + PERM_FUSED_WAVES - 1) / PERM_FUSED_WAVES + 63) & ~63;
+  const int a0 = min(N, wave * R), a1 = min(N, a0 + R);
+  int idv[PERM_FUSED_G];
+#pragma unroll
+  for (int g = 0; g < PERM_FUSED_G; ++g) {
+    const int a = a0 + g * 64 + lane;
+    const int v = ids[min(a, N - 1)];
+    idv[g] = a < a1 ? v : -1;
+  }
+  for (int q = tid; q < PERM_FUSED_WAVES * E; q += 1024) hist[q / E][q % E] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < PERM_FUSED_G; ++g) {
+    const int e = idv[g];
+    if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
+  }
+  __syncthreads();
+  int cnt = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < PERM_FUSED_WAVES; ++w) {
+      const int v = hist[w][tid];
+      hist[w][tid] = cnt;
+      cnt += v;
+    }
+  }
+  const int ntile = (tid < E && cnt > 0) ? (cnt + bm - 1) / bm : 0;
+  int tot_rows, tot_tiles;
+  const int off = block_excl_scan(cnt, sh, tot_rows);
+  const int toff = block_excl_scan(ntile, sh, tot_tiles);
+  if (tid < E) {
+    counts[tid] = cnt;
+    offsets[tid] = off;
+#pragma unroll
+    for (int w = 0; w < PERM_FUSED_WAVES; ++w) hist[w][tid] += off;
+    for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
+      const int r0 = i * bm;
+      *(int4*)(tile_info + 4 * (toff + i)) =
+          make_int4(tid, off + r0, min(bm, cnt - r0), 0);
+    }
+  }
+  if (tid == 0) {
+    offsets[E] = tot_rows;
+    *num_tiles = min(tot_tiles, max_tiles);
+  }
+  __syncthreads();
+  // each wave walks its own range with its own base row: program order
+  // within the wave orders the reads and updates of hist[wave][*]
+  int* run = hist[wave];
+  const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int g = 0; g < PERM_FUSED_G; ++g) {
+    const int a = a0 + g * 64 + lane;
+    const int raw = idv[g];
+    const bool valid = raw >= 0 && raw < E;
+    const int e = valid ? raw : 0;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const int bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int start = valid ? run[e] : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const int pos = start + __popcll(peers & lt);
+      sorted_idx[pos] = a;
+      inv_pos[a] = pos;
+      if ((peers >> lane) == 1ull) run[e] = start + __popcll(peers);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+}  // namespace sllm

@@ -17,6 +17,7 @@
 //   s = fp32(1 / (1 + exp(-x))) is evaluated in fp64 as the reference does
 //   (ref/deepseek_v4.py:526-528), ties to the lower expert id.
 #include "launch.h"
+#include "permute_fused.h"
 
 namespace sllm {
 
@@ -135,26 +136,47 @@ __global__ __launch_bounds__(256, 1) void router_gemm_kernel(
 // through LDS.
 constexpr int RG_SMALL_T = 64;
 
+// With gate_out, one extra workgroup (after the E / 16 expert tiles)
+// computes the shared-expert gate sigmoid(x . sgl) of every token (its 16
+// weight rows all read sgl; column 0 is kept).
 __global__ __launch_bounds__(512) void router_gemm_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    float* __restrict__ logits, int T, int E, int H) {
+    float* __restrict__ logits, int T, int E, int H,
+    const uint16_t* __restrict__ sgl, float* __restrict__ gate_out) {
   __shared__ float part[8][RG_SMALL_T][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int e0 = blockIdx.x * 16;
+  const bool gate_tile = e0 >= E;
   const int nti = (T + 15) / 16;
-  const uint16_t* brow = w + (size_t)min(e0 + lr, E - 1) * H + lg * 8;
+  const uint16_t* brow = (gate_tile ? sgl : w + (size_t)min(e0 + lr, E - 1) * H) + lg * 8;
+  const uint16_t* arow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    arow[i] = x + (size_t)min(i * 16 + lr, T - 1) * H + lg * 8;
   f32x4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int k0 = wave * 32; k0 < H; k0 += 256) {
-    const bf16x8 b = *(const bf16x8*)(brow + k0);
+  // the wave's K slices (w, w + 8, ...) in groups of 4, all loads of a group
+  // in flight together (rows past T re-read row T - 1; slices past H are
+  // clamped and skipped)
+  const int nsl = H / 32;
+  for (int g0 = wave; g0 < nsl; g0 += 32) {
+    bf16x8 b[4], a[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < nti) {
-        const bf16x8 a = *(const bf16x8*)(
-            x + (size_t)min(i * 16 + lr, T - 1) * H + k0 + lg * 8);
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[i], 0, 0, 0);
+    for (int j = 0; j < 4; ++j) {
+      const int k0 = min(g0 + 8 * j, nsl - 1) * 32;
+      b[j] = *(const bf16x8*)(brow + k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[j][i] = *(const bf16x8*)(arow[i] + k0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (g0 + 8 * j < nsl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i < nti)
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][i], b[j], acc[i], 0, 0, 0);
       }
     }
   }
@@ -168,21 +190,24 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
     float s = 0.f;
 #pragma unroll
     for (int wv = 0; wv < 8; ++wv) s += part[wv][r][c];
-    if (e0 + c < E) logits[(size_t)r * E + e0 + c] = s;
+    if (gate_tile) {
+      if (c == 0) gate_out[r] = sigmoid_f32(s);
+    } else if (e0 + c < E) {
+      logits[(size_t)r * E + e0 + c] = s;
+    }
   }
 }
 
 // --------------------------------------------------------------------------
 // softmax top-k with renormalisation (ref/qwen4_exp.py:118-140)
 // --------------------------------------------------------------------------
+// One token's softmax top-k on the calling wave: row = the token's E logits;
+// lanes j < topk write slot j of w_row / id_row (and of id_lds when given).
 template <int EPL>
-__global__ __launch_bounds__(256) void route_softmax_kernel(
-    const float* __restrict__ logits, float* __restrict__ w_out,
-    int* __restrict__ id_out, int T, int E, int topk, float eps) {
+__device__ __forceinline__ void route_softmax_token(
+    const float* __restrict__ row, int E, int topk, float eps,
+    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const float* row = logits + (size_t)t * E;
   float v[EPL];
   float m = -INFINITY;
 #pragma unroll
@@ -237,9 +262,45 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
     }
   }
   if (lane < topk) {
-    w_out[(size_t)t * topk + lane] = mine / (wsum + eps);
-    id_out[(size_t)t * topk + lane] = myid;
+    w_row[lane] = mine / (wsum + eps);
+    id_row[lane] = myid;
+    if (id_lds) id_lds[lane] = myid;
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_softmax_kernel(
+    const float* __restrict__ logits, float* __restrict__ w_out,
+    int* __restrict__ id_out, int T, int E, int topk, float eps) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  route_softmax_token<EPL>(logits + (size_t)t * E, E, topk, eps,
+                           w_out + (size_t)t * topk, id_out + (size_t)t * topk,
+                           nullptr);
+}
+
+// Decode (T * topk <= PERM_FUSED_MAX_N, E <= PERM_FUSED_MAX_E): softmax
+// top-k of every token (wave w takes tokens w, w + 16, ...) and the
+// expert-major permutation in one workgroup, the ids passed through LDS.
+template <int EPL>
+__global__ __launch_bounds__(1024) void route_permute_small_kernel(
+    const float* __restrict__ logits, float* __restrict__ w_out,
+    int* __restrict__ id_out, int T, int E, int topk, float eps, int nbits,
+    int bm, int* __restrict__ counts, int* __restrict__ offsets,
+    int* __restrict__ sorted_idx, int* __restrict__ inv_pos,
+    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles) {
+  __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
+  __shared__ int sh[1024];
+  __shared__ int ids_lds[PERM_FUSED_MAX_N];
+  const int wave = threadIdx.x >> 6;
+  for (int t = wave; t < T; t += PERM_FUSED_WAVES)
+    route_softmax_token<EPL>(logits + (size_t)t * E, E, topk, eps,
+                             w_out + (size_t)t * topk,
+                             id_out + (size_t)t * topk, ids_lds + t * topk);
+  __syncthreads();
+  permute_fused_body(ids_lds, T * topk, E, nbits, bm, counts, offsets,
+                     sorted_idx, inv_pos, tile_info, num_tiles, max_tiles,
+                     hist, sh);
 }
 
 // --------------------------------------------------------------------------
@@ -390,11 +451,58 @@ int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
                "router_gemm: need T,E>0 and H %% 128 == 0 (T=%d E=%d H=%d)",
                T, E, H);
   if (T <= RG_SMALL_T) {
-    router_gemm_small_kernel<<<ceil_div(E, 16), 512, 0, st>>>(x, w, logits,
-                                                              T, E, H);
+    router_gemm_small_kernel<<<ceil_div(E, 16), 512, 0, st>>>(
+        x, w, logits, T, E, H, nullptr, nullptr);
   } else {
     dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
     router_gemm_kernel<<<grid, 256, 0, st>>>(x, w, logits, T, E, H);
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
+                             float* logits, int T, int E, int H,
+                             const uint16_t* sgl, float* gate_out,
+                             hipStream_t st) {
+  SLLM_REQUIRE(x && w && logits && T > 0 && T <= RG_SMALL_T && E > 0 &&
+                   H % 32 == 0 && (!gate_out || sgl),
+               "router_small_gate: bad args (T=%d E=%d H=%d)", T, E, H);
+  router_gemm_small_kernel<<<ceil_div(E, 16) + (gate_out ? 1 : 0), 512, 0,
+                             st>>>(x, w, logits, T, E, H, sgl, gate_out);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+// One workgroup routes every token (a wave per token): worth it only while
+// the tokens fit one pass of the 16 waves; larger batches route with the
+// multi-workgroup kernel.
+bool route_permute_small_fits(int T, int E, int topk) {
+  return T <= PERM_FUSED_WAVES && (long)T * topk <= PERM_FUSED_MAX_N &&
+         E <= PERM_FUSED_MAX_E;
+}
+
+int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
+                               int E, int topk, float eps, int bm,
+                               int* counts, int* offsets, int* sorted_idx,
+                               int* inv_pos, int* tile_info, int* num_tiles,
+                               int max_tiles, hipStream_t st) {
+  SLLM_REQUIRE(logits && w && ids && route_permute_small_fits(T, E, topk) &&
+                   topk > 0 && topk <= E && topk <= 64 && T > 0,
+               "route_permute_small: bad sizes (T=%d E=%d k=%d)", T, E, topk);
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  switch (epl_for(E)) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_permute_small_kernel<n><<<1, 1024, 0, st>>>(                        \
+        logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,          \
+        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles);                \
+    break;
+    CASE(1) CASE(2) CASE(4) CASE(8) CASE(16)
+#undef CASE
+    default:
+      SLLM_REQUIRE(false, "route_permute_small: E=%d too large", E);
   }
   SLLM_LAUNCHED();
   return 0;
