@@ -40,6 +40,7 @@ constexpr int ST_LDS = 144;          // A row stride in LDS (128 + 16 pad)
 constexpr int ST_MAX_ITEMS = 32;     // work items per workgroup
 constexpr int ST_WAVES = 8;          // waves per workgroup
 constexpr int ST_THREADS = 64 * ST_WAVES;
+static_assert(ST_THREADS == 4 * ST_BM, "four lanes per activation-scale row");
 
 // ---------------------------------------------------------------------------
 // packed layouts
@@ -306,7 +307,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     pKB = KB;
     pa0 = S.a + (size_t)rsrc[i][a_row0] * K + a_chunk * 16;
     pa1 = S.a + (size_t)rsrc[i][64 + a_row0] * K + a_chunk * 16;
-    psa = S.sa + (size_t)rsrc[i][tid & (ST_BM - 1)] * KB;
+    // four lanes share each activation-scale row, so a wave's scale load
+    // touches 16 rows (cache lines) rather than 64
+    psa = S.sa + (size_t)rsrc[i][tid >> 2] * KB;
     const size_t blk0 = ((size_t)d.y * NT + nt) * KB;
     if constexpr (BF == SF_FP4) {
       pb = S.wp + blk0 * Stream<BF, MODE>::BLK + (wave * 2) * 1024 + lane * 16;
@@ -498,8 +501,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
         *(uint4*)(a_lds[buf] + r * ST_LDS + a_chunk * 16) =
             make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
       }
-      const uint32_t ms = tid < crows ? ~0u : 0u;
-      if (tid < ST_BM) sa_lds[buf][tid] = __uint_as_float(__float_as_uint(acur.s) & ms);
+      const uint32_t ms = (tid >> 2) < crows ? ~0u : 0u;
+      if ((tid & 3) == 0) sa_lds[buf][tid >> 2] = __uint_as_float(__float_as_uint(acur.s) & ms);
     }
     __syncthreads();
     // both operands are prefetched three steps ahead; the activations of a

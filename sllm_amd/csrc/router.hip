@@ -35,11 +35,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 //
 // Prefill (T > 64): a workgroup owns a 64-token x 128-expert tile; both
 // operands go through LDS in 128-wide K chunks (row stride padded to
-// 272 B), with two chunks' global loads in flight (two register stages,
-// two LDS buffers) while one is multiplied. Wave (wm, we) of the 2 x 2
-// arrangement computes 32 tokens x 64 experts as 2 x 4 subtiles. x is read
-// E / 128 times and W T / 64 times, both mostly from L2.
+// 272 B). Three register stages keep three chunks' global loads in flight
+// (the loads are L2 hits for the most part, so the kernel is bound by their
+// latency, not by bytes) while two LDS buffers alternate between store and
+// multiply. Wave (wm, we) of the 2 x 2 arrangement computes 32 tokens x 64
+// experts as 2 x 4 subtiles. x is read E / 128 times and W T / 64 times,
+// both mostly from L2.
 constexpr int RG_TT = 64, RG_TE = 128, RG_KC = 128, RG_LS = 136;  // LS in bf16
+constexpr int RG_NS = 3;  // register stages (prefetch distance in chunks)
 
 __global__ __launch_bounds__(256, 1) void router_gemm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
@@ -55,18 +58,19 @@ __global__ __launch_bounds__(256, 1) void router_gemm_kernel(
   const int srow = tid >> 4, scol = (tid & 15) * 8;  // scol in bf16
   const uint16_t* xg = x + (size_t)min(t0 + srow, T - 1) * H + scol;
   const uint16_t* wg = w + (size_t)min(e0 + srow, E - 1) * H + scol;
-  u32x4 r0[12], r1[12];  // the two register stages
+  int xro[4], wro[8];  // row offsets (rows past T / E re-read the last row)
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    xro[q] = (min(t0 + srow + 16 * q, T - 1) - min(t0 + srow, T - 1)) * H;
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    wro[q] = (min(e0 + srow + 16 * q, E - 1) - min(e0 + srow, E - 1)) * H;
+  u32x4 r[RG_NS][12];
   auto gload = [&](u32x4 (&rg)[12], int k0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = min(t0 + srow + 16 * q, T - 1) - min(t0 + srow, T - 1);
-      rg[q] = *(const u32x4*)(xg + (size_t)row * H + k0);
-    }
+    for (int q = 0; q < 4; ++q) rg[q] = *(const u32x4*)(xg + xro[q] + k0);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int row = min(e0 + srow + 16 * q, E - 1) - min(e0 + srow, E - 1);
-      rg[4 + q] = *(const u32x4*)(wg + (size_t)row * H + k0);
-    }
+    for (int q = 0; q < 8; ++q) rg[4 + q] = *(const u32x4*)(wg + wro[q] + k0);
   };
   auto sstore = [&](const u32x4 (&rg)[12], int b) __attribute__((always_inline)) {
 #pragma unroll
@@ -99,25 +103,41 @@ __global__ __launch_bounds__(256, 1) void router_gemm_kernel(
     }
   };
   const int nk = H / RG_KC;
-  // chunk kc lives in register stage kc & 1 and LDS buffer kc & 1; the
-  // prefetch of chunk kc + 2 reuses the stage chunk kc just left
-  // prefetches past the last chunk re-read the last chunk (kept
-  // unconditional so the register stages stay in registers)
+  // chunk kc lives in register stage kc % 3 and LDS buffer kc % 2. A step
+  // stores its chunk, waits at the barrier (every wave is then done with the
+  // other LDS buffer's multiply of the step before), refills its register
+  // stage with chunk kc + 3 and multiplies. Main-loop prefetches past the
+  // last chunk re-read it (unconditional loads keep the wait counts exact);
+  // the tail steps load only what exists.
   auto kof = [&](int kc) { return min(kc, nk - 1) * RG_KC; };
-  gload(r0, 0);
-  gload(r1, kof(1));
-  for (int kc = 0; kc < nk; kc += 2) {
-    sstore(r0, 0);
+  auto step = [&](u32x4 (&rg)[12], int b, int kc) __attribute__((always_inline)) {
+    sstore(rg, b);
     __syncthreads();
-    gload(r0, kof(kc + 2));
-    mma(0);
-    if (kc + 1 < nk) {
-      sstore(r1, 1);
-      __syncthreads();
-      gload(r1, kof(kc + 3));
-      mma(1);
-    }
+    gload(rg, kof(kc + RG_NS));
+    mma(b);
+  };
+  auto tail_step = [&](u32x4 (&rg)[12], int b, int kc) __attribute__((always_inline)) {
+    sstore(rg, b);
+    __syncthreads();
+    if (kc + RG_NS < nk) gload(rg, kc * RG_KC + RG_NS * RG_KC);
+    mma(b);
+  };
+#pragma unroll
+  for (int s0 = 0; s0 < RG_NS; ++s0) gload(r[s0], kof(s0));
+  int kc = 0;
+  for (; kc + 6 <= nk; kc += 6) {
+    step(r[0], 0, kc);
+    step(r[1], 1, kc + 1);
+    step(r[2], 0, kc + 2);
+    step(r[0], 1, kc + 3);
+    step(r[1], 0, kc + 4);
+    step(r[2], 1, kc + 5);
   }
+  if (kc < nk) tail_step(r[0], 0, kc);
+  if (kc + 1 < nk) tail_step(r[1], 1, kc + 1);
+  if (kc + 2 < nk) tail_step(r[2], 0, kc + 2);
+  if (kc + 3 < nk) tail_step(r[0], 1, kc + 3);
+  if (kc + 4 < nk) tail_step(r[1], 0, kc + 4);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
