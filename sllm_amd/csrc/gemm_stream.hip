@@ -205,7 +205,13 @@ __device__ __forceinline__ void st_sched_pattern() {
 }
 
 // item descriptor in LDS: x = seg | nt << 1, y = e, z = row_begin, w = rows
-template <int BF, int MODE>
+// Activation scales: with every K a multiple of 512 (PERSTEP false), items
+// are whole groups of four steps, and the second step of each unrolled
+// four-step body loads the scales of the next group -- lane (row tid / 4,
+// block tid % 4), one 4-byte load, a wave touching 16 rows -- which the
+// first step of the next body stores to LDS. Otherwise (PERSTEP) each step
+// loads its own scale, four lanes per row.
+template <int BF, int MODE, bool PERSTEP>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, int pow2) {
   constexpr int YS = 264;  // bf16 row stride of the down-projection staging
@@ -213,7 +219,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   __shared__ int rsrc[ST_MAX_ITEMS][ST_BM];
   __shared__ float rwl[ST_MAX_ITEMS][ST_BM];
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][ST_BM * ST_LDS];
-  __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM];
+  // activation scales of the tile rows: per four-step group (double
+  // buffered by group parity), or per step (PERSTEP)
+  __shared__ __attribute__((aligned(16))) float sa_lds[2][ST_BM][PERSTEP ? 1 : 4];
   __shared__ __attribute__((aligned(16))) float red[ST_BM][ST_WAVES];
   __shared__ __attribute__((aligned(16))) uint16_t ystage[MODE == 1 ? ST_BM * YS : 8];
 
@@ -280,7 +288,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
 
   struct ASet {
     uint4 v[2];
-    float s;
+    float s;  // PERSTEP: the row's scale of this step
   };
 
   // ---- prefetch cursor ------------------------------------------------------
@@ -298,6 +306,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   int pi = 0, pkb = 0, pKB = 1;
   const uint8_t *pa0 = nullptr, *pa1 = nullptr, *pb = nullptr;
   const float *psa = nullptr, *ps0 = nullptr, *ps1 = nullptr;
+  float sgrp = 0.f;  // !PERSTEP: scale of (row tid / 4, block tid % 4) of a group
   const uint16_t* ps4 = nullptr;
   auto p_enter = [&](int i) {
     const int4 d = desc[i];
@@ -307,8 +316,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     pKB = KB;
     pa0 = S.a + (size_t)rsrc[i][a_row0] * K + a_chunk * 16;
     pa1 = S.a + (size_t)rsrc[i][64 + a_row0] * K + a_chunk * 16;
-    // four lanes share each activation-scale row, so a wave's scale load
-    // touches 16 rows (cache lines) rather than 64
+    // four lanes share each activation-scale row (a wave's scale load
+    // touches 16 rows)
     psa = S.sa + (size_t)rsrc[i][tid >> 2] * KB;
     const size_t blk0 = ((size_t)d.y * NT + nt) * KB;
     if constexpr (BF == SF_FP4) {
@@ -339,10 +348,12 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
       p_enter(pi);
     }
   };
+  // the group of four steps starting at the prefetch cursor (pkb % 4 == 0)
+  auto p_group_scales = [&]() { sgrp = psa[pkb + (tid & 3)]; };
   auto fetch_a = [&](ASet& af) {
     af.v[0] = *(const uint4*)(pa0 + pkb * 128);
     af.v[1] = *(const uint4*)(pa1 + pkb * 128);
-    af.s = psa[pkb];
+    if constexpr (PERSTEP) af.s = psa[pkb];
   };
   auto load_b = [&](BSet<BF>& b) {
     const uint8_t* base = pb + (size_t)pkb * Stream<BF, MODE>::BLK;
@@ -489,7 +500,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
 
 
   // ---- one pipeline step ----------------------------------------------------
-  auto step = [&](int st, ASet& acur, ASet& aload, BSet<BF>& bcur,
+  // j: the step's position in the unrolled four-step body
+  auto step = [&](int st, int j, ASet& acur, ASet& aload, BSet<BF>& bcur,
                   BSet<BF>& bload) {
     const int buf = st & 1;
     {  // A(st) registers -> LDS, rows past the tile zeroed
@@ -502,7 +514,13 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
             make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
       }
       const uint32_t ms = (tid >> 2) < crows ? ~0u : 0u;
-      if ((tid & 3) == 0) sa_lds[buf][tid >> 2] = __uint_as_float(__float_as_uint(acur.s) & ms);
+      if constexpr (PERSTEP) {
+        if ((tid & 3) == 0)
+          sa_lds[buf][tid >> 2][0] = __uint_as_float(__float_as_uint(acur.s) & ms);
+      } else if (j == 0) {  // this group's scales, loaded three steps ago
+        sa_lds[(st >> 2) & 1][tid >> 2][tid & 3] =
+            __uint_as_float(__float_as_uint(sgrp) & ms);
+      }
     }
     __syncthreads();
     // both operands are prefetched three steps ahead; the activations of a
@@ -513,12 +531,17 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     // change is a branch), keeping the loads, LDS reads and MFMAs in one
     // scheduling region.
     p_advance();
+    if (!PERSTEP && j == 1) p_group_scales();
     fetch_a(aload);
     load_b(bload);
     // compute step st over all eight 16-row groups: rows past the tile are
     // zero in LDS, and a branch-free step lets the compiler issue the LDS
     // reads of the next groups ahead of the MFMAs of the current one.
     const uint8_t* lds = a_lds[buf];
+    auto sx_of = [&](int row) -> float {  // activation scale of a tile row
+      if constexpr (PERSTEP) return sa_lds[buf][row][0];
+      else return sa_lds[(st >> 2) & 1][row][st & 3];
+    };
     auto a_frag = [&](int mi) {
       const uint8_t* row = lds + (mi * 16 + lc) * ST_LDS;
       const uint8_t* p0 = BF == SF_FP4 ? row + lg * 16 : row + lg * 32;
@@ -536,7 +559,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
       const float sb0 = bcur.sb0, sb1 = MODE == 0 ? bcur.sb1 : bcur.sb0;
       f32x4 part[2][2];
       auto rescale = [&](int m) {
-        const float sx = sa_lds[buf][m * 16 + lc];
+        const float sx = sx_of(m * 16 + lc);
         const float f0 = sx * sb0, f1 = sx * sb1;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -567,7 +590,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         const v8i x = a_frag(mi);
-        const uint32_t sxe = e8m0_bits(sa_lds[buf][mi * 16 + lc]);
+        const uint32_t sxe = e8m0_bits(sx_of(mi * 16 + lc));
 #pragma unroll
         for (int s = 0; s < 2; ++s)
           acc[mi][s] = st_mma<BF>(bcur.v[s], x, acc[mi][s], sbe[s], sxe);
@@ -589,6 +612,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   BSet<BF> b0, b1, b2, b3;
   ASet a0, a1, a2, a3;
   p_enter(0);
+  if (!PERSTEP) p_group_scales();
   c_enter(0);
   fetch_a(a0);
   load_b(b0);
@@ -600,14 +624,16 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   load_b(b2);
   int st = 0;
   for (; st + 4 <= total_steps; st += 4) {
-    step(st, a0, a3, b0, b3);
-    step(st + 1, a1, a0, b1, b0);
-    step(st + 2, a2, a1, b2, b1);
-    step(st + 3, a3, a2, b3, b2);
+    step(st, 0, a0, a3, b0, b3);
+    step(st + 1, 1, a1, a0, b1, b0);
+    step(st + 2, 2, a2, a1, b2, b1);
+    step(st + 3, 3, a3, a2, b3, b2);
   }
-  if (st < total_steps) step(st, a0, a3, b0, b3);
-  if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
-  if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+  // (only PERSTEP totals leave a remainder: otherwise every item is whole
+  // groups of four steps)
+  if (st < total_steps) step(st, 0, a0, a3, b0, b3);
+  if (st + 1 < total_steps) step(st + 1, 1, a1, a0, b1, b0);
+  if (st + 2 < total_steps) step(st + 2, 2, a2, a1, b2, b1);
 }
 
 // ---------------------------------------------------------------------------
@@ -629,7 +655,7 @@ constexpr int SD_LS = 136;  // bf16 row stride of the LDS activation tile
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int v4uv __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t pack_bf16_hi(float a, float b) {
   // fp32 values that are exact in bf16: keep the upper halves
@@ -642,7 +668,7 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
   const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(d0, true);
   const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(d1, false);
   const f32x2 e = __builtin_amdgcn_cvt_pk_f32_fp8(d1, true);
-  const u32x4v r = {pack_bf16_hi(a.x, a.y), pack_bf16_hi(b.x, b.y),
+  const v4uv r = {pack_bf16_hi(a.x, a.y), pack_bf16_hi(b.x, b.y),
                     pack_bf16_hi(c.x, c.y), pack_bf16_hi(e.x, e.y)};
   return __builtin_bit_cast(bf16x8, r);
 }
@@ -659,7 +685,7 @@ __device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t d, float scale) {
   float f[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) f[j] = e2m1_f32((d >> (4 * j)) & 15u) * scale;
-  const u32x4v r = {pack_bf16_hi(f[0], f[1]), pack_bf16_hi(f[2], f[3]),
+  const v4uv r = {pack_bf16_hi(f[0], f[1]), pack_bf16_hi(f[2], f[3]),
                     pack_bf16_hi(f[4], f[5]), pack_bf16_hi(f[6], f[7])};
   return __builtin_bit_cast(bf16x8, r);
 }
@@ -741,7 +767,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   // activation tile of a K step: 16 rows x 128 values; thread tid takes row
   // tid / 32 and values [4 (tid % 32), +4)
   const int a_row = tid >> 5, a_col = (tid & 31) * 4;
-  typedef typename std::conditional<MODE == 0, u32x2, u32x4v>::type AVec;
+  typedef typename std::conditional<MODE == 0, u32x2, v4uv>::type AVec;
   struct ASet {
     AVec v;
   };
@@ -952,6 +978,7 @@ static int num_cus() {
 template <int BF, int MODE>
 static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
                      float limit, int pow2, long upper_items, hipStream_t st) {
+  const bool perstep = s0.K % 512 != 0 || (s1 && s1->K % 512 != 0);
   // workgroups per XCD: at least one per CU, and enough that no workgroup
   // receives more than ST_MAX_ITEMS items (an XCD's range holds at most
   // ceil(upper / 8) items, dealt round-robin over its workgroups)
@@ -962,8 +989,12 @@ static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
   const long grid = 8 * nx;
   SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
   SegDesc dummy = s0;
-  moe_stream_kernel<BF, MODE><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
+  if (perstep)
+    moe_stream_kernel<BF, MODE, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
+  else
+    moe_stream_kernel<BF, MODE, false><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
   SLLM_LAUNCHED();
   return 0;
 }
