@@ -11,8 +11,9 @@
 // then ascending flat assignment index a = t*k + j, i.e.
 // np.argsort(ids.ravel(), kind="stable").
 //
-// Small problems use one fused workgroup (permute_fused_kernel); otherwise
-// three kernels, all deterministic:
+// Small problems use one fused workgroup (permute_fused_kernel); up to 1024
+// experts, hist followed by permute_chunk_kernel (scan and scatter in one
+// launch); otherwise three kernels, all deterministic:
 //  1. hist:    chunks of PERM_CHUNK assignments, LDS histogram per chunk.
 //  2. scan:    one workgroup; per-expert exclusive scan over chunks, then an
 //              exclusive scan over experts (offsets), chunk bases, and the
@@ -28,6 +29,7 @@
 namespace sllm {
 
 constexpr int PERM_CHUNK = 1024;
+constexpr int PERM_SCAN_REG = 48;  // chunk counts an expert keeps in registers
 
 __global__ __launch_bounds__(256) void permute_hist_kernel(
     const int* __restrict__ ids, int N, int E, int* __restrict__ chunk_hist) {
@@ -59,20 +61,25 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
   __syncthreads();
   for (int e0 = 0; e0 < E; e0 += 1024) {
     const int e = e0 + tid;
+    // The expert's chunk counts stay in registers between the count and
+    // the base pass (chunks beyond PERM_SCAN_REG are re-read). All loads of
+    // a batch are in flight at once: a dependent load per chunk would expose
+    // the memory latency nchunks times.
+    int v[PERM_SCAN_REG];
     int cnt = 0;
     if (e < E) {
-      // eight chunk counts in flight at a time (a dependent load per chunk
-      // would expose the memory latency nchunks times)
-      for (int c0 = 0; c0 < nchunks; c0 += 8) {
-        int v[8];
+#pragma unroll
+      for (int j = 0; j < PERM_SCAN_REG; ++j)
+        v[j] = j < nchunks ? chunk_hist[(size_t)j * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < PERM_SCAN_REG; ++j) cnt += v[j];
+      for (int c0 = PERM_SCAN_REG; c0 < nchunks; c0 += 8) {
+        int w[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          v[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
+          w[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (c0 + j < nchunks) chunk_hist[(size_t)(c0 + j) * E + e] = cnt;
-          cnt += v[j];  // exclusive within expert
-        }
+        for (int j = 0; j < 8; ++j) cnt += w[j];
       }
     }
     int ntile = (e < E && cnt > 0) ? (cnt + bm - 1) / bm : 0;
@@ -82,14 +89,24 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
     if (e < E) {
       counts[e] = cnt;
       offsets[e] = off;
-      for (int c0 = 0; c0 < nchunks; c0 += 8) {
-        int v[8];
+      // chunk bases: the expert's offset plus its exclusive prefix over
+      // chunks
+      int run = off;
+#pragma unroll
+      for (int j = 0; j < PERM_SCAN_REG; ++j) {
+        if (j < nchunks) chunk_hist[(size_t)j * E + e] = run;
+        run += v[j];
+      }
+      for (int c0 = PERM_SCAN_REG; c0 < nchunks; c0 += 8) {
+        int w[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          v[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
+          w[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + e] : 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (c0 + j < nchunks) chunk_hist[(size_t)(c0 + j) * E + e] = v[j] + off;
+        for (int j = 0; j < 8; ++j) {
+          if (c0 + j < nchunks) chunk_hist[(size_t)(c0 + j) * E + e] = run;
+          run += w[j];
+        }
       }
       for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
         const int r0 = i * bm;
@@ -117,7 +134,20 @@ __global__ __launch_bounds__(64) void permute_scatter_kernel(
   extern __shared__ int run[];
   const int c = blockIdx.x;
   const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) run[e] = chunk_base[(size_t)c * E + e];
+  // the chunk's expert bases, eight loads in flight per lane
+  for (int e0 = 0; e0 < E; e0 += 512) {
+    int b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = e0 + j * 64 + lane;
+      b[j] = e < E ? chunk_base[(size_t)c * E + e] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = e0 + j * 64 + lane;
+      if (e < E) run[e] = b[j];
+    }
+  }
   __syncthreads();
   const int a0 = c * PERM_CHUNK, a1 = min(N, a0 + PERM_CHUNK);
   const uint64_t lt = (1ull << lane) - 1ull;
@@ -149,6 +179,89 @@ __global__ __launch_bounds__(64) void permute_scatter_kernel(
     __syncthreads();  // every lane has read run[] before it advances
     if (valid && (peers >> lane) == 1ull) run[e] += __popcll(peers);
     __syncthreads();
+  }
+}
+
+// Scan and scatter in one launch (E <= PERM_FUSED_MAX_E): workgroup c owns
+// chunk c (16 waves x 64 assignments) and derives everything it needs from
+// the chunk histograms itself -- every expert's total (an exclusive scan of
+// the totals gives the expert offsets) and the expert's count in earlier
+// chunks -- so no single-workgroup scan pass runs in between. Within the
+// chunk, per-wave LDS histograms give each wave its per-expert base, and
+// the waves scatter their 64 assignments with ballot ranks. Workgroup 0 also
+// writes counts, offsets and the tile table.
+__global__ __launch_bounds__(1024) void permute_chunk_kernel(
+    const int* __restrict__ ids, int N, int E, int nbits, int bm, int nchunks,
+    const int* __restrict__ chunk_hist, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted_idx,
+    int* __restrict__ inv_pos, int* __restrict__ tile_info,
+    int* __restrict__ num_tiles, int max_tiles) {
+  __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
+  __shared__ int sh[1024];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x;
+  const int a = c * PERM_CHUNK + wave * 64 + lane;
+  const int raw = a < N ? ids[a] : -1;
+  for (int q = tid; q < PERM_FUSED_WAVES * E; q += 1024) hist[q / E][q % E] = 0;
+  // expert tid: total over all chunks and count in the chunks before c
+  int tot = 0, pre = 0;
+  if (tid < E) {
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      int v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        v[j] = c0 + j < nchunks ? chunk_hist[(size_t)(c0 + j) * E + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        tot += v[j];
+        pre += c0 + j < c ? v[j] : 0;
+      }
+    }
+  }
+  __syncthreads();
+  const bool valid = raw >= 0 && raw < E;  // out-of-range ids are dropped
+  if (valid) atomicAdd(&hist[wave][raw], 1);
+  int tot_rows, tot_tiles;
+  const int off = block_excl_scan(tot, sh, tot_rows);  // (its barriers also
+                                                       // order the atomics)
+  if (c == 0) {
+    const int ntile = (tid < E && tot > 0) ? (tot + bm - 1) / bm : 0;
+    const int toff = block_excl_scan(ntile, sh, tot_tiles);
+    if (tid < E) {
+      counts[tid] = tot;
+      offsets[tid] = off;
+      for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
+        const int r0 = i * bm;
+        *(int4*)(tile_info + 4 * (toff + i)) =
+            make_int4(tid, off + r0, min(bm, tot - r0), 0);
+      }
+    }
+    if (tid == 0) {
+      offsets[E] = tot_rows;
+      *num_tiles = min(tot_tiles, max_tiles);
+    }
+  }
+  if (tid < E) {  // per-wave bases of expert tid within the chunk
+    int run = off + pre;
+#pragma unroll
+    for (int w = 0; w < PERM_FUSED_WAVES; ++w) {
+      const int h = hist[w][tid];
+      hist[w][tid] = run;
+      run += h;
+    }
+  }
+  __syncthreads();
+  const int e = valid ? raw : 0;
+  uint64_t peers = __ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const int bit = (e >> b) & 1;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  if (valid) {
+    const int pos = hist[wave][e] + __popcll(peers & ((1ull << lane) - 1ull));
+    sorted_idx[pos] = a;
+    inv_pos[a] = pos;
   }
 }
 
@@ -193,6 +306,14 @@ int launch_permute(const int* ids, int N, int E, int bm, int* counts,
   const size_t lds = (size_t)E * sizeof(int);
   permute_hist_kernel<<<nchunks, 256, lds, st>>>(ids, N, E, chunk_hist);
   SLLM_LAUNCHED();
+  if (E <= PERM_FUSED_MAX_E) {
+    static_assert(PERM_CHUNK == PERM_FUSED_WAVES * 64, "one group per wave");
+    permute_chunk_kernel<<<nchunks, 1024, 0, st>>>(
+        ids, N, E, nbits, bm, nchunks, chunk_hist, counts, offsets, sorted_idx,
+        inv_pos, tile_info, num_tiles, max_tiles);
+    SLLM_LAUNCHED();
+    return 0;
+  }
   permute_scan_kernel<<<1, 1024, 0, st>>>(chunk_hist, nchunks, E, bm, counts,
                                           offsets, tile_info, num_tiles,
                                           max_tiles);
