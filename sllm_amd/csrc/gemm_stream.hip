@@ -441,13 +441,16 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
           const float amax = fmaxf(fmaxf(fmaxf(r0.x, r0.y), fmaxf(r0.z, r0.w)),
                                    fmaxf(fmaxf(r1.x, r1.y), fmaxf(r1.z, r1.w)));
           float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
-          if (pow2) {
+          float inv;
+          if (pow2) {  // power-of-two scale: its reciprocal is exact
             const uint32_t bits = __float_as_uint(sc);
             const int ex = (int)((bits >> 23) & 0xFF) - 127 +
                            ((bits & 0x7FFFFF) ? 1 : 0);
             sc = __uint_as_float((uint32_t)(ex + 127) << 23);
+            inv = __uint_as_float((uint32_t)(127 - ex) << 23);
+          } else {
+            inv = __builtin_amdgcn_rcpf(sc);  // within 1 ulp of 1 / sc
           }
-          const float inv = 1.0f / sc;
           float y[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v)
@@ -459,10 +462,11 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
         }
       }
       __syncthreads();
+      // streaming stores: h is read back only by the next kernel
       for (int c = tid; c < rows * 8; c += ST_THREADS) {
         const int r = c >> 3, c16 = c & 7;
-        *(uint4*)(S.hq + (size_t)(rb + r) * S.N + nt * 128 + c16 * 16) =
-            *(const uint4*)(h_lds + r * ST_LDS + c16 * 16);
+        __builtin_nontemporal_store(*(const v4u*)(h_lds + r * ST_LDS + c16 * 16),
+                                    (v4u*)(S.hq + (size_t)(rb + r) * S.N + nt * 128 + c16 * 16));
       }
       __syncthreads();  // h_lds is the next step's A buffer
     } else {
