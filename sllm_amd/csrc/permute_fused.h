@@ -7,21 +7,29 @@
 
 namespace sllm {
 
-// Block-wide exclusive scan of one value per thread (1024 threads).
+// Block-wide exclusive scan of one value per thread (1024 threads, 16
+// waves): a shuffle scan inside each wave, the 16 wave totals through LDS,
+// two barriers in all. sh needs 16 ints.
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
-  const int tid = threadIdx.x;
-  sh[tid] = v;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    int add = tid >= o ? sh[tid - o] : 0;
-    __syncthreads();
-    sh[tid] += add;
-    __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;  // inclusive scan within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
   }
-  int incl = sh[tid];
-  total = sh[1023];
+  if (lane == 63) sh[wave] = x;
   __syncthreads();
-  return incl - v;
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    const int t = sh[w];
+    base += w < wave ? t : 0;
+    tot += t;
+  }
+  total = tot;
+  __syncthreads();  // sh is reused by the next scan
+  return base + x - v;
 }
 
 // One workgroup of 16 waves (1024 threads) permutes N <= PERM_FUSED_MAX_N
