@@ -241,6 +241,7 @@ def run_c4(args):
                      args.steps, args.warmup)
     st = _stage_times(lambda ev: ds_call(layer, x, out, ws, T, "prefill",
                                          stage_events=ev), len(STAGES))
+    routing_us = _c4_routing_us(c, layer.rng)
     flops = 6 * H * I * T * k + 6 * H * Is * T
     wbytes = touched * 3 * H * I // 2 + touched * 3 * H * I // 32
     bytes_ = wbytes + 3 * H * Is + E * H * 2 + 2 * T * H * 2
@@ -257,9 +258,48 @@ def run_c4(args):
            "expert_up": {"algorithmic_bytes": up_bytes, "ms": st["expert_up"],
                          "GBps": round(up_bytes / t_up / 1e9, 1),
                          "TFLOPs": round(up_flops / t_up / 1e12, 1),
-                         "mfma_frac_fp8_rate": round(up_flops / t_up / (PEAK_FP8_TFLOPS * 1e12), 4)}}
+                         "mfma_frac_fp8_rate": round(up_flops / t_up / (PEAK_FP8_TFLOPS * 1e12), 4)},
+           "routing_us": routing_us}
     print(json.dumps(res), flush=True)
     return 0
+
+
+def _c4_routing_us(c, rng, reps=20):
+    """The two DeepSeek routing kernels alone at C4 shape (synthetic fp32
+    logits N(0,1)): group-limited sigmoid top-k with bias, and a hash layer
+    (a seeded (vocab, k) token-id table of uniform expert ids; vocab 129280
+    as DeepSeek-V3/V4)."""
+    import numpy as np
+    from sllm_amd import _lib
+    from sllm_amd.runtime import DeviceBuffer, Event, sync, to_device_raw
+    T, E, k = c["T"], c["E"], c["k"]
+    V = 129280
+    L = _lib.lib()
+    lg = to_device_raw(rng.standard_normal((T, E)).astype(np.float32))
+    bias = to_device_raw((rng.standard_normal(E) * 0.01).astype(np.float32))
+    table = to_device_raw(rng.integers(0, E, (V, k)).astype(np.int32))
+    tok = to_device_raw(rng.integers(0, V, T).astype(np.int32))
+    w, ids = DeviceBuffer(T * k * 4), DeviceBuffer(T * k * 4)
+    calls = {
+        "grouped_topk": lambda: L.sllm_moe_route_grouped(
+            lg.ptr, bias.ptr, w.ptr, ids.ptr, T, E, k, c["n_group"],
+            c["topk_group"], 1, np.float32(c["route_scale"]), None),
+        "hash": lambda: L.sllm_moe_route_hash(
+            lg.ptr, tok.ptr, table.ptr, V, w.ptr, ids.ptr, T, E, k, 1,
+            np.float32(c["route_scale"]), None),
+    }
+    out = {}
+    for name, call in calls.items():
+        _lib.check(call(), name)
+        sync()
+        e0, e1 = Event(), Event()
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        e1.synchronize()
+        out[name] = round(e0.elapsed_ms(e1) / reps * 1e3, 2)
+    return out
 
 
 def run_c5(args):

@@ -154,6 +154,15 @@ int sllm_moe_route_grouped(const float* logits, const float* bias,
                            float* w_out, int* id_out, int T, int E, int topk,
                            int n_group, int topk_group, int scoring,
                            float route_scale, void* stream);
+/* hash-layer routing (ref/deepseek_v4.py:545-552, upstream
+ * ref/hf_sources/dsv4/model.py:620-627): ids = tid2eid[clip(token_ids[t],
+ * 0, vocab-1)] (tid2eid (vocab, topk) int32, table order, no bias), weights
+ * = those experts' scores, renormalized unless softmax, times route_scale.
+ * scoring as in sllm_moe_route_grouped; E <= 2048, topk <= 64. */
+int sllm_moe_route_hash(const float* logits, const int* token_ids,
+                        const int* tid2eid, int vocab, float* w_out,
+                        int* id_out, int T, int E, int topk, int scoring,
+                        float route_scale, void* stream);
 /* Stable expert-major permutation of ids (N = T*k int32) with a ragged tile
  * table of ceil(count/bm) row tiles per expert: tile_info holds max_tiles
  * int4 {expert, first permuted row, rows, 0}. new (the reference has no
@@ -320,6 +329,13 @@ typedef struct sllm_moe_ds_args {
   const void* w2_s_packed;
   const void* s13_packed;
   const void* s2_packed;
+  /* Optional hash routing (the first n_hash_layers of DeepSeek-V4,
+   * ref/deepseek_v4.py:545-552): with tid2eid (vocab, topk) int32 and the
+   * tokens' ids token_ids (T) int32, routing takes the table's experts
+   * instead of the biased top-k (see sllm_moe_route_hash). */
+  const int* token_ids;
+  const int* tid2eid;
+  int vocab;
 } sllm_moe_ds_args;
 
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a);

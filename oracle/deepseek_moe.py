@@ -93,13 +93,29 @@ def select_experts(biased, top_k: int, n_group: int = 1, topk_group: int = 1):
     return _stable_topk_desc(masked, top_k)
 
 
+def hash_select(token_ids, tid2eid):
+    """Hash-layer expert ids, ref/deepseek_v4.py:545-552 (text branch):
+    tid2eid[clip(token_ids, 0, vocab - 1)] -> (T, k) int64, in table order."""
+    table = np.asarray(tid2eid, np.int64)
+    ids = np.clip(np.asarray(token_ids, np.int64), 0, table.shape[0] - 1)
+    return table[ids]
+
+
 def moe_route(logits, bias, top_k: int, scoring: str = "sigmoid",
-              route_scale: float = 1.0, n_group: int = 1, topk_group: int = 1):
-    """ref/deepseek_v4.py:540-561 (non-hash branch) on fp32 logits ->
-    (weights (T, k) f32, idx (T, k) int64)."""
+              route_scale: float = 1.0, n_group: int = 1, topk_group: int = 1,
+              token_ids=None, tid2eid=None):
+    """ref/deepseek_v4.py:540-561 on fp32 logits -> (weights (T, k) f32,
+    idx (T, k) int64). With tid2eid (a hash layer) the ids come from the
+    token-id table and the bias is not used (:545-552); otherwise the
+    biased top-k, optionally group-limited."""
     scores = gate_scores(logits, scoring)
-    biased = scores + np.asarray(bias, np.float32) if bias is not None else scores
-    idx = select_experts(biased, top_k, n_group, topk_group).astype(np.int64)
+    if tid2eid is not None:
+        idx = hash_select(token_ids, tid2eid)
+        if idx.shape[1] != top_k:
+            raise ValueError("tid2eid must have top_k columns")
+    else:
+        biased = scores + np.asarray(bias, np.float32) if bias is not None else scores
+        idx = select_experts(biased, top_k, n_group, topk_group).astype(np.int64)
     w = np.take_along_axis(scores, idx, axis=-1)
     if scoring != "softmax":
         w = w / w.sum(-1, keepdims=True)
@@ -119,14 +135,14 @@ def expert_ffn(x, w1, w3, w2, limit: float):
 
 def moe_block_forward(x, logits, bias, experts, shared, top_k, limit,
                       scoring="sigmoid", route_scale=1.0, n_group=1,
-                      topk_group=1):
+                      topk_group=1, token_ids=None, tid2eid=None):
     """Un-quantized layer with the upstream combine. ``experts`` maps
     e -> (w1, w3, w2) fp32 (a callable or a sequence); ``shared`` is
     (w1, w3, w2) or None."""
     x = np.asarray(x, np.float32)
     T, H = x.shape
     w, idx = moe_route(logits, bias, top_k, scoring, route_scale, n_group,
-                       topk_group)
+                       topk_group, token_ids, tid2eid)
     y = np.zeros((T, top_k, H), np.float32)
     get = experts if callable(experts) else (lambda e: experts[e])
     for e in np.unique(idx):
@@ -175,14 +191,15 @@ def _swiglu_clamped(g, u, limit):
 
 def moe_layer_mxfp4(x, logits, W: DeepseekMxfp4Weights, top_k: int,
                     limit: float, scoring="sigmoid", route_scale=1.0,
-                    n_group=1, topk_group=1, return_parts=False):
+                    n_group=1, topk_group=1, return_parts=False,
+                    token_ids=None, tid2eid=None):
     """The quantized DeepSeek-style layer. x (T, H) float32 holding bf16
     values; logits (T, E) fp32. out = sum_{j ascending} y_j + shared(x)
     where y_j = W2(q(w_j * swiglu(W1 q(x), W3 q(x))))."""
     x = np.asarray(x, np.float32)
     T, H = x.shape
     w, idx = moe_route(logits, W.bias, top_k, scoring, route_scale, n_group,
-                       topk_group)
+                       topk_group, token_ids, tid2eid)
     xq, sx = quant.act_quant(x, pow2=True)
     y = np.zeros((T, top_k, H), np.float32)
     for e in np.unique(idx):

@@ -57,6 +57,7 @@ class DeepseekArgs(Structure):
         ("stream", P), ("stage_events", P),
         ("w13_packed", P), ("w13_s_packed", P), ("w2_packed", P),
         ("w2_s_packed", P), ("s13_packed", P), ("s2_packed", P),
+        ("token_ids", P), ("tid2eid", P), ("vocab", c_int),
     ]
 
 
@@ -102,6 +103,8 @@ SIGNATURES = {
                                             c_int]),
     "sllm_gemm_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int]),
     "sllm_moe_router_gemm": (c_int, [P, P, P, c_int, c_int, c_int, P]),
+    "sllm_moe_route_hash": (c_int, [P, P, P, c_int, P, P, c_int, c_int, c_int,
+                                    c_int, c_float, P]),
     "sllm_moe_route_softmax": (c_int, [P, P, P, c_int, c_int, c_int, c_float,
                                        P]),
     "sllm_moe_route_grouped": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int,

@@ -25,6 +25,10 @@ int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,
                          hipStream_t st);
+int launch_route_hash(const float* logits, const int* token_ids,
+                      const int* tid2eid, int vocab, float* w, int* ids,
+                      int T, int E, int topk, int scoring, float route_scale,
+                      hipStream_t st);
 size_t permute_scratch_bytes(int N, int E);
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,

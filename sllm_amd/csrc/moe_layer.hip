@@ -389,6 +389,8 @@ long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
 
 int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   if (check_common(a, "sllm_moe_ds_forward")) return -1;
+  SLLM_REQUIRE(!a->tid2eid || (a->token_ids && a->vocab > 0),
+               "sllm_moe_ds_forward: hash routing needs token_ids and vocab");
   const bool sh = a->s1 != nullptr;
   SLLM_REQUIRE(a->w1 && a->w1_s && a->w3 && a->w3_s && a->w2 && a->w2_s,
                "sllm_moe_ds_forward: null expert weights");
@@ -426,8 +428,12 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
                                              (const uint16_t*)a->router_w,
                                              logits, T, E, H, st));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-        launch_route_grouped(logits, a->bias, w, ids, T, E, k, a->n_group,
-                             a->topk_group, a->scoring, a->route_scale, st));
+        a->tid2eid
+            ? launch_route_hash(logits, a->token_ids, a->tid2eid, a->vocab, w,
+                                ids, T, E, k, a->scoring, a->route_scale, st)
+            : launch_route_grouped(logits, a->bias, w, ids, T, E, k,
+                                   a->n_group, a->topk_group, a->scoring,
+                                   a->route_scale, st));
   STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
         launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
                        ntiles, p.max_tiles, ws + p.pscr, st));

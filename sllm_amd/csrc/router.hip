@@ -329,19 +329,14 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
 // --------------------------------------------------------------------------
 enum Scoring { SCORE_SOFTMAX = 0, SCORE_SIGMOID = 1, SCORE_SQRTSOFTPLUS = 2 };
 
+// Scores of one token's logits row on the calling wave (lane holds experts
+// lane + 64 i): softmax in fp64 (ref/deepseek_v4.py:524-525), sigmoid in
+// fp64 then fp32 (:526-528), sqrt(softplus) (:529-530, :534-537).
 template <int EPL>
-__global__ __launch_bounds__(256) void route_grouped_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias,
-    float* __restrict__ w_out, int* __restrict__ id_out, int T, int E,
-    int topk, int n_group, int topk_group, int scoring, float route_scale) {
-  __shared__ float sb[4][EPL * 64];
+__device__ __forceinline__ void gate_scores_row(const float* __restrict__ row,
+                                                int E, int scoring,
+                                                float (&sc)[EPL]) {
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int t_raw = blockIdx.x * 4 + wv;
-  const bool active = t_raw < T;
-  const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
-  const float* row = logits + (size_t)t * E;
-  float sc[EPL];
   if (scoring == SCORE_SOFTMAX) {
     double m = -INFINITY;
     double xv[EPL];
@@ -379,6 +374,21 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
       }
     }
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_grouped_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias,
+    float* __restrict__ w_out, int* __restrict__ id_out, int T, int E,
+    int topk, int n_group, int topk_group, int scoring, float route_scale) {
+  __shared__ float sb[4][EPL * 64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int t_raw = blockIdx.x * 4 + wv;
+  const bool active = t_raw < T;
+  const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
+  float sc[EPL];
+  gate_scores_row<EPL>(logits + (size_t)t * E, E, scoring, sc);
   float b[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -455,6 +465,46 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
     float wv_ = scoring == SCORE_SOFTMAX ? mine : mine / wsum;
     w_out[(size_t)t * topk + lane] = wv_ * route_scale;
     id_out[(size_t)t * topk + lane] = myid;
+  }
+}
+
+// Hash layers (ref/deepseek_v4.py:545-552; upstream model.py:620-627,
+// text branch): the expert ids of token t are tid2eid[clip(token_ids[t],
+// 0, vocab - 1)] in table order -- no bias, no top-k -- and the weights are
+// those experts' scores, renormalized unless softmax (summed in slot
+// order), times route_scale. One wave per token; the row's scores go
+// through LDS so that lane j can read the score of its slot's expert.
+template <int EPL>
+__global__ __launch_bounds__(256) void route_hash_kernel(
+    const float* __restrict__ logits, const int* __restrict__ token_ids,
+    const int* __restrict__ tid2eid, int vocab, float* __restrict__ w_out,
+    int* __restrict__ id_out, int T, int E, int topk, int scoring,
+    float route_scale) {
+  __shared__ float sb[4][EPL * 64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int t_raw = blockIdx.x * 4 + wv;
+  const bool active = t_raw < T;
+  const int t = active ? t_raw : T - 1;
+  float sc[EPL];
+  gate_scores_row<EPL>(logits + (size_t)t * E, E, scoring, sc);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (lane + 64 * i < E) sb[wv][lane + 64 * i] = sc[i];
+  __syncthreads();
+  const int tok = min(max(token_ids[t], 0), vocab - 1);
+  int e = 0;
+  float se = 0.f;
+  if (lane < topk) {
+    e = tid2eid[(size_t)tok * topk + lane];
+    se = (e >= 0 && e < E) ? sb[wv][e] : __uint_as_float(0x7FC00000u);
+  }
+  float wsum = 0.f;
+  for (int j = 0; j < topk; ++j) wsum += __shfl(se, j, kWave);
+  if (active && lane < topk) {
+    const float wv_ = scoring == SCORE_SOFTMAX ? se : se / wsum;
+    w_out[(size_t)t * topk + lane] = wv_ * route_scale;
+    id_out[(size_t)t * topk + lane] = e;
   }
 }
 
@@ -581,6 +631,33 @@ int launch_route_grouped(const float* logits, const float* bias, float* w,
   return 0;
 }
 
+int launch_route_hash(const float* logits, const int* token_ids,
+                      const int* tid2eid, int vocab, float* w, int* ids,
+                      int T, int E, int topk, int scoring, float route_scale,
+                      hipStream_t st) {
+  SLLM_REQUIRE(logits && token_ids && tid2eid && w && ids,
+               "route_hash: null pointer");
+  SLLM_REQUIRE(T > 0 && E > 0 && E <= 2048 && topk > 0 && topk <= 64 &&
+                   topk <= E && vocab > 0 && scoring >= 0 && scoring <= 2,
+               "route_hash: bad sizes (T=%d E=%d k=%d vocab=%d scoring=%d)",
+               T, E, topk, vocab, scoring);
+  const int grid = ceil_div(T, 4);
+  switch (epl_for(E)) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_hash_kernel<n><<<grid, 256, 0, st>>>(logits, token_ids, tid2eid,    \
+                                               vocab, w, ids, T, E, topk,     \
+                                               scoring, route_scale);         \
+    break;
+    CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
+#undef CASE
+    default:
+      SLLM_REQUIRE(false, "route_hash: E=%d too large", E);
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
 }  // namespace sllm
 
 using namespace sllm;
@@ -640,6 +717,15 @@ int sllm_moe_route_softmax(const float* logits, float* w_out, int* id_out,
                            int T, int E, int topk, float eps, void* stream) {
   return launch_route_softmax(logits, w_out, id_out, T, E, topk, eps,
                               (hipStream_t)stream);
+}
+
+int sllm_moe_route_hash(const float* logits, const int* token_ids,
+                        const int* tid2eid, int vocab, float* w_out,
+                        int* id_out, int T, int E, int topk, int scoring,
+                        float route_scale, void* stream) {
+  return launch_route_hash(logits, token_ids, tid2eid, vocab, w_out, id_out,
+                           T, E, topk, scoring, route_scale,
+                           (hipStream_t)stream);
 }
 
 int sllm_moe_route_grouped(const float* logits, const float* bias,

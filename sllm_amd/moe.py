@@ -116,7 +116,8 @@ def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
 
 def _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
              scoring, route_scale, swiglu_limit, x, logits, weights, out,
-             debug, workspace, workspace_bytes, stream):
+             debug, workspace, workspace_bytes, stream, token_ids=None,
+             vocab=0):
     a = _lib.DeepseekArgs()
     a.T, a.H, a.E, a.I, a.Is, a.topk = T, H, E, I, Is, topk
     a.mode = _mode(mode)
@@ -141,6 +142,10 @@ def _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
     a.workspace = ptr(workspace)
     a.workspace_bytes = int(workspace_bytes or 0)
     a.stream = stream_handle(stream)
+    # hash layers: weights["tid2eid"] (vocab, topk) int32 + per-call token ids
+    a.tid2eid = ptr(w.get("tid2eid"))
+    a.token_ids = ptr(token_ids)
+    a.vocab = int(vocab)
     return a
 
 
@@ -159,17 +164,22 @@ def deepseek_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
                          mode="auto", out_f32=False, n_group=1, topk_group=1,
                          scoring="sigmoid", route_scale=1.0, swiglu_limit=0.0,
                          logits=None, workspace=None, workspace_bytes=None,
-                         stream=None, debug=None, stage_events=None) -> None:
+                         stream=None, debug=None, stage_events=None,
+                         token_ids=None, vocab=0) -> None:
     """One DeepSeek-style MoE layer on device buffers (shapes in
     include/sllm_moe.h sllm_moe_ds_args). `weights` maps router_w, bias, w1,
-    w1_s, w3, w3_s, w2, w2_s [, s1, s1_s, s3, s3_s, s2, s2_s]."""
+    w1_s, w3, w3_s, w2, w2_s [, s1, s1_s, s3, s3_s, s2, s2_s] [, tid2eid];
+    a hash layer (weights["tid2eid"], vocab rows) also takes the tokens' ids
+    `token_ids` (T int32 device buffer)."""
     if workspace_bytes is None:
         workspace_bytes = getattr(workspace, "nbytes", None)
         if workspace_bytes is None and hasattr(workspace, "numel"):
             workspace_bytes = workspace.numel() * workspace.element_size()
+    if weights.get("tid2eid") is not None and token_ids is None:
+        raise ValueError("a hash layer needs token_ids")
     a = _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
                  scoring, route_scale, swiglu_limit, x, logits, weights, out,
-                 debug, workspace, workspace_bytes, stream)
+                 debug, workspace, workspace_bytes, stream, token_ids, vocab)
     evs = _event_array(stage_events)
     if evs is not None:
         import ctypes
@@ -304,7 +314,7 @@ class DeepseekMoE:
     def __init__(self, router_w, bias, w1, w1_s, w3, w3_s, w2, w2_s, s1=None,
                  s1_s=None, s3=None, s3_s=None, s2=None, s2_s=None, top_k=8,
                  n_group=1, topk_group=1, scoring="sigmoid", route_scale=1.0,
-                 swiglu_limit=0.0, packed=True):
+                 swiglu_limit=0.0, packed=True, tid2eid=None):
         self.E, self.I = np.asarray(w1).shape[:2]
         self.H = np.asarray(w2).shape[1]
         self.Is = 0 if s1 is None else np.asarray(s1).shape[0]
@@ -330,12 +340,27 @@ class DeepseekMoE:
             if s1 is not None:
                 b["s13_packed"], _ = pack_weights(0, 1, b["s1"], b["s3"], 1, Is, H)
                 b["s2_packed"], _ = pack_weights(0, 0, b["s2"], None, 1, H, Is)
+        # hash layer (ref/deepseek_v4.py:545-552): experts from the token-id
+        # table instead of the biased top-k
+        self.vocab = 0
+        if tid2eid is not None:
+            t = np.ascontiguousarray(tid2eid, np.int32)
+            if t.ndim != 2 or t.shape[1] != self.top_k:
+                raise ValueError("tid2eid must be (vocab, top_k)")
+            self.vocab = t.shape[0]
+            b["tid2eid"] = _up(t)
         self._w = b
         self._ws = None
 
-    def forward(self, x, logits=None, mode="auto", return_routing=False):
+    def forward(self, x, logits=None, mode="auto", return_routing=False,
+                token_ids=None):
         x = np.asarray(x, np.float32)
         T = x.shape[0]
+        tok = None
+        if self.vocab:
+            if token_ids is None:
+                raise ValueError("a hash layer needs token_ids")
+            tok = _up(np.asarray(token_ids).reshape(T).astype(np.int32))
         n = deepseek_workspace_bytes(T, self.H, self.E, self.I, self.Is,
                                      self.top_k, mode, self.Is > 0,
                                      logits is not None)
@@ -356,7 +381,8 @@ class DeepseekMoE:
                              topk_group=self.topk_group, scoring=self.scoring,
                              route_scale=self.route_scale,
                              swiglu_limit=self.swiglu_limit, logits=lg,
-                             workspace=self._ws, debug=dbg)
+                             workspace=self._ws, debug=dbg, token_ids=tok,
+                             vocab=self.vocab)
         y = out.copy_host().reshape(T, self.H)
         if not return_routing:
             return y

@@ -187,6 +187,26 @@ def test_route_grouped_matches_oracle(L, G, kg, scoring):
     np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("scoring", ["sigmoid", "softmax", "sqrtsoftplus"])
+def test_route_hash_matches_oracle(L, scoring):
+    """Hash layers: ids from the token-id table (out-of-range token ids
+    clipped), weights the chosen experts' scores (ref/deepseek_v4.py:545-552)."""
+    rng = np.random.default_rng(11)
+    T, E, k, V = 301, 256, 8, 50
+    logits = (rng.standard_normal((T, E)) * 0.9).astype(np.float32)
+    tid2eid = np.stack([rng.permutation(E)[:k] for _ in range(V)]).astype(np.int32)
+    tok = rng.integers(-5, V + 5, T).astype(np.int32)
+    w, ids = empty(T * k * 4), empty(T * k * 4)
+    sc = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}[scoring]
+    L.check(L.lib().sllm_moe_route_hash(dev(logits).ptr, dev(tok).ptr,
+                                        dev(tid2eid).ptr, V, w.ptr, ids.ptr, T,
+                                        E, k, sc, np.float32(1.5), None))
+    wr, ir = dm.moe_route(logits, None, k, scoring, 1.5, token_ids=tok,
+                          tid2eid=tid2eid)
+    np.testing.assert_array_equal(host(ids, np.int32, (T, k)), ir.astype(np.int32))
+    np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=2e-6, atol=1e-7)
+
+
 def test_router_gemm_matches_fp64(L):
     rng = np.random.default_rng(3)
     for T, E, H in [(4096, 512, 2048), (64, 16, 1024), (33, 100, 256),

@@ -155,6 +155,42 @@ def test_deepseek_prefill_small(T, G, kg, L, packed):
     assert rel < 3e-3 and mabs < 0.05 * scale
 
 
+@pytest.mark.parametrize("T,mode", [(200, "prefill"), (8, "decode")])
+def test_deepseek_hash_layer(T, mode):
+    """A hash layer (first n_hash_layers of DeepSeek-V4): experts from the
+    token-id table, weights from the sigmoid scores."""
+    x, W = deepseek_mxfp4(seed=T + 7, T=T, H=512, E=16, I=256, Is=256)
+    rng = np.random.default_rng(T)
+    V, k = 40, 4
+    tid2eid = np.stack([rng.permutation(16)[:k] for _ in range(V)]).astype(np.int32)
+    tok = rng.integers(0, V, T).astype(np.int32)
+    layer = deepseek_layer(W, k, scoring="sigmoid", route_scale=2.5,
+                           tid2eid=tid2eid)
+    y, r = layer.forward(x, mode=mode, return_routing=True, token_ids=tok)
+    w_ref, ids_ref = dm.moe_route(r["logits"], W.bias, k, "sigmoid", 2.5,
+                                  token_ids=tok, tid2eid=tid2eid)
+    np.testing.assert_array_equal(r["ids"], ids_ref.astype(np.int32))
+    np.testing.assert_allclose(r["w"], w_ref, rtol=2e-6)
+    if mode == "prefill":
+        want = dm.moe_layer_mxfp4(x, r["logits"], W, k, 0.0, "sigmoid", 2.5,
+                                  token_ids=tok, tid2eid=tid2eid)
+        rel, mabs, scale = _report("deepseek hash prefill", y, want)
+        assert rel < 3e-3 and mabs < 0.05 * scale
+    else:  # decode keeps activations unquantized: dequantized-weight oracle
+        from oracle.codecs import dequant_fp4_block, dequant_fp8_block
+
+        def ex(e):
+            return (dequant_fp4_block(W.w1_p[e], W.w1_s[e]),
+                    dequant_fp4_block(W.w3_p[e], W.w3_s[e]),
+                    dequant_fp4_block(W.w2_p[e], W.w2_s[e]))
+        sh = (dequant_fp8_block(W.s1_q, W.s1_s), dequant_fp8_block(W.s3_q, W.s3_s),
+              dequant_fp8_block(W.s2_q, W.s2_s))
+        want = dm.moe_block_forward(x, r["logits"], W.bias, ex, sh, k, 0.0,
+                                    "sigmoid", 2.5, token_ids=tok, tid2eid=tid2eid)
+        rel, mabs, scale = _report("deepseek hash decode", y, want)
+        assert rel < 1e-4
+
+
 def test_deepseek_prefill_c4_shapes():
     """C4 geometry (H 7168, I = Is = 2048, top-8, 8 groups keep 4) with
     E = 32 experts and T = 256 tokens so the CPU oracle stays fast."""

@@ -41,6 +41,29 @@ def test_route_matches_closed_form():
         np.testing.assert_allclose(w[t], ws, rtol=2e-6)
 
 
+def test_hash_route_closed_form():
+    """Hash layers (ref/deepseek_v4.py:545-552): ids from the token-id table
+    with out-of-range ids clipped, table order kept, bias ignored; weights
+    are the scores of those ids, renormalized unless softmax."""
+    rng = np.random.default_rng(5)
+    T, E, k, V = 12, 16, 4, 9
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    tid2eid = np.stack([rng.permutation(E)[:k] for _ in range(V)]).astype(np.int32)
+    tok = rng.integers(-3, V + 3, T)                 # some out of range
+    bias = np.full(E, 100.0, np.float32)             # would dominate a top-k
+    for scoring in ("sigmoid", "softmax", "sqrtsoftplus"):
+        w, idx = dm.moe_route(lg, bias, k, scoring, 1.5, token_ids=tok,
+                              tid2eid=tid2eid)
+        s = dm.gate_scores(lg, scoring)
+        for t in range(T):
+            row = tid2eid[min(max(int(tok[t]), 0), V - 1)]
+            np.testing.assert_array_equal(idx[t], row)
+            ws = s[t, row].astype(np.float64)
+            if scoring != "softmax":
+                ws = ws / ws.sum()
+            np.testing.assert_allclose(w[t], ws * 1.5, rtol=2e-6)
+
+
 def _brute_group(b, k, G, kg):
     E = b.size
     gs = E // G
