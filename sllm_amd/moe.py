@@ -241,11 +241,10 @@ class QwenMoE:
     def __init__(self, router_w, wg, wu, wd, wg_s=None, wu_s=None, wd_s=None,
                  sg=None, su=None, sd=None, sg_s=None, su_s=None, sd_s=None,
                  sgl=None, top_k=8, eps=1e-20, packed=True):
-        self.wdtype = 0 if wg_s is not None else 1
-        self.E, self.I, self.H = np.asarray(wg).shape
-        self.Is = 0 if su is None else np.asarray(su).shape[0]
-        self.top_k = int(top_k)
-        self.eps = float(eps)
+        wdtype = 0 if wg_s is not None else 1
+        E, I, H = np.asarray(wg).shape
+        Is = 0 if su is None else np.asarray(su).shape[0]
+        self.wdtype = wdtype
         cast = (lambda a: np.ascontiguousarray(a, np.uint8)) if self.wdtype == 0 \
             else (lambda a: to_bf16(a))
         b = {"router_w": _up(to_bf16(router_w)),
@@ -261,11 +260,27 @@ class QwenMoE:
                 b.update(sg_s=_up(np.asarray(sg_s, np.float32)),
                          su_s=_up(np.asarray(su_s, np.float32)),
                          sd_s=_up(np.asarray(sd_s, np.float32)))
-        if packed and self.wdtype == 0:
-            E, I, H, Is = self.E, self.I, self.H, self.Is
+        self._finish(b, E, I, H, Is, top_k, eps, wdtype, packed)
+
+    @classmethod
+    def from_device(cls, bufs, *, E, I, H, Is, top_k=8, eps=1e-20, packed=True):
+        """FP8 weights already resident on the device (for example from
+        sllm_amd.loader): the buffers of __init__'s layout -- router_w (bf16
+        bits), wg/wu/wd e4m3 codes with fp32 wg_s/wu_s/wd_s block scales,
+        optional shared sg/su/sd (+ scales) and sgl."""
+        self = cls.__new__(cls)
+        self._finish(dict(bufs), E, I, H, Is, top_k, eps, 0, packed)
+        return self
+
+    def _finish(self, b, E, I, H, Is, top_k, eps, wdtype, packed):
+        self.wdtype = wdtype
+        self.E, self.I, self.H, self.Is = int(E), int(I), int(H), int(Is)
+        self.top_k = int(top_k)
+        self.eps = float(eps)
+        if packed and wdtype == 0:
             b["wgu_packed"], _ = pack_weights(0, 1, b["wg"], b["wu"], E, I, H)
             b["wd_packed"], _ = pack_weights(0, 0, b["wd"], None, E, H, I)
-            if su is not None:
+            if Is:
                 b["sgu_packed"], _ = pack_weights(0, 1, b["sg"], b["su"], 1, Is, H)
                 b["sd_packed"], _ = pack_weights(0, 0, b["sd"], None, 1, H, Is)
         self._w = b
@@ -315,12 +330,9 @@ class DeepseekMoE:
                  s1_s=None, s3=None, s3_s=None, s2=None, s2_s=None, top_k=8,
                  n_group=1, topk_group=1, scoring="sigmoid", route_scale=1.0,
                  swiglu_limit=0.0, packed=True, tid2eid=None):
-        self.E, self.I = np.asarray(w1).shape[:2]
-        self.H = np.asarray(w2).shape[1]
-        self.Is = 0 if s1 is None else np.asarray(s1).shape[0]
-        self.top_k, self.n_group, self.topk_group = int(top_k), int(n_group), int(topk_group)
-        self.scoring, self.route_scale = scoring, float(route_scale)
-        self.swiglu_limit = float(swiglu_limit)
+        E, I = np.asarray(w1).shape[:2]
+        H = np.asarray(w2).shape[1]
+        Is = 0 if s1 is None else np.asarray(s1).shape[0]
         b = {"router_w": _up(to_bf16(router_w)),
              "bias": _up(np.asarray(bias, np.float32)) if bias is not None else None}
         for k, v in (("w1", w1), ("w1_s", w1_s), ("w3", w3), ("w3_s", w3_s),
@@ -331,13 +343,34 @@ class DeepseekMoE:
                 b[k] = _up(np.ascontiguousarray(v, np.uint8))
             for k, v in (("s1_s", s1_s), ("s3_s", s3_s), ("s2_s", s2_s)):
                 b[k] = _up(np.asarray(v, np.float32))
+        self._finish(b, E, I, H, Is, top_k, n_group, topk_group, scoring,
+                     route_scale, swiglu_limit, packed, tid2eid)
+
+    @classmethod
+    def from_device(cls, bufs, *, E, I, H, Is, top_k=8, n_group=1,
+                    topk_group=1, scoring="sigmoid", route_scale=1.0,
+                    swiglu_limit=0.0, packed=True, tid2eid=None):
+        """Weights already resident on the device (for example from
+        sllm_amd.loader): the buffers of __init__'s layout -- router_w (bf16
+        bits), bias (fp32 or None), packed e2m1 w1/w3/w2 with raw e8m0
+        w1_s/w3_s/w2_s, optional shared s1/s3/s2 e4m3 with fp32 scales."""
+        self = cls.__new__(cls)
+        self._finish(dict(bufs), E, I, H, Is, top_k, n_group, topk_group,
+                     scoring, route_scale, swiglu_limit, packed, tid2eid)
+        return self
+
+    def _finish(self, b, E, I, H, Is, top_k, n_group, topk_group, scoring,
+                route_scale, swiglu_limit, packed, tid2eid):
+        self.E, self.I, self.H, self.Is = int(E), int(I), int(H), int(Is)
+        self.top_k, self.n_group, self.topk_group = int(top_k), int(n_group), int(topk_group)
+        self.scoring, self.route_scale = scoring, float(route_scale)
+        self.swiglu_limit = float(swiglu_limit)
         if packed:
-            E, I, H, Is = self.E, self.I, self.H, self.Is
             b["w13_packed"], b["w13_s_packed"] = pack_weights(
                 1, 1, b["w1"], b["w3"], E, I, H, b["w1_s"], b["w3_s"])
             b["w2_packed"], b["w2_s_packed"] = pack_weights(
                 1, 0, b["w2"], None, E, H, I, b["w2_s"])
-            if s1 is not None:
+            if Is:
                 b["s13_packed"], _ = pack_weights(0, 1, b["s1"], b["s3"], 1, Is, H)
                 b["s2_packed"], _ = pack_weights(0, 0, b["s2"], None, 1, H, Is)
         # hash layer (ref/deepseek_v4.py:545-552): experts from the token-id

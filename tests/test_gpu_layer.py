@@ -191,6 +191,91 @@ def test_deepseek_hash_layer(T, mode):
         assert rel < 1e-4
 
 
+def _qwen_checkpoint(path, W, prefix, scale_tag):
+    """W in a Qwen FP8 checkpoint's naming: per-expert F8_E4M3 weights with
+    `weight_scale_inv` blocks stored as `scale_tag` (BF16 or F32)."""
+    from oracle.codecs import encode_bf16_rne
+    from sllm_amd.loader import write_safetensors
+
+    def sc(a):
+        return (("BF16", a.shape, encode_bf16_rne(a)) if scale_tag == "BF16"
+                else ("F32", a.shape, np.asarray(a, np.float32)))
+    t = {f"{prefix}.gate.weight": ("BF16", W.router_w.shape, encode_bf16_rne(W.router_w))}
+    mats = [("gate", W.wg_q, W.wg_s), ("up", W.wu_q, W.wu_s), ("down", W.wd_q, W.wd_s)]
+    for e in range(W.wg_q.shape[0]):
+        for m, q, sv in mats:
+            n = f"{prefix}.experts.{e}.{m}_proj.weight"
+            t[n] = ("F8_E4M3", q[e].shape, q[e])
+            t[n + "_scale_inv"] = sc(sv[e])
+    if W.has_shared:
+        for m, q, sv in [("gate", W.sg_q, W.sg_s), ("up", W.su_q, W.su_s),
+                         ("down", W.sd_q, W.sd_s)]:
+            n = f"{prefix}.shared_expert.{m}_proj.weight"
+            t[n] = ("F8_E4M3", q.shape, q)
+            t[n + "_scale_inv"] = sc(sv)
+        t[f"{prefix}.shared_expert_gate.weight"] = ("BF16", W.sgl.shape,
+                                                    encode_bf16_rne(W.sgl))
+    write_safetensors(path, t)
+
+
+@pytest.mark.parametrize("scale_tag", ["BF16", "F32"])
+def test_load_qwen_checkpoint(tmp_path, scale_tag):
+    """A layer loaded from checkpoint bytes (no host dequantization) equals
+    the layer built from the same arrays, bit for bit."""
+    from oracle.codecs import decode_bf16, encode_bf16_rne
+    from sllm_amd import loader
+    x, W = qwen_fp8(seed=21, T=96, H=512, E=8, I=256, Is=256)
+    if scale_tag == "BF16":  # the stored scales are the bf16-rounded ones
+        for a in ("wg_s", "wu_s", "wd_s", "sg_s", "su_s", "sd_s"):
+            setattr(W, a, decode_bf16(encode_bf16_rne(getattr(W, a))))
+    prefix = "model.language_model.layers.0.mlp"
+    p = str(tmp_path / "qwen.safetensors")
+    _qwen_checkpoint(p, W, prefix, scale_tag)
+    got = loader.load_qwen_moe(loader.Checkpoint(p), prefix, top_k=4)
+    want = qwen_layer(W, 4)
+    for mode in ("prefill", "decode"):
+        np.testing.assert_array_equal(got.forward(x, mode=mode),
+                                      want.forward(x, mode=mode))
+
+
+@pytest.mark.parametrize("hash_layer", [False, True])
+def test_load_deepseek_checkpoint(tmp_path, hash_layer):
+    """DeepSeek layer from converted-checkpoint bytes: packed E2M1 experts
+    with F8_E8M0 scales, F8_E4M3 shared expert with E8M0 128x128 scales."""
+    from oracle.codecs import encode_bf16_rne
+    from sllm_amd import loader
+    x, W = deepseek_mxfp4(seed=22, T=96, H=512, E=16, I=256, Is=256)
+    k, pre = 4, "layers.0."
+    rng = np.random.default_rng(22)
+    tid2eid = np.stack([rng.permutation(16)[:k] for _ in range(30)]).astype(np.int32)
+    tok = rng.integers(0, 30, x.shape[0]).astype(np.int32)
+
+    def e8(sv):  # fp32 powers of two -> e8m0 codes
+        return ((np.asarray(sv, np.float32).view(np.uint32) >> 23) & 0xFF).astype(np.uint8)
+    t = {f"{pre}ffn.gate.weight": ("BF16", W.router_w.shape, encode_bf16_rne(W.router_w)),
+         f"{pre}ffn.gate.bias": ("F32", W.bias.shape, W.bias),
+         "tid2eid": ("I32", tid2eid.shape, tid2eid)}
+    for e in range(16):
+        for w, q, sv in (("w1", W.w1_p, W.w1_s), ("w3", W.w3_p, W.w3_s),
+                         ("w2", W.w2_p, W.w2_s)):
+            t[f"{pre}ffn.experts.{e}.{w}.weight"] = ("U8", q[e].shape, q[e])
+            t[f"{pre}ffn.experts.{e}.{w}.scale"] = ("F8_E8M0", sv[e].shape, sv[e])
+    for w, q, sv in (("w1", W.s1_q, W.s1_s), ("w3", W.s3_q, W.s3_s),
+                     ("w2", W.s2_q, W.s2_s)):
+        t[f"{pre}ffn.shared_experts.{w}.weight"] = ("F8_E4M3", q.shape, q)
+        t[f"{pre}ffn.shared_experts.{w}.scale"] = ("F8_E8M0", sv.shape, e8(sv))
+    p = str(tmp_path / "ds.safetensors")
+    loader.write_safetensors(p, t)
+    route = dict(scoring="sigmoid", route_scale=2.5, swiglu_limit=10.0)
+    got = loader.load_deepseek_moe(loader.Checkpoint(p), pre, k,
+                                   hash_layer=hash_layer, **route)
+    want = deepseek_layer(W, k, tid2eid=tid2eid if hash_layer else None, **route)
+    kw = {"token_ids": tok} if hash_layer else {}
+    for mode in ("prefill", "decode"):
+        np.testing.assert_array_equal(got.forward(x, mode=mode, **kw),
+                                      want.forward(x, mode=mode, **kw))
+
+
 def test_deepseek_prefill_c4_shapes():
     """C4 geometry (H 7168, I = Is = 2048, top-8, 8 groups keep 4) with
     E = 32 experts and T = 256 tokens so the CPU oracle stays fast."""
