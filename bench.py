@@ -322,6 +322,107 @@ def run_loader(args):
     return 0
 
 
+# the hybrid family's dense MLP (recipes/schema.py:146 and :357 defaults)
+DENSE = dict(H=5120, I=17408)
+
+
+def run_device_decode(args):
+    """The device-decode drop-ins (sllm_amd.decode) at decode batch sizes.
+    MoE: the C2/C3 layer behind DeviceMoEStack; `hook_us` is the wall time
+    of one `moe(x, i)` call with host arrays (the contract of the reference's
+    Q4DeviceDecodeState._moe: bf16 conversion, upload, the fused layer,
+    download), `device_us` the same layer on device buffers (moe_dev) between
+    HIP events. Dense: a DENSE-shaped FP8 SwiGLU MLP behind DenseSwiGLU,
+    device time and HBM rate of its weight stream. L2 and MALL are flushed
+    with a 512 MiB fill before every timed call."""
+    import numpy as np
+    from sllm_amd import _lib
+    from sllm_amd.decode import DenseSwiGLU, DeviceMoEStack
+    from sllm_amd.moe import QwenMoE
+    from sllm_amd.runtime import (DeviceBuffer, Event, fill_normal, memset,
+                                  sync, to_bf16, to_device_raw)
+    c = dict(C2)
+    H, E, I, Is, k = c["H"], c["E"], c["I"], c["Is"], c["k"]
+    rng = np.random.default_rng(args.seed)
+    flush = DeviceBuffer(512 << 20)
+    iters = args.decode_iters
+
+    def dev_us(call):
+        a0, a1 = Event(), Event()
+        times = []
+        for it in range(iters + 3):
+            memset(flush, it & 0xFF, flush.nbytes)
+            a0.record()
+            call()
+            a1.record()
+            a1.synchronize()
+            if it >= 3:
+                times.append(a0.elapsed_ms(a1) * 1e3)
+        return statistics.median(times)
+
+    def host_us(call):
+        times = []
+        for it in range(iters + 3):
+            memset(flush, it & 0xFF, flush.nbytes)
+            sync()
+            t0 = time.perf_counter()
+            call()
+            if it >= 3:
+                times.append((time.perf_counter() - t0) * 1e6)
+        return statistics.median(times)
+
+    base = DeviceLayer(c, seed=args.seed)
+    w = {n: base.w[n] for n in ("router_w", "wg", "wg_s", "wu", "wu_s", "wd",
+                                "wd_s", "sg", "sg_s", "su", "su_s", "sd", "sd_s",
+                                "sgl", "wgu_packed", "wd_packed", "sgu_packed",
+                                "sd_packed")}
+    stack = DeviceMoEStack([QwenMoE.from_device(w, E=E, I=I, H=H, Is=Is, top_k=k)])
+    moe = {}
+    for B in (1, 8, 32):
+        x = to_bf16_values(rng.standard_normal((B, H)).astype(np.float32))
+        xd = to_device_raw(to_bf16(x))
+        od = DeviceBuffer(B * H * 4)
+        moe[str(B)] = {"hook_us": round(host_us(lambda: stack.moe(x, 0)), 1),
+                       "device_us": round(dev_us(lambda: stack.moe_dev(xd, od, 0, B)), 1)}
+        log(f"moe hook B={B}: {moe[str(B)]}")
+    del stack, base, w
+    sync()
+
+    Hd, Id = DENSE["H"], DENSE["I"]
+    L = _lib.lib()
+    tmp = DeviceBuffer(Id * Hd * 4)
+    b = {"router_w": to_device_raw(np.zeros(Hd, np.uint16))}
+    for j, (key, n, kk) in enumerate((("wg", Id, Hd), ("wu", Id, Hd), ("wd", Hd, Id))):
+        fill_normal(tmp, n * kk, args.seed * 1000 + 700 + j, 0.02)
+        b[key] = DeviceBuffer(n * kk)
+        b[key + "_s"] = DeviceBuffer((n // 128) * (kk // 128) * 4)
+        _lib.check(L.sllm_quantize_weight_fp8(tmp.ptr, n, kk, 0, b[key].ptr,
+                                              b[key + "_s"].ptr, None), "quantize")
+    sync()
+    tmp.free()
+    mlp = DenseSwiGLU(QwenMoE.from_device(b, E=1, I=Id, H=Hd, Is=0, top_k=1))
+    wbytes = 3 * Hd * Id + 3 * (Id // 128) * (Hd // 128) * 4
+    dense = {}
+    for B in (1, 8, 32):
+        x = to_bf16_values(rng.standard_normal((B, Hd)).astype(np.float32))
+        xd = to_device_raw(to_bf16(x))
+        od = DeviceBuffer(B * Hd * 4)
+        us = dev_us(lambda: mlp.forward_dev(xd, od, B))
+        nb = wbytes + B * Hd * 2 + B * Hd * 4
+        dense[str(B)] = {"device_us": round(us, 1), "bytes": nb,
+                         "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                         "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        if B == 1:
+            dense[str(B)]["hook_us"] = round(host_us(lambda: mlp(x)), 1)
+        log(f"dense B={B}: {dense[str(B)]}")
+    print(json.dumps({"metric": "device-decode drop-ins: per-call µs",
+                      "moe": {"config": "C3 (C2 shapes, FP8)", "batches": moe},
+                      "dense_mlp": {"config": {"hidden": Hd, "intermediate": Id,
+                                               "weights": "e4m3 + fp32 128x128 block scales"},
+                                    "batches": dense}}), flush=True)
+    return 0
+
+
 def _c4_routing_us(c, rng, reps=20):
     """The two DeepSeek routing kernels alone at C4 shape (synthetic fp32
     logits N(0,1)): group-limited sigmoid top-k with bias, and a hash layer
@@ -549,6 +650,9 @@ def main(argv=None) -> int:
                     help="only time loading a synthetic C2-shaped FP8 "
                          "checkpoint (safetensors, reference naming) to the "
                          "device and exit")
+    ap.add_argument("--device-decode", action="store_true",
+                    help="only time the device-decode drop-ins (MoE hook and "
+                         "dense SwiGLU MLP) at decode batch sizes and exit")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run the library's copy kernel over MIB MiB five "
                          "times (the known-size reference for scaling HBM "
@@ -582,6 +686,8 @@ def main(argv=None) -> int:
         return 0
     if args.loader:
         return run_loader(args)
+    if args.device_decode:
+        return run_device_decode(args)
     if args.config == "c4":
         return run_c4(args)
     if args.config == "c5":

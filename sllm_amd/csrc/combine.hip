@@ -74,6 +74,69 @@ __global__ __launch_bounds__(256) void combine_kernel(
   }
 }
 
+// fp32 rows (the decode paths), possibly as ks K-chunk slices (split-K).
+// A workgroup covers 256 columns of one token (so that a few tokens still
+// spread over many CUs); its 4 waves take every 4th of the topk * ks routed
+// slices and the ks_sh shared ones (slot-major, then K slice, then shared),
+// issue them in batches of 8 independent loads, and the 4 wave sums are
+// added in wave order through LDS: a fixed order for every call.
+constexpr int CF_WAVES = 4;
+constexpr int CF_COLS = 256;
+constexpr int CF_BATCH = 8;
+
+__global__ __launch_bounds__(64 * CF_WAVES) void combine_f32_kernel(
+    const float* __restrict__ y, const int* __restrict__ inv_pos, int topk,
+    const float* __restrict__ y_shared, int H, int out_f32,
+    void* __restrict__ out, int ks, long kstride, int ks_sh,
+    long kstride_sh) {
+  __shared__ int pos[64];
+  __shared__ float4 part[CF_WAVES][64];
+  const int t = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x < topk) pos[threadIdx.x] = inv_pos[(size_t)t * topk + threadIdx.x];
+  __syncthreads();
+  const int c = min(blockIdx.x * CF_COLS + lane * 4, H - 4);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int nr = topk * ks, nsl = nr + (y_shared ? ks_sh : 0);
+  for (int b = wave; b < nsl; b += CF_WAVES * CF_BATCH) {
+    float4 v[CF_BATCH];
+#pragma unroll
+    for (int u = 0; u < CF_BATCH; ++u) {
+      const int sl = min(b + u * CF_WAVES, nsl - 1);
+      const float* src =
+          sl < nr ? y + (sl % ks) * kstride + (size_t)pos[sl / ks] * H
+                  : y_shared + (sl - nr) * kstride_sh + (size_t)t * H;
+      v[u] = *(const float4*)(src + c);
+    }
+#pragma unroll
+    for (int u = 0; u < CF_BATCH; ++u) {
+      if (b + u * CF_WAVES < nsl) {
+        acc.x += v[u].x;
+        acc.y += v[u].y;
+        acc.z += v[u].z;
+        acc.w += v[u].w;
+      }
+    }
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0 || blockIdx.x * CF_COLS + lane * 4 >= H) return;
+#pragma unroll
+  for (int w = 1; w < CF_WAVES; ++w) {
+    const float4 q = part[w][lane];
+    acc.x += q.x;
+    acc.y += q.y;
+    acc.z += q.z;
+    acc.w += q.w;
+  }
+  if (out_f32) {
+    *(float4*)((float*)out + (size_t)t * H + c) = acc;
+  } else {
+    *(uint2*)((uint16_t*)out + (size_t)t * H + c) =
+        make_uint2((uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16),
+                   (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16));
+  }
+}
+
 int launch_combine(const void* y, int y_f32, const int* inv_pos, int topk,
                    const void* y_shared, int T, int H, int out_f32, void* out,
                    hipStream_t st) {
@@ -81,13 +144,32 @@ int launch_combine(const void* y, int y_f32, const int* inv_pos, int topk,
   SLLM_REQUIRE(T > 0 && H % 8 == 0 && topk > 0 && topk <= 64,
                "combine: bad sizes (T=%d H=%d k=%d)", T, H, topk);
   if (y_f32)
-    combine_kernel<float><<<T, 256, 0, st>>>((const float*)y, inv_pos, topk,
-                                             (const float*)y_shared, H,
-                                             out_f32, out);
+    return launch_combine_split((const float*)y, inv_pos, topk,
+                                (const float*)y_shared, T, H, out_f32, out, 1,
+                                0, 1, 0, st);
   else
     combine_kernel<uint16_t><<<T, 256, 0, st>>>(
         (const uint16_t*)y, inv_pos, topk, (const uint16_t*)y_shared, H,
         out_f32, out);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_combine_split(const float* y, const int* inv_pos, int topk,
+                         const float* y_shared, int T, int H, int out_f32,
+                         void* out, int ks, long kstride, int ks_sh,
+                         long kstride_sh, hipStream_t st) {
+  SLLM_REQUIRE(y && inv_pos && out, "combine: null pointer");
+  SLLM_REQUIRE(T > 0 && T < 65536 && H % 4 == 0 && H >= 4 && topk > 0 &&
+                   topk <= 64 &&
+                   ks >= 1 && ks_sh >= 1 && kstride % 4 == 0 &&
+                   kstride_sh % 4 == 0,
+               "combine: bad sizes (T=%d H=%d k=%d ks=%d/%d)", T, H, topk, ks,
+               ks_sh);
+  const dim3 grid((H + CF_COLS - 1) / CF_COLS, T);
+  combine_f32_kernel<<<grid, 64 * CF_WAVES, 0, st>>>(y, inv_pos, topk, y_shared,
+                                                  H, out_f32, out, ks, kstride,
+                                                  ks_sh, kstride_sh);
   SLLM_LAUNCHED();
   return 0;
 }

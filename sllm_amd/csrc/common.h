@@ -100,19 +100,49 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+// Maxima through DPP lane moves instead of LDS shuffles (a top-k makes
+// one such reduction per selected element, so their latency adds up): xor 1
+// and xor 2 within quads, half-row and row mirrors (max over 16 lanes in
+// every lane of a row), then row_bcast15 / row_bcast31 carry the row maxima
+// up so that lane 63 holds the wave's; readlane broadcasts it. Lanes a row
+// mask leaves out keep `ident`, the identity of the max.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t ident) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, CTRL,
+                                               ROW_MASK, 0xF, false);
 }
 
+__device__ __forceinline__ float wave_max(float v) {
+  const uint32_t ni = __float_as_uint(-INFINITY);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x141>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x140>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x142, 0xA>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x143, 0xC>(__float_as_uint(v), ni)));
+  return __uint_as_float(
+      (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
+  const uint64_t w =
+      ((uint64_t)dpp_u32<CTRL, ROW_MASK>((uint32_t)(v >> 32), 0u) << 32) |
+      dpp_u32<CTRL, ROW_MASK>((uint32_t)v, 0u);
+  return w > v ? w : v;
+}
+
+// keys are >= 0 (0 = no candidate)
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
-  return v;
+  v = dpp_max_u64_step<0xB1>(v);
+  v = dpp_max_u64_step<0x4E>(v);
+  v = dpp_max_u64_step<0x141>(v);
+  v = dpp_max_u64_step<0x140>(v);
+  v = dpp_max_u64_step<0x142, 0xA>(v);
+  v = dpp_max_u64_step<0x143, 0xC>(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ float silu_f32(float x) {

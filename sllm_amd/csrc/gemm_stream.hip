@@ -24,6 +24,7 @@
 //   activation rows through that XCD's L2.
 // * Item descriptors and gathered row indices of a workgroup's items are
 //   loaded into LDS once at the start.
+#include <algorithm>
 #include <type_traits>
 
 #include "launch.h"
@@ -717,7 +718,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
 
   auto seg_items_dec = [&](const SegDesc& S) {
     const int rt = S.tile_info ? *S.num_tiles : (S.total_rows + SD_BM - 1) / SD_BM;
-    return rt * (S.N / NTW);
+    return rt * (S.N / NTW) * S.ksplit;
   };
   const int n0 = seg_items_dec(S0);
   const int n1 = nseg > 1 ? seg_items_dec(S1) : 0;
@@ -735,7 +736,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     const SegDesc& S = seg ? S1 : S0;
     const int li = seg ? it - n0 : it;
     const int ntn = S.N / NTW;
-    const int rt = li / ntn, nt = li % ntn;
+    const int q = li / S.ksplit, kc = li % S.ksplit;
+    const int rt = q / ntn, nt = q % ntn;
     int e = 0, rb, rows;
     if (S.tile_info) {
       const int4 d = *(const int4*)(S.tile_info + 4 * rt);
@@ -746,7 +748,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       rb = rt * SD_BM;
       rows = min(SD_BM, S.total_rows - rb);
     }
-    desc[tid] = make_int4(seg | (nt << 1), e, rb, rows);
+    // x: segment (bit 0), column slab (bits 1-15), K chunk (bits 16-30)
+    desc[tid] = make_int4(seg | (nt << 1) | (kc << 16), e, rb, rows);
   }
   __syncthreads();
   for (int q = tid; q < nitems * SD_BM; q += ST_THREADS) {
@@ -765,8 +768,20 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   }
   __syncthreads();
 
+  // K steps [kb0, kb0 + nkb) of item i: chunk kc of ksplit near-equal parts
+  auto kchunk = [&](int i, int& kb0, int& nkb) {
+    const int x = desc[i].x;
+    const SegDesc& S = (x & 1) ? S1 : S0;
+    const int KB = S.K / 128, kc = x >> 16;
+    kb0 = kc * KB / S.ksplit;
+    nkb = (kc + 1) * KB / S.ksplit - kb0;
+  };
   int total_steps = 0;
-  for (int i = 0; i < nitems; ++i) total_steps += ((desc[i].x & 1) ? S1.K : S0.K) / 128;
+  for (int i = 0; i < nitems; ++i) {
+    int kb0, nkb;
+    kchunk(i, kb0, nkb);
+    total_steps += nkb;
+  }
 
   // activation tile of a K step: 16 rows x 128 values; thread tid takes row
   // tid / 32 and values [4 (tid % 32), +4)
@@ -788,12 +803,13 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   const uint16_t* ps4 = nullptr;
   auto p_enter = [&](int i) {
     const int4 d = desc[i];
-    const int seg = d.x & 1, nt = d.x >> 1;
+    const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF;
     const SegDesc& S = seg ? S1 : S0;
     const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
-    pKB = KB;
-    pa = S.a + ((size_t)rsrc[i][a_row] * K + a_col) * (MODE == 0 ? 2 : 4);
-    const size_t blk0 = ((size_t)d.y * NT + nt) * KB;
+    int kb0;
+    kchunk(i, kb0, pKB);
+    pa = S.a + ((size_t)rsrc[i][a_row] * K + kb0 * 128 + a_col) * (MODE == 0 ? 2 : 4);
+    const size_t blk0 = ((size_t)d.y * NT + nt) * KB + kb0;
     if constexpr (BF == SF_FP4) {
       pb = S.wp + blk0 * BLK + (wave * 2) * 1024 + lane * 16;
       ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
@@ -804,7 +820,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
         ps1 = (const float*)S.s1 + blk0;
       } else {
         const int nblk = nt * 2 + wave / 4;
-        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB;
+        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB + kb0;
       }
     }
   };
@@ -848,17 +864,17 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
 
   int ci = 0, ckb = 0, cKB = 1, crows = 0;
   auto c_enter = [&](int i) {
-    const int4 d = desc[i];
-    cKB = ((d.x & 1) ? S1.K : S0.K) / 128;
-    crows = d.w;
+    int kb0;
+    kchunk(i, kb0, cKB);
+    crows = desc[i].w;
   };
 
   // acc[s][v]: token lc of the tile, output column 4 lg + v of subtile s
   auto epilogue = [&](int i) {
     const int4 d = desc[i];
-    const int seg = d.x & 1, nt = d.x >> 1;
+    const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF, kc = d.x >> 16;
     const SegDesc& S = seg ? S1 : S0;
-    if (lc < d.w) {
+    if (lc < d.w) {  // mode 1 writes K chunk kc's slice (kc = 0 unsplit)
       const float rw = rwl[i][lc];
       if constexpr (MODE == 0) {
         float h[4];
@@ -876,7 +892,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       } else {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          float* out = (float*)S.y + (size_t)(d.z + lc) * S.N + nt * 256 + wave * 32 + s * 16 + lg * 4;
+          float* out = (float*)S.y + kc * S.pstride + (size_t)(d.z + lc) * S.N +
+                       nt * 256 + wave * 32 + s * 16 + lg * 4;
           *(float4*)out = make_float4(acc[s][0] * rw, acc[s][1] * rw,
                                       acc[s][2] * rw, acc[s][3] * rw);
         }
@@ -965,6 +982,20 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
 }
 
+// Decode down projections cut each item's K range into chunks until the
+// launch has about DEC_TARGET_ITEMS items (two per CU), so that a few long
+// items (one expert: a dense MLP, a single token) do not leave most CUs
+// idle; the chunk results are summed by the combine.
+constexpr long DEC_TARGET_ITEMS = 512;
+constexpr int DEC_MAX_KSPLIT = 32;
+
+int dec_ksplit(long upper_items, int KB) {
+  if (upper_items <= 0 || KB <= 1) return 1;
+  long ks = (DEC_TARGET_ITEMS + upper_items - 1) / upper_items;
+  ks = std::min<long>(ks, std::min(KB, DEC_MAX_KSPLIT));
+  return (int)std::max<long>(ks, 1);
+}
+
 static int num_cus() {
   static int n = 0;
   if (n == 0) {
@@ -1051,16 +1082,18 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   return 0;
 }
 
-int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
-                      int topk, float limit, long upper_items,
-                      hipStream_t st) {
+int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
+                      const SegDesc* s1_in, int topk, float limit,
+                      long upper_items, hipStream_t st) {
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1),
                "stream decode gemm: bad format");
   const int ntw = mode == 0 ? 128 : 256;
-  for (const SegDesc* s : {&s0, s1}) {
-    if (!s) continue;
+  SegDesc seg[2] = {s0_in, s1_in ? *s1_in : s0_in};
+  for (int i = 0; i < (s1_in ? 2 : 1); ++i) {
+    SegDesc* s = &seg[i];
+    if (s->ksplit < 1) s->ksplit = 1;
     SLLM_REQUIRE(s->a && s->wp && s->s0 && s->N % ntw == 0 &&
-                     s->K % 128 == 0 && s->K > 0,
+                     s->K % 128 == 0 && s->K > 0 && s->N / ntw < 32768,
                  "stream decode gemm: bad segment (N=%d K=%d)", s->N, s->K);
     SLLM_REQUIRE(mode == 1 ? s->y != nullptr : s->hq != nullptr,
                  "stream decode gemm: missing outputs");
@@ -1068,7 +1101,14 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                  "stream decode gemm: missing W3 scales");
     SLLM_REQUIRE((!s->gather && !s->row_w_by_idx) || s->sorted_idx,
                  "stream decode gemm: gather / row_w_by_idx need sorted_idx");
+    SLLM_REQUIRE(s->ksplit <= s->K / 128 && s->ksplit < 32768 &&
+                     (s->ksplit == 1 ||
+                      (mode == 1 && s->pstride > 0 && s->pstride % 4 == 0)),
+                 "stream decode gemm: bad K split %d (K=%d, mode %d)",
+                 s->ksplit, s->K, mode);
   }
+  const SegDesc& s0 = seg[0];
+  const SegDesc* s1 = s1_in ? &seg[1] : nullptr;
 #define GO(B, M) return go_stream_dec<B, M>(s0, s1, topk, limit, upper_items, st)
   if (mode == 0) {
     if (bf == SF_FP4) GO(SF_FP4, 0);

@@ -85,6 +85,11 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   uint8_t* hq;             // mode 0 outputs at permuted row p
   float* hs;
   uint16_t* y;             // mode 1 output at permuted row p
+  // decode mode 1 split-K: each (row tile, column slab) item is cut into
+  // ksplit K chunks (0 / 1: none) whose partial rows land in y slices
+  // pstride elements apart, summed by launch_combine_split
+  int ksplit;
+  long pstride;
 };
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
@@ -98,6 +103,9 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
                       hipStream_t st);
+// K chunks for a decode down launch whose item count is at most
+// upper_items over KB 128-wide K steps.
+int dec_ksplit(long upper_items, int KB);
 long packed_bytes(int fp4, int up, int E, int N, int K);
 long packed_scale_bytes(int up, int E, int N, int K);
 
@@ -111,5 +119,11 @@ int launch_gemv(int wf, int swiglu, const void* act, int act_bf16,
 int launch_combine(const void* y, int y_f32, const int* inv_pos, int topk,
                    const void* y_shared, int T, int H, int out_f32, void* out,
                    hipStream_t st);
+// fp32 rows held as ks / ks_sh K-chunk slices kstride / kstride_sh
+// elements apart (split-K decode); summed slice by slice in order.
+int launch_combine_split(const float* y, const int* inv_pos, int topk,
+                         const float* y_shared, int T, int H, int out_f32,
+                         void* out, int ks, long kstride, int ks_sh,
+                         long kstride_sh, hipStream_t st);
 
 }  // namespace sllm

@@ -14,6 +14,8 @@
 //           MFMA GEMMs over ragged row tiles.
 //  decode:  fp32 activations against dequantized weights in a
 //           bandwidth-bound GEMV over the touched experts only.
+#include <algorithm>
+
 #include "../../include/sllm_moe.h"
 #include "launch.h"
 
@@ -27,6 +29,8 @@ struct Plan {
   bool decode;
   int N;          // T * topk
   int bm, max_tiles;
+  // decode: K chunks of the streamed down launches (routed / shared)
+  int ks_dn, ks_dn_sh;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh;
   size_t total;
@@ -43,9 +47,14 @@ static bool pick_decode(int mode, int T) {
          (mode == SLLM_MOE_MODE_AUTO && T <= DECODE_MAX_T);
 }
 
+// separate_shared: the shared expert's streamed projections are launches
+// of their own (DeepSeek: other weight format) rather than a second segment
+// of the routed ones.
 static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
-                      bool has_shared, bool need_logits, bool force_gemv) {
+                      bool has_shared, bool need_logits, bool force_gemv,
+                      bool separate_shared = false) {
   Plan p{};
+  p.ks_dn = p.ks_dn_sh = 1;
   p.decode = force_gemv || pick_decode(mode, T);
   p.N = T * topk;
   if (p.decode) {
@@ -68,10 +77,22 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.pscr = take(c, permute_scratch_bytes(p.N, E));
   p.gate = take(c, (size_t)T * 4);
   if (p.decode) {
+    if (!force_gemv) {  // the streamed kernels (the GEMV path does not split)
+      const long rt = p.max_tiles;
+      const long sh_rt = has_shared ? (T + DECODE_BM - 1) / DECODE_BM : 0;
+      if (separate_shared) {
+        p.ks_dn = dec_ksplit(rt * (H / 256), I / 128);
+        if (has_shared) p.ks_dn_sh = dec_ksplit(sh_rt * (H / 256), Is / 128);
+      } else {
+        p.ks_dn = p.ks_dn_sh =
+            dec_ksplit(rt * (H / 256) + sh_rt * (H / 256),
+                       (has_shared ? std::min(I, Is) : I) / 128);
+      }
+    }
     p.hq = take(c, (size_t)p.N * I * 4);                      // h fp32
     p.hq_sh = has_shared ? take(c, (size_t)T * Is * 4) : 0;   // h_sh fp32
-    p.y = take(c, (size_t)p.N * H * 4);                       // y fp32
-    p.y_sh = has_shared ? take(c, (size_t)T * H * 4) : 0;
+    p.y = take(c, (size_t)p.ks_dn * p.N * H * 4);             // y fp32 slices
+    p.y_sh = has_shared ? take(c, (size_t)p.ks_dn_sh * T * H * 4) : 0;
   } else {
     p.xq = take(c, (size_t)T * H);
     p.sx = take(c, (size_t)T * (H / 128) * 4);
@@ -267,15 +288,22 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       r2.tile_info = tiles; r2.num_tiles = ntiles;
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
       r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
+      r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
       s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
       s2.wp = (const uint8_t*)a->sd_packed; s2.s0 = a->sd_s; s2.N = H;
       s2.K = Is; s2.row_w = gate; s2.y = (uint16_t*)y_sh;
+      s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
             launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
-                              (long)p.max_tiles * (H / 256) + sh_rt * (H / 256),
+                              (long)p.max_tiles * (H / 256) * p.ks_dn +
+                                  sh_rt * (H / 256) * p.ks_dn_sh,
                               st));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
+      STAGE(clk, SLLM_MOE_STAGE_COMBINE,
+            launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32, a->out,
+                                 p.ks_dn, (long)p.N * H, p.ks_dn_sh,
+                                 (long)T * H, st));
     } else {
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
@@ -298,9 +326,9 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
             nullptr, (const uint8_t*)a->sd, a->sd_s, nullptr,
             nullptr, H, Is, gate, 0.f, y_sh, st));
     }
-    }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
+    }
   } else {
     uint8_t* xq = (uint8_t*)(ws + p.xq);
     float* sx = (float*)(ws + p.sx);
@@ -383,7 +411,7 @@ long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
   }
   const bool sh = a->s1 != nullptr;
   return (long)make_plan(a->T, a->H, a->E, a->I, sh ? a->Is : 0, a->topk,
-                         a->mode, sh, !a->logits_given, false)
+                         a->mode, sh, !a->logits_given, false, true)
       .total;
 }
 
@@ -403,7 +431,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   const int Is = sh ? a->Is : 0;
   const float L = a->swiglu_limit;
   const Plan p = make_plan(T, H, E, I, Is, k, a->mode, sh, !a->logits_given,
-                           false);
+                           false, true);
   SLLM_REQUIRE(a->workspace_bytes >= (long)p.total,
                "sllm_moe_ds_forward: workspace %ld < %zu bytes",
                a->workspace_bytes, p.total);
@@ -459,12 +487,13 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.tile_info = tiles; r2.num_tiles = ntiles;
     r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
     r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
+    r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_stream_dec(2, 0, r1, nullptr, k, L,
                             (long)p.max_tiles * (I / 128), st));
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
           launch_stream_dec(2, 1, r2, nullptr, k, 0.f,
-                            (long)p.max_tiles * (H / 256), st));
+                            (long)p.max_tiles * (H / 256) * p.ks_dn, st));
     if (sh) {
       SegDesc s1{};
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
@@ -474,13 +503,17 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
       s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
       s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
+      s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
             launch_stream_dec(1, 0, s1, nullptr, k, L, sh_rt * (Is / 128), st));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
-            launch_stream_dec(1, 1, s2, nullptr, k, 0.f, sh_rt * (H / 256), st));
+            launch_stream_dec(1, 1, s2, nullptr, k, 0.f,
+                              sh_rt * (H / 256) * p.ks_dn_sh, st));
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
-          launch_combine(y, 1, inv, k, y_sh, T, H, a->out_f32, a->out, st));
+          launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32, a->out,
+                               p.ks_dn, (long)p.N * H, p.ks_dn_sh,
+                               (long)T * H, st));
   } else if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);

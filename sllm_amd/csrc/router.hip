@@ -274,7 +274,7 @@ __device__ __forceinline__ void route_softmax_token(
         pe = p[i];
         key[i] = 0;
       }
-    pe = __shfl(pe, owner, kWave);
+    pe = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pe), owner));
     wsum += pe;
     if (lane == kk) {
       mine = pe;
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
         se = sc[i];
         key[i] = 0;
       }
-    se = __shfl(se, owner, kWave);
+    se = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(se), owner));
     wsum += se;
     if (lane == kk) {
       mine = se;

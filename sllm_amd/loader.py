@@ -259,6 +259,24 @@ def load_qwen_moe(ckpt: Checkpoint, prefix: str, top_k: int, eps: float = 1e-20,
                                packed=packed)
 
 
+def load_dense_mlp(ckpt: Checkpoint, prefix: str, packed: bool = True):
+    """A dense FP8 SwiGLU MLP at `prefix` (`{prefix}.{gate,up,down}_proj.weight`
+    F8_E4M3 + `weight_scale_inv`) as a one-expert, top-1 QwenMoE with a zero
+    router (the form sllm_amd.decode.DenseSwiGLU runs)."""
+    from .moe import QwenMoE
+    I, H = ckpt.spec(f"{prefix}.gate_proj.weight")[1]
+    b = {"router_w": to_device_raw(np.zeros(H, np.uint16))}
+    for key, m, shape in (("wg", "gate", (I, H)), ("wu", "up", (I, H)),
+                          ("wd", "down", (H, I))):
+        n = f"{prefix}.{m}_proj.weight"
+        b[key] = _stack(ckpt, [n], ("F8_E4M3",), shape)
+        s = scale_f32(ckpt, n + "_scale_inv")
+        if s.shape != (_cdiv(shape[0], 128), _cdiv(shape[1], 128)):
+            raise CheckpointError(f"{n}_scale_inv is {s.shape}, not 128x128 blocks")
+        b[key + "_s"] = to_device_raw(np.ascontiguousarray(s, np.float32))
+    return QwenMoE.from_device(b, E=1, I=I, H=H, Is=0, top_k=1, packed=packed)
+
+
 def load_deepseek_moe(ckpt: Checkpoint, prefix: str, top_k: int, n_group=1,
                       topk_group=1, scoring="sigmoid", route_scale=1.0,
                       swiglu_limit=0.0, packed: bool = True,

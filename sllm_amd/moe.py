@@ -267,7 +267,9 @@ class QwenMoE:
         """FP8 weights already resident on the device (for example from
         sllm_amd.loader): the buffers of __init__'s layout -- router_w (bf16
         bits), wg/wu/wd e4m3 codes with fp32 wg_s/wu_s/wd_s block scales,
-        optional shared sg/su/sd (+ scales) and sgl."""
+        optional shared sg/su/sd (+ scales) and sgl. Streaming-layout
+        buffers already in `bufs` (wgu_packed, wd_packed, sgu_packed,
+        sd_packed) are used as they are instead of packed again."""
         self = cls.__new__(cls)
         self._finish(dict(bufs), E, I, H, Is, top_k, eps, 0, packed)
         return self
@@ -277,7 +279,7 @@ class QwenMoE:
         self.E, self.I, self.H, self.Is = int(E), int(I), int(H), int(Is)
         self.top_k = int(top_k)
         self.eps = float(eps)
-        if packed and wdtype == 0:
+        if packed and wdtype == 0 and "wgu_packed" not in b:
             b["wgu_packed"], _ = pack_weights(0, 1, b["wg"], b["wu"], E, I, H)
             b["wd_packed"], _ = pack_weights(0, 0, b["wd"], None, E, H, I)
             if Is:

@@ -172,6 +172,38 @@ def deepseek_layer(W, top_k, packed=True, **route):
                        W.w2_p, W.w2_s, top_k=top_k, **kw, **route)
 
 
+def qwen_checkpoint_tensors(W, prefix, scale_tag="BF16"):
+    """W in a Qwen FP8 checkpoint's naming under `prefix` (a `.mlp` block):
+    per-expert F8_E4M3 weights with `weight_scale_inv` blocks stored as
+    `scale_tag` (BF16 or F32), BF16 router and shared-expert gate. Returns
+    {name: (dtype tag, shape, array)} for sllm_amd.loader.write_safetensors."""
+    def sc(a):
+        return (("BF16", a.shape, codecs.encode_bf16_rne(a)) if scale_tag == "BF16"
+                else ("F32", a.shape, np.asarray(a, np.float32)))
+    t = {f"{prefix}.gate.weight": ("BF16", W.router_w.shape,
+                                   codecs.encode_bf16_rne(W.router_w))}
+    mats = [("gate", W.wg_q, W.wg_s), ("up", W.wu_q, W.wu_s), ("down", W.wd_q, W.wd_s)]
+    for e in range(W.wg_q.shape[0]):
+        for m, q, sv in mats:
+            n = f"{prefix}.experts.{e}.{m}_proj.weight"
+            t[n] = ("F8_E4M3", q[e].shape, q[e])
+            t[n + "_scale_inv"] = sc(sv[e])
+    if W.has_shared:
+        for m, q, sv in [("gate", W.sg_q, W.sg_s), ("up", W.su_q, W.su_s),
+                         ("down", W.sd_q, W.sd_s)]:
+            n = f"{prefix}.shared_expert.{m}_proj.weight"
+            t[n] = ("F8_E4M3", q.shape, q)
+            t[n + "_scale_inv"] = sc(sv)
+        t[f"{prefix}.shared_expert_gate.weight"] = ("BF16", W.sgl.shape,
+                                                    codecs.encode_bf16_rne(W.sgl))
+    return t
+
+
+def qwen_checkpoint(path, W, prefix, scale_tag="BF16"):
+    from sllm_amd.loader import write_safetensors
+    write_safetensors(path, qwen_checkpoint_tensors(W, prefix, scale_tag))
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

@@ -14,8 +14,8 @@ from oracle import deepseek_moe as dm
 from oracle import qwen_moe as qm
 
 from tests._fixtures import (certified_route_ties, deepseek_layer,
-                             deepseek_mxfp4, deepseek_mxfp4_gpu, qwen_fp8,
-                             qwen_fp8_gpu, qwen_layer, rel_l2)
+                             deepseek_mxfp4, deepseek_mxfp4_gpu, qwen_checkpoint,
+                             qwen_fp8, qwen_fp8_gpu, qwen_layer, rel_l2)
 
 pytestmark = pytest.mark.gpu
 
@@ -191,33 +191,6 @@ def test_deepseek_hash_layer(T, mode):
         assert rel < 1e-4
 
 
-def _qwen_checkpoint(path, W, prefix, scale_tag):
-    """W in a Qwen FP8 checkpoint's naming: per-expert F8_E4M3 weights with
-    `weight_scale_inv` blocks stored as `scale_tag` (BF16 or F32)."""
-    from oracle.codecs import encode_bf16_rne
-    from sllm_amd.loader import write_safetensors
-
-    def sc(a):
-        return (("BF16", a.shape, encode_bf16_rne(a)) if scale_tag == "BF16"
-                else ("F32", a.shape, np.asarray(a, np.float32)))
-    t = {f"{prefix}.gate.weight": ("BF16", W.router_w.shape, encode_bf16_rne(W.router_w))}
-    mats = [("gate", W.wg_q, W.wg_s), ("up", W.wu_q, W.wu_s), ("down", W.wd_q, W.wd_s)]
-    for e in range(W.wg_q.shape[0]):
-        for m, q, sv in mats:
-            n = f"{prefix}.experts.{e}.{m}_proj.weight"
-            t[n] = ("F8_E4M3", q[e].shape, q[e])
-            t[n + "_scale_inv"] = sc(sv[e])
-    if W.has_shared:
-        for m, q, sv in [("gate", W.sg_q, W.sg_s), ("up", W.su_q, W.su_s),
-                         ("down", W.sd_q, W.sd_s)]:
-            n = f"{prefix}.shared_expert.{m}_proj.weight"
-            t[n] = ("F8_E4M3", q.shape, q)
-            t[n + "_scale_inv"] = sc(sv)
-        t[f"{prefix}.shared_expert_gate.weight"] = ("BF16", W.sgl.shape,
-                                                    encode_bf16_rne(W.sgl))
-    write_safetensors(path, t)
-
-
 @pytest.mark.parametrize("scale_tag", ["BF16", "F32"])
 def test_load_qwen_checkpoint(tmp_path, scale_tag):
     """A layer loaded from checkpoint bytes (no host dequantization) equals
@@ -230,7 +203,7 @@ def test_load_qwen_checkpoint(tmp_path, scale_tag):
             setattr(W, a, decode_bf16(encode_bf16_rne(getattr(W, a))))
     prefix = "model.language_model.layers.0.mlp"
     p = str(tmp_path / "qwen.safetensors")
-    _qwen_checkpoint(p, W, prefix, scale_tag)
+    qwen_checkpoint(p, W, prefix, scale_tag)
     got = loader.load_qwen_moe(loader.Checkpoint(p), prefix, top_k=4)
     want = qwen_layer(W, 4)
     for mode in ("prefill", "decode"):
