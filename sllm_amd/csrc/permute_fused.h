@@ -62,7 +62,10 @@ __device__ __forceinline__ void permute_fused_body(
     const int v = ids[min(a, N - 1)];
     idv[g] = a < a1 ? v : -1;
   }
-  for (int q = tid; q < PERM_FUSED_WAVES * E; q += 1024) hist[q / E][q % E] = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < PERM_FUSED_WAVES; ++w) hist[w][tid] = 0;
+  }
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < PERM_FUSED_G; ++g) {

@@ -221,8 +221,89 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
 // --------------------------------------------------------------------------
 // softmax top-k with renormalisation (ref/qwen4_exp.py:118-140)
 // --------------------------------------------------------------------------
+// Top-k keys: the order key of the value (f32_order_key) in the high half,
+// ~e in the low half, so that a larger key is a larger value and, among
+// equal values, the lower expert id e; 0 = no candidate.
+__device__ __forceinline__ uint64_t topk_key(float v, int e) {
+  return ((uint64_t)f32_order_key(v) << 32) |
+         (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+__device__ __forceinline__ float topk_key_value(uint64_t key) {
+  const uint32_t k = (uint32_t)(key >> 32);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+__device__ __forceinline__ int topk_key_id(uint64_t key) {
+  return (int)(0xFFFFFFFFu - (uint32_t)key);
+}
+
+// Descending sorting networks (2, 4, 8 inputs: 1, 5, 19 comparators).
+template <int N>
+__device__ __forceinline__ void sort_desc(uint64_t (&k)[N]) {
+  auto ce = [&](int i, int j) {
+    const uint64_t a = k[i], b = k[j];
+    const bool sw = b > a;
+    k[i] = sw ? b : a;
+    k[j] = sw ? a : b;
+  };
+  if constexpr (N == 2) {
+    ce(0, 1);
+  } else if constexpr (N == 4) {
+    ce(0, 1); ce(2, 3); ce(0, 2); ce(1, 3); ce(1, 2);
+  } else if constexpr (N == 8) {
+    ce(0, 2); ce(1, 3); ce(4, 6); ce(5, 7);
+    ce(0, 4); ce(1, 5); ce(2, 6); ce(3, 7);
+    ce(0, 1); ce(2, 3); ce(4, 5); ce(6, 7);
+    ce(2, 4); ce(3, 5);
+    ce(1, 4); ce(3, 6);
+    ce(1, 2); ce(3, 4); ce(5, 6);
+  }
+}
+
+// Descending top-k of the wave's candidate keys (candidate e = lane + 64 i
+// in key[i]); lane j < topk returns pick j's key (0 past the candidates).
+// Up to 8 keys per lane: each lane sorts its keys once, then every pick
+// is one wave maximum of the lanes' heads and a pop on the owning lane.
+// More keys per lane: every pick takes the lane maxima afresh.
+template <int EPL>
+__device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
+                                                   int topk) {
+  const int lane = threadIdx.x & 63;
+  uint64_t mine = 0;
+  if constexpr (EPL <= 8) {
+    sort_desc<EPL>(key);
+    for (int kk = 0; kk < topk; ++kk) {
+      const uint64_t best = wave_max_u64(key[0]);
+      if (lane == kk) mine = best;
+      if (lane == (topk_key_id(best) & 63)) {
+#pragma unroll
+        for (int i = 0; i + 1 < EPL; ++i) key[i] = key[i + 1];
+        key[EPL - 1] = 0;
+      }
+    }
+  } else {
+    for (int kk = 0; kk < topk; ++kk) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
+      best = wave_max_u64(best);
+      if (lane == kk) mine = best;
+      const int e = topk_key_id(best);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (lane == (e & 63) && i == (e >> 6)) key[i] = 0;
+    }
+  }
+  return mine;
+}
+
 // One token's softmax top-k on the calling wave: row = the token's E logits;
 // lanes j < topk write slot j of w_row / id_row (and of id_lds when given).
+// The selection runs on the logits (softmax is monotone in them); pick j's
+// probability is exp(l - max) / sum recomputed from its key, and the
+// weights are those probabilities over their sum in pick order plus eps
+// (ref/qwen4_exp.py:118-140).
 template <int EPL>
 __device__ __forceinline__ void route_softmax_token(
     const float* __restrict__ row, int E, int topk, float eps,
@@ -237,52 +318,23 @@ __device__ __forceinline__ void route_softmax_token(
     m = fmaxf(m, v[i]);
   }
   m = wave_max(m);
-  float p[EPL];
   float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + 64 * i;
-    p[i] = e < E ? expf(v[i] - m) : 0.f;
-    s += p[i];
-  }
-  s = wave_sum(s);
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) p[i] = p[i] / s;
-
   uint64_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + 64 * i;
-    key[i] = e < E ? (((uint64_t)f32_order_key(v[i]) << 32) |
-                      (uint64_t)(0xFFFFFFFFu - (uint32_t)e))
-                   : 0ull;
+    s += e < E ? expf(v[i] - m) : 0.f;
+    key[i] = e < E ? topk_key(v[i], e) : 0ull;
   }
+  s = wave_sum(s);
+  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
+  const float pn = expf(topk_key_value(pick) - m) / s;  // lane j: pick j
   float wsum = 0.f;
-  float mine = 0.f;  // lane j < topk keeps slot j's probability
-  int myid = 0;
-  for (int kk = 0; kk < topk; ++kk) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-    best = wave_max_u64(best);
-    int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
-    int owner = e & 63, slot = e >> 6;
-    float pe = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane == owner && i == slot) {
-        pe = p[i];
-        key[i] = 0;
-      }
-    pe = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pe), owner));
-    wsum += pe;
-    if (lane == kk) {
-      mine = pe;
-      myid = e;
-    }
-  }
+  for (int j = 0; j < topk; ++j)
+    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pn), j));
   if (lane < topk) {
-    w_row[lane] = mine / (wsum + eps);
+    const int myid = topk_key_id(pick);
+    w_row[lane] = pn / (wsum + eps);
     id_row[lane] = myid;
     if (id_lds) id_lds[lane] = myid;
   }
@@ -382,6 +434,7 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
     float* __restrict__ w_out, int* __restrict__ id_out, int T, int E,
     int topk, int n_group, int topk_group, int scoring, float route_scale) {
   __shared__ float sb[4][EPL * 64];
+  __shared__ float scl[4][EPL * 64];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int t_raw = blockIdx.x * 4 + wv;
@@ -434,33 +487,15 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
   for (int i = 0; i < EPL; ++i) {
     int e = lane + 64 * i;
     bool ok = e < E && (keep_all || ((gkeep >> (e / gs)) & 1ull));
-    key[i] = ok ? (((uint64_t)f32_order_key(b[i]) << 32) |
-                   (uint64_t)(0xFFFFFFFFu - (uint32_t)e))
-                : 0ull;
+    key[i] = ok ? topk_key(b[i], e) : 0ull;
+    if (e < E) scl[wv][e] = sc[i];  // the picks' unbiased scores, by id
   }
-  float wsum = 0.f, mine = 0.f;
-  int myid = 0;
-  for (int kk = 0; kk < topk; ++kk) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-    best = wave_max_u64(best);
-    int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
-    int owner = e & 63, slot = e >> 6;
-    float se = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane == owner && i == slot) {
-        se = sc[i];
-        key[i] = 0;
-      }
-    se = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(se), owner));
-    wsum += se;
-    if (lane == kk) {
-      mine = se;
-      myid = e;
-    }
-  }
+  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
+  const int myid = topk_key_id(pick);
+  const float mine = lane < topk ? scl[wv][min(max(myid, 0), E - 1)] : 0.f;
+  float wsum = 0.f;
+  for (int j = 0; j < topk; ++j)
+    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mine), j));
   if (active && lane < topk) {
     float wv_ = scoring == SCORE_SOFTMAX ? mine : mine / wsum;
     w_out[(size_t)t * topk + lane] = wv_ * route_scale;
