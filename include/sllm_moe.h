@@ -57,6 +57,16 @@ int sllm_buf_d2h_raw(void* dst, const void* src, long nbytes);
 long sllm_mem_free_bytes(void);
 /* ref kernels.cu:425 / _sllm_cuda.py:384-386 */
 int sllm_sync(void);
+/* new (no reference counterpart; the decode hook's host boundary, for
+ * kernels/q4_device_decode.py:316-339 callers that pass host arrays):
+ * page-locked host staging, stream-ordered copies in either direction
+ * (hipMemcpyDefault), a stream wait, and fp32 -> bf16 bits on the host with
+ * round to nearest even. */
+void* sllm_host_new(long nbytes);
+int sllm_host_free(void* p);
+int sllm_copy_async(void* dst, const void* src, long nbytes, void* stream);
+int sllm_stream_sync(void* stream);
+int sllm_host_f32_to_bf16(void* dst, const float* src, long n);
 
 /* ---------------------------------------------------------------------- */
 /* Measurement and synthetic-data helpers (new; no reference counterpart:  */

@@ -77,6 +77,11 @@ SIGNATURES = {
     "sllm_buf_d2h_raw": (c_int, [P, P, c_long]),
     "sllm_mem_free_bytes": (c_long, []),
     "sllm_sync": (c_int, []),
+    "sllm_host_new": (c_void_p, [c_long]),
+    "sllm_host_free": (c_int, [P]),
+    "sllm_copy_async": (c_int, [P, P, c_long, P]),
+    "sllm_stream_sync": (c_int, [P]),
+    "sllm_host_f32_to_bf16": (c_int, [P, P, c_long]),
     "sllm_event_new": (c_void_p, []),
     "sllm_event_free": (c_int, [P]),
     "sllm_event_record": (c_int, [P, P]),

@@ -130,6 +130,53 @@ int sllm_buf_d2h_raw(void* dst, const void* src, long nbytes) {
   return 0;
 }
 
+void* sllm_host_new(long nbytes) {
+  if (nbytes <= 0) {
+    set_error("sllm_host_new: nbytes must be positive");
+    return nullptr;
+  }
+  void* p = nullptr;
+  if (hipHostMalloc(&p, (size_t)nbytes, hipHostMallocDefault) != hipSuccess) {
+    set_error("sllm_host_new: hipHostMalloc of %ld bytes failed", nbytes);
+    return nullptr;
+  }
+  return p;
+}
+
+int sllm_host_free(void* p) {
+  if (!p) return 0;
+  SLLM_HIP(hipDeviceSynchronize());  // queued copies may still use it
+  SLLM_HIP(hipHostFree(p));
+  return 0;
+}
+
+int sllm_copy_async(void* dst, const void* src, long nbytes, void* stream) {
+  SLLM_REQUIRE(dst && src && nbytes >= 0, "sllm_copy_async: bad args");
+  if (nbytes == 0) return 0;
+  SLLM_HIP(hipMemcpyAsync(dst, src, (size_t)nbytes, hipMemcpyDefault,
+                          (hipStream_t)stream));
+  return 0;
+}
+
+int sllm_stream_sync(void* stream) {
+  SLLM_HIP(hipStreamSynchronize((hipStream_t)stream));
+  return 0;
+}
+
+// Host-side fp32 -> bf16 bits, round to nearest even on the 32-bit pattern
+// (the carry of 0xFFFFFFFF wraps to 0, as in a 16-bit truncation of the
+// widened sum).
+int sllm_host_f32_to_bf16(void* dst, const float* src, long n) {
+  SLLM_REQUIRE(dst && src && n >= 0, "sllm_host_f32_to_bf16: bad args");
+  const uint32_t* u = (const uint32_t*)src;
+  uint16_t* d = (uint16_t*)dst;
+  for (long i = 0; i < n; ++i) {
+    const uint64_t v = (uint64_t)u[i] + 0x7FFFu + ((u[i] >> 16) & 1u);
+    d[i] = (uint16_t)(v >> 16);
+  }
+  return 0;
+}
+
 long sllm_mem_free_bytes(void) {
   size_t fr = 0, tot = 0;
   if (hipMemGetInfo(&fr, &tot) != hipSuccess) {

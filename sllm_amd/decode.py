@@ -29,25 +29,53 @@ stored e4m3 + 128x128 block-scale format.
 
 from __future__ import annotations
 
-from ctypes import c_void_p
+from ctypes import c_float, c_void_p
 
 import numpy as np
 
 from . import _lib
 from .moe import QwenMoE, _qwen_args, qwen_workspace_bytes
-from .runtime import DeviceBuffer, memset, ptr, stream_handle, sync, to_bf16
+from .runtime import DeviceBuffer, memset, ptr, stream_handle, sync
 
 TEXT_PREFIX = "model.language_model"
 
 
+class _Pinned:
+    """Page-locked host staging (sllm_host_new)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = _lib.lib().sllm_host_new(self.nbytes)
+        if not self.ptr:
+            raise RuntimeError("sllm_host_new failed: " + _lib.last_error())
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                _lib.lib().sllm_host_free(c_void_p(self.ptr))
+                self.ptr = None
+        except Exception:
+            pass
+
+
 class _Runner:
     """Calls the fused layer for a QwenMoE at decode sizes, reusing the
-    bf16 input staging, the output buffer, the workspace and the argument
-    block of each (layer, n)."""
+    device input staging, the output buffer, the workspace, the argument
+    block of each (layer, n) and page-locked host staging: a host call is
+    one host bf16 rounding, an upload, the layer and a download, ordered on
+    one stream with one wait."""
 
     def __init__(self):
         self._x = self._out = self._ws = self._zl = None
+        self._hx = self._hy = None
         self._args = {}
+
+    def _pin(self, name, nbytes):
+        b = getattr(self, name)
+        if b is None or b.nbytes < nbytes:
+            b = _Pinned(max(int(nbytes), 64))
+            setattr(self, name, b)
+        return b
 
     def _grow(self, name, nbytes):
         b = getattr(self, name)
@@ -92,19 +120,21 @@ class _Runner:
         x = np.asarray(x, np.float32)
         if x.ndim != 2 or x.shape[1] != layer.H:
             raise ValueError(f"x must be (n, {layer.H}), got {x.shape}")
-        n = x.shape[0]
+        n, cnt = x.shape[0], x.size
+        x = np.ascontiguousarray(x)
         a = self.args(layer, n, zero_logits)
+        hx, hy = self._pin("_hx", cnt * 2), self._pin("_hy", cnt * 4)
         L = _lib.lib()
-        xb = np.ascontiguousarray(to_bf16(x))
-        _lib.check(L.sllm_buf_h2d_raw(c_void_p(self._x.ptr),
-                                      xb.ctypes.data_as(c_void_p), xb.nbytes),
-                   "sllm_buf_h2d_raw")
+        _lib.check(L.sllm_host_f32_to_bf16(c_void_p(hx.ptr), x.ctypes.data_as(c_void_p),
+                                           cnt), "sllm_host_f32_to_bf16")
+        _lib.check(L.sllm_copy_async(c_void_p(self._x.ptr), c_void_p(hx.ptr),
+                                     cnt * 2, None), "sllm_copy_async")
         _lib.check(L.sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
-        y = np.empty((n, layer.H), np.float32)
-        _lib.check(L.sllm_buf_d2h_raw(y.ctypes.data_as(c_void_p),
-                                      c_void_p(self._out.ptr), y.nbytes),
-                   "sllm_buf_d2h_raw")
-        return y
+        _lib.check(L.sllm_copy_async(c_void_p(hy.ptr), c_void_p(self._out.ptr),
+                                     cnt * 4, None), "sllm_copy_async")
+        _lib.check(L.sllm_stream_sync(None), "sllm_stream_sync")
+        return np.ctypeslib.as_array((c_float * cnt).from_address(hy.ptr)) \
+            .reshape(n, layer.H).copy()
 
     def run_dev(self, layer: QwenMoE, x, out, n, zero_logits=False,
                 out_f32=True, stream=None) -> None:

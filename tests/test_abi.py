@@ -70,3 +70,22 @@ def test_error_contract_without_gpu():
     with pytest.raises(RuntimeError, match="rc=-1"):
         _lib.check(rc, "q4 kernel")
     assert q4.available()
+
+
+def test_host_bf16_rounding_matches_python():
+    """sllm_host_f32_to_bf16 (host code, no GPU) against runtime.to_bf16 on
+    random values and the patterns where rounding carries or wraps."""
+    import numpy as np
+    from sllm_amd import _lib
+    from sllm_amd.runtime import to_bf16
+    rng = np.random.default_rng(5)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000,
+                        0x7F800001, 0x7F7FFFFF, 0x00000001, 0x3F808000,
+                        0x3F818000, 0x3F80FFFF, 0xFFFFFFFF, 0x7FFFFFFF],
+                       np.uint32)
+    bits = np.concatenate([rng.integers(0, 2**32, 4096, dtype=np.uint64)
+                           .astype(np.uint32), special])
+    x = bits.view(np.float32)
+    got = np.empty(x.size, np.uint16)
+    _lib.check(_lib.lib().sllm_host_f32_to_bf16(got.ctypes.data, x.ctypes.data, x.size))
+    np.testing.assert_array_equal(got, to_bf16(x))
