@@ -4,31 +4,36 @@
 
 namespace sllm {
 
+// ks > 1 (T <= 64 only; router_ksplit): the router GEMM writes ks partial
+// logit slices T * E floats apart, and the routing launches given the same
+// ks add them in order (storing the sum into slice 0).
+int router_ksplit(int T, int H);
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
-                       int T, int E, int H, hipStream_t st);
+                       int T, int E, int H, hipStream_t st, int ks = 1);
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
-                         int E, int topk, float eps, hipStream_t st);
+                         int E, int topk, float eps, hipStream_t st,
+                         int ks = 1);
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).
 int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
                              float* logits, int T, int E, int H,
                              const uint16_t* sgl, float* gate_out,
-                             hipStream_t st);
+                             hipStream_t st, int ks = 1);
 bool route_permute_small_fits(int T, int E, int topk);
 int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int E, int topk, float eps, int bm,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
-                               int max_tiles, hipStream_t st);
+                               int max_tiles, hipStream_t st, int ks = 1);
 int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,
-                         hipStream_t st);
+                         hipStream_t st, int ks = 1);
 int launch_route_hash(const float* logits, const int* token_ids,
                       const int* tid2eid, int vocab, float* w, int* ids,
                       int T, int E, int topk, int scoring, float route_scale,
-                      hipStream_t st);
+                      hipStream_t st, int ks = 1);
 size_t permute_scratch_bytes(int N, int E);
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,

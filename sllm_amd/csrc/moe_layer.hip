@@ -29,8 +29,9 @@ struct Plan {
   bool decode;
   int N;          // T * topk
   int bm, max_tiles;
-  // decode: K chunks of the streamed down launches (routed / shared)
-  int ks_dn, ks_dn_sh;
+  // decode: K chunks of the streamed down launches (routed / shared) and
+  // partial-logit slices of the router GEMM
+  int ks_dn, ks_dn_sh, ks_r;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh;
   size_t total;
@@ -55,6 +56,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
                       bool separate_shared = false) {
   Plan p{};
   p.ks_dn = p.ks_dn_sh = 1;
+  p.ks_r = p.decode && need_logits ? router_ksplit(T, H) : 1;
   p.decode = force_gemv || pick_decode(mode, T);
   p.N = T * topk;
   if (p.decode) {
@@ -65,7 +67,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N);
   }
   size_t c = 0;
-  p.logits = need_logits ? take(c, (size_t)T * E * 4) : 0;
+  p.logits = need_logits ? take(c, (size_t)p.ks_r * T * E * 4) : 0;
   p.w = take(c, (size_t)p.N * 4);
   p.ids = take(c, (size_t)p.N * 4);
   p.counts = take(c, (size_t)E * 4);
@@ -231,7 +233,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
           launch_router_small_gate((const uint16_t*)a->x,
                                    (const uint16_t*)a->router_w, logits, T, E,
                                    H, sh ? (const uint16_t*)a->sgl : nullptr,
-                                   sh ? gate : nullptr, st));
+                                   sh ? gate : nullptr, st, p.ks_r));
     gate_done = sh;
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
@@ -244,11 +246,11 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
-                                     ntiles, p.max_tiles, st));
+                                     ntiles, p.max_tiles, st, p.ks_r));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-          launch_route_softmax(logits, w, ids, T, E, k, eps, st));
+          launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st));
@@ -454,14 +456,15 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
         a->logits_given ? 0
                         : launch_router_gemm((const uint16_t*)a->x,
                                              (const uint16_t*)a->router_w,
-                                             logits, T, E, H, st));
+                                             logits, T, E, H, st, p.ks_r));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
         a->tid2eid
             ? launch_route_hash(logits, a->token_ids, a->tid2eid, a->vocab, w,
-                                ids, T, E, k, a->scoring, a->route_scale, st)
+                                ids, T, E, k, a->scoring, a->route_scale, st,
+                                p.ks_r)
             : launch_route_grouped(logits, a->bias, w, ids, T, E, k,
                                    a->n_group, a->topk_group, a->scoring,
-                                   a->route_scale, st));
+                                   a->route_scale, st, p.ks_r));
   STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
         launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
                        ntiles, p.max_tiles, ws + p.pscr, st));

@@ -16,6 +16,8 @@
 // - sigmoid routing selects by the fp32 biased score s + bias, where
 //   s = fp32(1 / (1 + exp(-x))) is evaluated in fp64 as the reference does
 //   (ref/deepseek_v4.py:526-528), ties to the lower expert id.
+#include <algorithm>
+
 #include "launch.h"
 #include "permute_fused.h"
 
@@ -156,64 +158,70 @@ __global__ __launch_bounds__(256, 1) void router_gemm_kernel(
 // through LDS.
 constexpr int RG_SMALL_T = 64;
 
-// With gate_out, one extra workgroup (after the E / 16 expert tiles)
-// computes the shared-expert gate sigmoid(x . sgl) of every token (its 16
-// weight rows all read sgl; column 0 is kept).
+// Decode-size router GEMM: workgroup (x, q) computes experts [16 x, +16)
+// over K chunk q of gridDim.y (32-wide K slices split evenly), all NTI
+// 16-token tiles, and writes its partial logits to slice q (q T E floats
+// in); the routing kernels add the slices in order. With gate_out, one
+// extra workgroup (x = E / 16, q = 0, whole K) computes the shared-expert
+// gate sigmoid(x . sgl) of every token (its 16 weight rows all read sgl;
+// column 0 is kept).
+template <int NTI>
 __global__ __launch_bounds__(512) void router_gemm_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     float* __restrict__ logits, int T, int E, int H,
     const uint16_t* __restrict__ sgl, float* __restrict__ gate_out) {
-  __shared__ float part[8][RG_SMALL_T][16];
+  __shared__ float part[8][NTI * 16][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int e0 = blockIdx.x * 16;
   const bool gate_tile = e0 >= E;
-  const int nti = (T + 15) / 16;
+  if (gate_tile && blockIdx.y > 0) return;  // the gate takes the whole K
+  const int nsl = H / 32, ks = gate_tile ? 1 : gridDim.y, q = blockIdx.y;
+  const int s0 = q * nsl / ks, s1 = (q + 1) * nsl / ks;
   const uint16_t* brow = (gate_tile ? sgl : w + (size_t)min(e0 + lr, E - 1) * H) + lg * 8;
-  const uint16_t* arow[4];
+  const uint16_t* arow[NTI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NTI; ++i)
     arow[i] = x + (size_t)min(i * 16 + lr, T - 1) * H + lg * 8;
-  f32x4 acc[4];
+  f32x4 acc[NTI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  // the wave's K slices (w, w + 8, ...) in groups of 4, all loads of a group
-  // in flight together (rows past T re-read row T - 1; slices past H are
-  // clamped and skipped)
-  const int nsl = H / 32;
-  for (int g0 = wave; g0 < nsl; g0 += 32) {
-    bf16x8 b[4], a[4][4];
+  for (int i = 0; i < NTI; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // the wave's K slices (s0 + w, s0 + w + 8, ...) in groups of 4, all loads
+  // of a group in flight together (rows past T re-read row T - 1; slices
+  // past the chunk are clamped and skipped)
+  for (int g0 = s0 + wave; g0 < s1; g0 += 32) {
+    bf16x8 b[4], a[4][NTI];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int k0 = min(g0 + 8 * j, nsl - 1) * 32;
+      const int k0 = min(g0 + 8 * j, s1 - 1) * 32;
       b[j] = *(const bf16x8*)(brow + k0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[j][i] = *(const bf16x8*)(arow[i] + k0);
+      for (int i = 0; i < NTI; ++i) a[j][i] = *(const bf16x8*)(arow[i] + k0);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (g0 + 8 * j < nsl) {
+      if (g0 + 8 * j < s1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i < nti)
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][i], b[j], acc[i], 0, 0, 0);
+        for (int i = 0; i < NTI; ++i)
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][i], b[j], acc[i], 0, 0, 0);
       }
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NTI; ++i)
 #pragma unroll
     for (int v = 0; v < 4; ++v) part[wave][i * 16 + lg * 4 + v][lr] = acc[i][v];
   __syncthreads();
-  for (int q = threadIdx.x; q < T * 16; q += 512) {
-    const int r = q >> 4, c = q & 15;
+  float* out = logits + (size_t)q * T * E;
+  for (int qq = threadIdx.x; qq < T * 16; qq += 512) {
+    const int r = qq >> 4, c = qq & 15;
     float s = 0.f;
 #pragma unroll
     for (int wv = 0; wv < 8; ++wv) s += part[wv][r][c];
     if (gate_tile) {
       if (c == 0) gate_out[r] = sigmoid_f32(s);
     } else if (e0 + c < E) {
-      logits[(size_t)r * E + e0 + c] = s;
+      out[(size_t)r * E + e0 + c] = s;
     }
   }
 }
@@ -298,6 +306,20 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
   return mine;
 }
 
+// Logit e of a row held as ks K-chunk slices kstride floats apart (the
+// split decode router GEMM), added in slice order. With several slices the
+// owning wave (store) writes the sum back into slice 0, which then holds
+// the logits the routing used (the debug copy reads slice 0).
+__device__ __forceinline__ float logit_sum(float* row, int e, int ks,
+                                           long kstride, bool store = true) {
+  float v = row[e];
+  if (ks > 1) {
+    for (int q = 1; q < ks; ++q) v += row[q * kstride + e];
+    if (store) row[e] = v;
+  }
+  return v;
+}
+
 // One token's softmax top-k on the calling wave: row = the token's E logits;
 // lanes j < topk write slot j of w_row / id_row (and of id_lds when given).
 // The selection runs on the logits (softmax is monotone in them); pick j's
@@ -306,7 +328,7 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
 // (ref/qwen4_exp.py:118-140).
 template <int EPL>
 __device__ __forceinline__ void route_softmax_token(
-    const float* __restrict__ row, int E, int topk, float eps,
+    float* row, int ks, long kstride, int E, int topk, float eps,
     float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
   const int lane = threadIdx.x & 63;
   float v[EPL];
@@ -314,7 +336,7 @@ __device__ __forceinline__ void route_softmax_token(
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     int e = lane + 64 * i;
-    v[i] = e < E ? row[e] : -INFINITY;
+    v[i] = e < E ? logit_sum(row, e, ks, kstride) : -INFINITY;
     m = fmaxf(m, v[i]);
   }
   m = wave_max(m);
@@ -342,11 +364,11 @@ __device__ __forceinline__ void route_softmax_token(
 
 template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
-    const float* __restrict__ logits, float* __restrict__ w_out,
-    int* __restrict__ id_out, int T, int E, int topk, float eps) {
+    float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
+    int E, int topk, float eps, int ks) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  route_softmax_token<EPL>(logits + (size_t)t * E, E, topk, eps,
+  route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
                            w_out + (size_t)t * topk, id_out + (size_t)t * topk,
                            nullptr);
 }
@@ -356,18 +378,18 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
 // expert-major permutation in one workgroup, the ids passed through LDS.
 template <int EPL>
 __global__ __launch_bounds__(1024) void route_permute_small_kernel(
-    const float* __restrict__ logits, float* __restrict__ w_out,
-    int* __restrict__ id_out, int T, int E, int topk, float eps, int nbits,
-    int bm, int* __restrict__ counts, int* __restrict__ offsets,
-    int* __restrict__ sorted_idx, int* __restrict__ inv_pos,
-    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles) {
+    float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
+    int E, int topk, float eps, int nbits, int bm, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted_idx,
+    int* __restrict__ inv_pos, int* __restrict__ tile_info,
+    int* __restrict__ num_tiles, int max_tiles, int ks) {
   __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
   __shared__ int sh[1024];
   __shared__ int ids_lds[PERM_FUSED_MAX_N];
   const int wave = threadIdx.x >> 6;
   for (int t = wave; t < T; t += PERM_FUSED_WAVES)
-    route_softmax_token<EPL>(logits + (size_t)t * E, E, topk, eps,
-                             w_out + (size_t)t * topk,
+    route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk,
+                             eps, w_out + (size_t)t * topk,
                              id_out + (size_t)t * topk, ids_lds + t * topk);
   __syncthreads();
   permute_fused_body(ids_lds, T * topk, E, nbits, bm, counts, offsets,
@@ -385,7 +407,8 @@ enum Scoring { SCORE_SOFTMAX = 0, SCORE_SIGMOID = 1, SCORE_SQRTSOFTPLUS = 2 };
 // lane + 64 i): softmax in fp64 (ref/deepseek_v4.py:524-525), sigmoid in
 // fp64 then fp32 (:526-528), sqrt(softplus) (:529-530, :534-537).
 template <int EPL>
-__device__ __forceinline__ void gate_scores_row(const float* __restrict__ row,
+__device__ __forceinline__ void gate_scores_row(float* row, int ks,
+                                                long kstride, bool store,
                                                 int E, int scoring,
                                                 float (&sc)[EPL]) {
   const int lane = threadIdx.x & 63;
@@ -395,7 +418,7 @@ __device__ __forceinline__ void gate_scores_row(const float* __restrict__ row,
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       int e = lane + 64 * i;
-      xv[i] = e < E ? (double)row[e] : -INFINITY;
+      xv[i] = e < E ? (double)logit_sum(row, e, ks, kstride, store) : -INFINITY;
       m = xv[i] > m ? xv[i] : m;
     }
 #pragma unroll
@@ -417,7 +440,7 @@ __device__ __forceinline__ void gate_scores_row(const float* __restrict__ row,
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       int e = lane + 64 * i;
-      double xv = e < E ? (double)row[e] : 0.0;
+      double xv = e < E ? (double)logit_sum(row, e, ks, kstride, store) : 0.0;
       if (scoring == SCORE_SIGMOID) {
         sc[i] = (float)(1.0 / (1.0 + exp(-xv)));
       } else {
@@ -430,9 +453,9 @@ __device__ __forceinline__ void gate_scores_row(const float* __restrict__ row,
 
 template <int EPL>
 __global__ __launch_bounds__(256) void route_grouped_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias,
-    float* __restrict__ w_out, int* __restrict__ id_out, int T, int E,
-    int topk, int n_group, int topk_group, int scoring, float route_scale) {
+    float* logits, const float* __restrict__ bias, float* __restrict__ w_out,
+    int* __restrict__ id_out, int T, int E, int topk, int n_group,
+    int topk_group, int scoring, float route_scale, int ks) {
   __shared__ float sb[4][EPL * 64];
   __shared__ float scl[4][EPL * 64];
   const int lane = threadIdx.x & 63;
@@ -441,7 +464,9 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
   const bool active = t_raw < T;
   const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
   float sc[EPL];
-  gate_scores_row<EPL>(logits + (size_t)t * E, E, scoring, sc);
+  // waves past T mirror row T - 1 without writing it
+  gate_scores_row<EPL>(logits + (size_t)t * E, ks, (long)T * E, active, E,
+                       scoring, sc);
   float b[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -511,10 +536,10 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
 // through LDS so that lane j can read the score of its slot's expert.
 template <int EPL>
 __global__ __launch_bounds__(256) void route_hash_kernel(
-    const float* __restrict__ logits, const int* __restrict__ token_ids,
+    float* logits, const int* __restrict__ token_ids,
     const int* __restrict__ tid2eid, int vocab, float* __restrict__ w_out,
     int* __restrict__ id_out, int T, int E, int topk, int scoring,
-    float route_scale) {
+    float route_scale, int ks) {
   __shared__ float sb[4][EPL * 64];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -522,7 +547,9 @@ __global__ __launch_bounds__(256) void route_hash_kernel(
   const bool active = t_raw < T;
   const int t = active ? t_raw : T - 1;
   float sc[EPL];
-  gate_scores_row<EPL>(logits + (size_t)t * E, E, scoring, sc);
+  // waves past T mirror row T - 1 without writing it
+  gate_scores_row<EPL>(logits + (size_t)t * E, ks, (long)T * E, active, E,
+                       scoring, sc);
 #pragma unroll
   for (int i = 0; i < EPL; ++i)
     if (lane + 64 * i < E) sb[wv][lane + 64 * i] = sc[i];
@@ -549,15 +576,37 @@ static int epl_for(int E) {
   return epl;
 }
 
+int router_ksplit(int T, int H) {
+  if (T > RG_SMALL_T) return 1;
+  return std::max(1, std::min(8, H / 256));
+}
+
+static int launch_router_small(const uint16_t* x, const uint16_t* w,
+                               float* logits, int T, int E, int H,
+                               const uint16_t* sgl, float* gate_out, int ks,
+                               hipStream_t st) {
+  SLLM_REQUIRE(ks >= 1 && ks <= H / 32, "router_small: bad K split %d", ks);
+  const dim3 grid(ceil_div(E, 16) + (gate_out ? 1 : 0), ks);
+  switch (ceil_div(T, 16)) {
+    case 1: router_gemm_small_kernel<1><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
+    case 2: router_gemm_small_kernel<2><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
+    case 3: router_gemm_small_kernel<3><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
+    default: router_gemm_small_kernel<4><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
-                       int T, int E, int H, hipStream_t st) {
+                       int T, int E, int H, hipStream_t st, int ks) {
   SLLM_REQUIRE(x && w && logits, "router_gemm: null pointer");
   SLLM_REQUIRE(T > 0 && E > 0 && H > 0 && H % 128 == 0,
                "router_gemm: need T,E>0 and H %% 128 == 0 (T=%d E=%d H=%d)",
                T, E, H);
+  SLLM_REQUIRE(ks == 1 || T <= RG_SMALL_T, "router_gemm: K split needs T <= %d",
+               RG_SMALL_T);
   if (T <= RG_SMALL_T) {
-    router_gemm_small_kernel<<<ceil_div(E, 16), 512, 0, st>>>(
-        x, w, logits, T, E, H, nullptr, nullptr);
+    return launch_router_small(x, w, logits, T, E, H, nullptr, nullptr, ks, st);
   } else {
     dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
     router_gemm_kernel<<<grid, 256, 0, st>>>(x, w, logits, T, E, H);
@@ -569,14 +618,11 @@ int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
 int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
                              float* logits, int T, int E, int H,
                              const uint16_t* sgl, float* gate_out,
-                             hipStream_t st) {
+                             hipStream_t st, int ks) {
   SLLM_REQUIRE(x && w && logits && T > 0 && T <= RG_SMALL_T && E > 0 &&
                    H % 32 == 0 && (!gate_out || sgl),
                "router_small_gate: bad args (T=%d E=%d H=%d)", T, E, H);
-  router_gemm_small_kernel<<<ceil_div(E, 16) + (gate_out ? 1 : 0), 512, 0,
-                             st>>>(x, w, logits, T, E, H, sgl, gate_out);
-  SLLM_LAUNCHED();
-  return 0;
+  return launch_router_small(x, w, logits, T, E, H, sgl, gate_out, ks, st);
 }
 
 // One workgroup routes every token (a wave per token): worth it only while
@@ -591,7 +637,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int E, int topk, float eps, int bm,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
-                               int max_tiles, hipStream_t st) {
+                               int max_tiles, hipStream_t st, int ks) {
+  SLLM_REQUIRE(ks >= 1, "route_permute_small: bad logit slices %d", ks);
   SLLM_REQUIRE(logits && w && ids && route_permute_small_fits(T, E, topk) &&
                    topk > 0 && topk <= E && topk <= 64 && T > 0,
                "route_permute_small: bad sizes (T=%d E=%d k=%d)", T, E, topk);
@@ -601,8 +648,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
 #define CASE(n)                                                               \
   case n:                                                                     \
     route_permute_small_kernel<n><<<1, 1024, 0, st>>>(                        \
-        logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,          \
-        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles);                \
+        (float*)logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,  \
+        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks);            \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16)
 #undef CASE
@@ -614,8 +661,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
 }
 
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
-                         int E, int topk, float eps, hipStream_t st) {
-  SLLM_REQUIRE(logits && w && ids, "route_softmax: null pointer");
+                         int E, int topk, float eps, hipStream_t st, int ks) {
+  SLLM_REQUIRE(logits && w && ids && ks >= 1, "route_softmax: null pointer");
   SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
                    topk <= 64,
                "route_softmax: need 0<topk<=E<=2048, topk<=64 (E=%d k=%d)",
@@ -624,8 +671,8 @@ int launch_route_softmax(const float* logits, float* w, int* ids, int T,
   switch (epl_for(E)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
-    route_softmax_kernel<n><<<grid, 256, 0, st>>>(logits, w, ids, T, E,       \
-                                                  topk, eps);                 \
+    route_softmax_kernel<n><<<grid, 256, 0, st>>>((float*)logits, w, ids, T,  \
+                                                  E, topk, eps, ks);          \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE
@@ -637,8 +684,8 @@ int launch_route_softmax(const float* logits, float* w, int* ids, int T,
 int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,
-                         hipStream_t st) {
-  SLLM_REQUIRE(logits && w && ids, "route_grouped: null pointer");
+                         hipStream_t st, int ks) {
+  SLLM_REQUIRE(logits && w && ids && ks >= 1, "route_grouped: null pointer");
   SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
                    topk <= 64,
                "route_grouped: need 0<topk<=E<=2048, topk<=64");
@@ -656,8 +703,8 @@ int launch_route_grouped(const float* logits, const float* bias, float* w,
 #define CASE(n)                                                               \
   case n:                                                                     \
     route_grouped_kernel<n><<<grid, 256, 0, st>>>(                            \
-        logits, bias, w, ids, T, E, topk, n_group, topk_group, scoring,       \
-        route_scale);                                                         \
+        (float*)logits, bias, w, ids, T, E, topk, n_group, topk_group,        \
+        scoring, route_scale, ks);                                            \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE
@@ -669,8 +716,8 @@ int launch_route_grouped(const float* logits, const float* bias, float* w,
 int launch_route_hash(const float* logits, const int* token_ids,
                       const int* tid2eid, int vocab, float* w, int* ids,
                       int T, int E, int topk, int scoring, float route_scale,
-                      hipStream_t st) {
-  SLLM_REQUIRE(logits && token_ids && tid2eid && w && ids,
+                      hipStream_t st, int ks) {
+  SLLM_REQUIRE(logits && token_ids && tid2eid && w && ids && ks >= 1,
                "route_hash: null pointer");
   SLLM_REQUIRE(T > 0 && E > 0 && E <= 2048 && topk > 0 && topk <= 64 &&
                    topk <= E && vocab > 0 && scoring >= 0 && scoring <= 2,
@@ -680,9 +727,10 @@ int launch_route_hash(const float* logits, const int* token_ids,
   switch (epl_for(E)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
-    route_hash_kernel<n><<<grid, 256, 0, st>>>(logits, token_ids, tid2eid,    \
-                                               vocab, w, ids, T, E, topk,     \
-                                               scoring, route_scale);         \
+    route_hash_kernel<n><<<grid, 256, 0, st>>>((float*)logits, token_ids,     \
+                                               tid2eid, vocab, w, ids, T, E,  \
+                                               topk, scoring, route_scale,    \
+                                               ks);                           \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE
