@@ -94,11 +94,6 @@ __device__ __forceinline__ uint32_t f32_order_key(float f) {
 // --------------------------------------------------------------------------
 // wave64 reductions
 // --------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
 
 // Maxima through DPP lane moves instead of LDS shuffles (a top-k makes
 // one such reduction per selected element, so their latency adds up): xor 1
@@ -130,6 +125,29 @@ __device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
       ((uint64_t)dpp_u32<CTRL, ROW_MASK>((uint32_t)(v >> 32), 0u) << 32) |
       dpp_u32<CTRL, ROW_MASK>((uint32_t)v, 0u);
   return w > v ? w : v;
+}
+
+// Sum by the same DPP pattern (a fixed order: quads, half rows, rows, then
+// rows 0+1 and 2+3, then the two halves), broadcast from lane 63.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x140>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x142, 0xA>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x143, 0xC>(__float_as_uint(v), 0u));
+  return __uint_as_float(
+      (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v, 0u));
+  v = max(v, dpp_u32<0x4E>(v, 0u));
+  v = max(v, dpp_u32<0x141>(v, 0u));
+  v = max(v, dpp_u32<0x140>(v, 0u));
+  v = max(v, dpp_u32<0x142, 0xA>(v, 0u));
+  v = max(v, dpp_u32<0x143, 0xC>(v, 0u));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // keys are >= 0 (0 = no candidate)

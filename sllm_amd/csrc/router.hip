@@ -282,7 +282,19 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
   if constexpr (EPL <= 8) {
     sort_desc<EPL>(key);
     for (int kk = 0; kk < topk; ++kk) {
-      const uint64_t best = wave_max_u64(key[0]);
+      // the maximum of the value halves; the full 64-bit keys only decide
+      // between lanes that share it
+      const uint32_t hi = (uint32_t)(key[0] >> 32);
+      const uint32_t mhi = wave_max_u32(hi);
+      const uint64_t bal = __ballot(hi == mhi);
+      uint64_t best;
+      if (__popcll(bal) == 1) {
+        const int owner = (int)__builtin_ctzll(bal);
+        best = ((uint64_t)mhi << 32) |
+               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], owner);
+      } else {
+        best = wave_max_u64(hi == mhi ? key[0] : 0ull);
+      }
       if (lane == kk) mine = best;
       if (lane == (topk_key_id(best) & 63)) {
 #pragma unroll
