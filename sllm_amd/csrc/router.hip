@@ -231,8 +231,10 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
 // --------------------------------------------------------------------------
 // Top-k keys: the order key of the value (f32_order_key) in the high half,
 // ~e in the low half, so that a larger key is a larger value and, among
-// equal values, the lower expert id e; 0 = no candidate.
+// equal values, the lower expert id e; 0 = no candidate. -0 is keyed as +0:
+// the two are equal values (and give equal probabilities), so they tie.
 __device__ __forceinline__ uint64_t topk_key(float v, int e) {
+  v = v == 0.f ? 0.f : v;
   return ((uint64_t)f32_order_key(v) << 32) |
          (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
 }

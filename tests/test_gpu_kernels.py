@@ -364,3 +364,24 @@ def test_pack_weights_layout(L, up):
     want, wants = _np_pack_fp4(f0, f1, s0, s1, up)
     np.testing.assert_array_equal(host(p4, np.uint8, (p4.nbytes,)), want)
     np.testing.assert_array_equal(host(ps, np.uint16, (ps.nbytes // 2,)), wants)
+
+
+@pytest.mark.parametrize("E,k", [(512, 10), (2048, 16), (64, 8)])
+def test_route_heavy_ties(L, E, k):
+    """Logits from a five-value set, signed zeros included: most picks tie
+    with other lanes and within a lane, so the lower-id rule decides
+    everywhere (both the sorted per-lane path, <= 8 keys per lane, and the
+    32-keys-per-lane path). Equal logits give bitwise equal probabilities,
+    so the oracle's order is exact and the ids must match bit for bit."""
+    rng = np.random.default_rng(E + k)
+    T = 40
+    vals = np.array([-2.0, -1.0, -0.0, 0.0, 1.0], np.float32)
+    logits = vals[rng.integers(0, 5, (T, E))]
+    logits[3] = 0.0
+    logits[4] = -0.0
+    w, ids = empty(T * k * 4), empty(T * k * 4)
+    L.check(L.lib().sllm_moe_route_softmax(dev(logits).ptr, w.ptr, ids.ptr, T, E,
+                                           k, np.float32(1e-20), None))
+    wr, ir = qm.moe_route(logits, k)
+    np.testing.assert_array_equal(host(ids, np.int32, (T, k)), ir.astype(np.int32))
+    np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=1e-5, atol=1e-7)

@@ -284,3 +284,20 @@ def test_deepseek_decode(B):
                                 "sigmoid", 2.5, 4, 2)
     rel, mabs, scale = _report(f"deepseek decode B={B}", y, want)
     assert rel < 1e-4
+
+
+@pytest.mark.parametrize("T", [1, 13, 32, 64])
+def test_decode_router_split_logits(T):
+    """Decode-size router GEMM with its K split over workgroups: the
+    partial-logit slices are summed in the routing kernel and stored back
+    (the debug copy reads them). Logits within 8 units of fp32 rounding of
+    the fp64 product, relative to sum |x||w|; routing exact on them."""
+    x, W = qwen_fp8(seed=80 + T, T=T, H=2048, E=64, I=256, Is=256)
+    layer = qwen_layer(W, 6)
+    y, r = layer.forward(x, mode="decode", return_routing=True)
+    want = x.astype(np.float64) @ W.router_w.astype(np.float64).T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(W.router_w.astype(np.float64)).T
+    assert np.all(np.abs(r["logits"] - want) <= 8 * 2.0 ** -24 * mag + 1e-30)
+    _check_routing(r, 64, 6)
+    rel = rel_l2(y, qm.moe_layer_fp8_dequant(x, r["logits"], W, 6))
+    assert rel < 1e-4
