@@ -874,9 +874,18 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF, kc = d.x >> 16;
     const SegDesc& S = seg ? S1 : S0;
-    if (lc < d.w) {  // mode 1 writes K chunk kc's slice (kc = 0 unsplit)
+    if (lc < d.w) {  // K chunk kc's slice (kc = 0 unsplit)
       const float rw = rwl[i][lc];
       if constexpr (MODE == 0) {
+        if (S.ksplit > 1) {  // chunk sums; launch_split_finish applies SwiGLU
+          float* pg = S.pp + kc * S.pstride + (size_t)(d.z + lc) * S.N +
+                      nt * 128 + wave * 16 + lg * 4;
+          *(float4*)pg = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+          *(float4*)(pg + S.ksplit * S.pstride) =
+              make_float4(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
+          acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+          return;
+        }
         float h[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -988,6 +997,78 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
 // idle; the chunk results are summed by the combine.
 constexpr long DEC_TARGET_ITEMS = 512;
 constexpr int DEC_MAX_KSPLIT = 32;
+
+// Gate/up: split only launches with fewer than two items per CU, into
+// chunks of at least four K steps, at most 8 (the finish reads every slice).
+int dec_ksplit_up(long upper_items, int KB) {
+  if (upper_items <= 0 || upper_items >= DEC_TARGET_ITEMS) return 1;
+  long ks = (DEC_TARGET_ITEMS + upper_items - 1) / upper_items;
+  ks = std::min<long>(ks, std::min(KB / 4, 8));
+  return (int)std::max<long>(ks, 1);
+}
+
+// h = silu(g) * u from the K-chunk slices of split mode-0 segments, rows
+// [0, total_rows) of each. A thread takes four columns of one row: all of
+// its 2 ks slice loads are issued together, then added in chunk order.
+constexpr int SF_MAX_KS = 8;
+
+__global__ __launch_bounds__(256) void split_finish_kernel(SegDesc S0,
+                                                           SegDesc S1, int nseg,
+                                                           float limit) {
+  const long n0 = (long)S0.total_rows * S0.N / 4;
+  const long n1 = nseg > 1 ? (long)S1.total_rows * S1.N / 4 : 0;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n0 + n1) return;
+  const bool second = i >= n0;
+  const SegDesc& S = second ? S1 : S0;
+  const long j = (second ? i - n0 : i) * 4;
+  const int ks = S.ksplit;
+  float4 g[SF_MAX_KS], u[SF_MAX_KS];
+#pragma unroll
+  for (int q = 0; q < SF_MAX_KS; ++q) {
+    const int qq = min(q, ks - 1);
+    g[q] = *(const float4*)(S.pp + qq * S.pstride + j);
+    u[q] = *(const float4*)(S.pp + (ks + qq) * S.pstride + j);
+  }
+  float gs[4] = {0.f, 0.f, 0.f, 0.f}, us[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < SF_MAX_KS; ++q) {
+    if (q < ks) {
+      gs[0] += g[q].x; gs[1] += g[q].y; gs[2] += g[q].z; gs[3] += g[q].w;
+      us[0] += u[q].x; us[1] += u[q].y; us[2] += u[q].z; us[3] += u[q].w;
+    }
+  }
+  float h[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float gv = gs[v], uv = us[v];
+    if (limit > 0.f) {
+      uv = fminf(fmaxf(uv, -limit), limit);
+      gv = fminf(gv, limit);
+    }
+    h[v] = silu_f32(gv) * uv;
+  }
+  *(float4*)((float*)S.hq + j) = make_float4(h[0], h[1], h[2], h[3]);
+}
+
+int launch_split_finish(const SegDesc& s0, const SegDesc* s1, float limit,
+                        hipStream_t st) {
+  long n = 0;
+  for (const SegDesc* s : {&s0, s1}) {
+    if (!s) continue;
+    SLLM_REQUIRE(s->pp && s->hq && s->ksplit >= 1 && s->ksplit <= SF_MAX_KS &&
+                     s->N % 4 == 0 && s->total_rows > 0 &&
+                     s->pstride >= (long)s->total_rows * s->N,
+                 "split finish: bad segment (rows=%d N=%d ks=%d)",
+                 s->total_rows, s->N, s->ksplit);
+    n += (long)s->total_rows * s->N / 4;
+  }
+  SLLM_REQUIRE(n < (1L << 31) * 256, "split finish: too large");
+  split_finish_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+      s0, s1 ? *s1 : s0, s1 ? 2 : 1, limit);
+  SLLM_LAUNCHED();
+  return 0;
+}
 
 int dec_ksplit(long upper_items, int KB) {
   if (upper_items <= 0 || KB <= 1) return 1;
@@ -1103,7 +1184,8 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                  "stream decode gemm: gather / row_w_by_idx need sorted_idx");
     SLLM_REQUIRE(s->ksplit <= s->K / 128 && s->ksplit < 32768 &&
                      (s->ksplit == 1 ||
-                      (mode == 1 && s->pstride > 0 && s->pstride % 4 == 0)),
+                      (s->pstride > 0 && s->pstride % 4 == 0 &&
+                       (mode == 1 || (s->pp && !s->row_w)))),
                  "stream decode gemm: bad K split %d (K=%d, mode %d)",
                  s->ksplit, s->K, mode);
   }

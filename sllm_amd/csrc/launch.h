@@ -90,11 +90,14 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   uint8_t* hq;             // mode 0 outputs at permuted row p
   float* hs;
   uint16_t* y;             // mode 1 output at permuted row p
-  // decode mode 1 split-K: each (row tile, column slab) item is cut into
-  // ksplit K chunks (0 / 1: none) whose partial rows land in y slices
-  // pstride elements apart, summed by launch_combine_split
+  // decode split-K: each (row tile, column slab) item is cut into ksplit K
+  // chunks (0 / 1: none) whose results land in slices pstride elements
+  // apart -- mode 1 in y (summed by launch_combine_split), mode 0 in pp
+  // (gate slices, then up slices; launch_split_finish writes h = SwiGLU of
+  // the sums to hq for rows [0, total_rows))
   int ksplit;
   long pstride;
+  float* pp;
 };
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
@@ -108,9 +111,16 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
                       hipStream_t st);
-// K chunks for a decode down launch whose item count is at most
-// upper_items over KB 128-wide K steps.
+// K chunks for a decode launch whose item count is at most upper_items
+// over KB 128-wide K steps: down launches (dec_ksplit) and gate/up launches
+// (dec_ksplit_up, which needs a finish launch and so splits only launches
+// that would leave most CUs idle).
 int dec_ksplit(long upper_items, int KB);
+int dec_ksplit_up(long upper_items, int KB);
+// h = silu(clamp(sum of gate slices)) * clamp(sum of up slices) for the
+// split mode-0 segments (limit > 0: the SwiGLU clamp of the DeepSeek path).
+int launch_split_finish(const SegDesc& s0, const SegDesc* s1, float limit,
+                        hipStream_t st);
 long packed_bytes(int fp4, int up, int E, int N, int K);
 long packed_scale_bytes(int up, int E, int N, int K);
 

@@ -29,11 +29,11 @@ struct Plan {
   bool decode;
   int N;          // T * topk
   int bm, max_tiles;
-  // decode: K chunks of the streamed down launches (routed / shared) and
-  // partial-logit slices of the router GEMM
-  int ks_dn, ks_dn_sh, ks_r;
+  // decode: K chunks of the streamed gate/up and down launches (routed /
+  // shared) and partial-logit slices of the router GEMM
+  int ks_up, ks_up_sh, ks_dn, ks_dn_sh, ks_r;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
-  size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh;
+  size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
   size_t total;
 };
 
@@ -55,16 +55,18 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
                       bool has_shared, bool need_logits, bool force_gemv,
                       bool separate_shared = false) {
   Plan p{};
-  p.ks_dn = p.ks_dn_sh = 1;
+  p.ks_up = p.ks_up_sh = p.ks_dn = p.ks_dn_sh = 1;
   p.ks_r = p.decode && need_logits ? router_ksplit(T, H) : 1;
   p.decode = force_gemv || pick_decode(mode, T);
   p.N = T * topk;
   if (p.decode) {
     p.bm = DECODE_BM;  // 16-row tiles: a touched expert's rows, mostly one tile
-    p.max_tiles = (p.N + DECODE_BM - 1) / DECODE_BM + (E < p.N ? E : p.N);
+    // tiles = sum over touched experts of ceil(n_e / bm)
+    //       <= touched + floor((N - 1) / bm) <= ceil(N / bm) + min(E, N) - 1
+    p.max_tiles = (p.N + DECODE_BM - 1) / DECODE_BM + (E < p.N ? E : p.N) - 1;
   } else {
     p.bm = PREFILL_BM;
-    p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N);
+    p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N) - 1;
   }
   size_t c = 0;
   p.logits = need_logits ? take(c, (size_t)p.ks_r * T * E * 4) : 0;
@@ -83,9 +85,15 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
       const long rt = p.max_tiles;
       const long sh_rt = has_shared ? (T + DECODE_BM - 1) / DECODE_BM : 0;
       if (separate_shared) {
+        p.ks_up = dec_ksplit_up(rt * (I / 128), H / 128);
         p.ks_dn = dec_ksplit(rt * (H / 256), I / 128);
-        if (has_shared) p.ks_dn_sh = dec_ksplit(sh_rt * (H / 256), Is / 128);
+        if (has_shared) {
+          p.ks_up_sh = dec_ksplit_up(sh_rt * (Is / 128), H / 128);
+          p.ks_dn_sh = dec_ksplit(sh_rt * (H / 256), Is / 128);
+        }
       } else {
+        p.ks_up = p.ks_up_sh =
+            dec_ksplit_up(rt * (I / 128) + sh_rt * (Is / 128), H / 128);
         p.ks_dn = p.ks_dn_sh =
             dec_ksplit(rt * (H / 256) + sh_rt * (H / 256),
                        (has_shared ? std::min(I, Is) : I) / 128);
@@ -95,6 +103,9 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.hq_sh = has_shared ? take(c, (size_t)T * Is * 4) : 0;   // h_sh fp32
     p.y = take(c, (size_t)p.ks_dn * p.N * H * 4);             // y fp32 slices
     p.y_sh = has_shared ? take(c, (size_t)p.ks_dn_sh * T * H * 4) : 0;
+    p.gu = p.ks_up > 1 ? take(c, (size_t)2 * p.ks_up * p.N * I * 4) : 0;
+    p.gu_sh = has_shared && p.ks_up_sh > 1
+                  ? take(c, (size_t)2 * p.ks_up_sh * T * Is * 4) : 0;
   } else {
     p.xq = take(c, (size_t)T * H);
     p.sx = take(c, (size_t)T * (H / 128) * 4);
@@ -277,14 +288,21 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
       r1.tile_info = tiles; r1.num_tiles = ntiles;
       r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
-      r1.N = I; r1.K = H; r1.hq = (uint8_t*)h;
+      r1.N = I; r1.K = H; r1.hq = (uint8_t*)h; r1.total_rows = p.N;
+      r1.ksplit = p.ks_up; r1.pp = (float*)(ws + p.gu);
+      r1.pstride = (long)p.N * I;
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
       s1.wp = (const uint8_t*)a->sgu_packed; s1.s0 = a->sg_s; s1.s1 = a->su_s;
       s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
+      s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
+      s1.pstride = (long)T * Is;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k, 0.f,
-                              (long)p.max_tiles * (I / 128) + sh_rt * (Is / 128),
-                              st));
+                              (long)p.max_tiles * (I / 128) * p.ks_up +
+                                  sh_rt * (Is / 128) * p.ks_up_sh,
+                              st) ||
+                (p.ks_up > 1 &&
+                 launch_split_finish(r1, sh ? &s1 : nullptr, 0.f, st)));
       SegDesc r2{}, s2{};
       r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
       r2.tile_info = tiles; r2.num_tiles = ntiles;
@@ -484,7 +502,9 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
     r1.tile_info = tiles; r1.num_tiles = ntiles;
     r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
-    r1.N = I; r1.K = H; r1.hq = (uint8_t*)h;
+    r1.N = I; r1.K = H; r1.hq = (uint8_t*)h; r1.total_rows = p.N;
+    r1.ksplit = p.ks_up; r1.pp = (float*)(ws + p.gu);
+    r1.pstride = (long)p.N * I;
     SegDesc r2{};
     r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
     r2.tile_info = tiles; r2.num_tiles = ntiles;
@@ -493,7 +513,8 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_stream_dec(2, 0, r1, nullptr, k, L,
-                            (long)p.max_tiles * (I / 128), st));
+                            (long)p.max_tiles * (I / 128) * p.ks_up, st) ||
+              (p.ks_up > 1 && launch_split_finish(r1, nullptr, L, st)));
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
           launch_stream_dec(2, 1, r2, nullptr, k, 0.f,
                             (long)p.max_tiles * (H / 256) * p.ks_dn, st));
@@ -502,13 +523,17 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
       s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
       s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
+      s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
+      s1.pstride = (long)T * Is;
       SegDesc s2{};
       s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
       s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
       s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
       s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
-            launch_stream_dec(1, 0, s1, nullptr, k, L, sh_rt * (Is / 128), st));
+            launch_stream_dec(1, 0, s1, nullptr, k, L,
+                              sh_rt * (Is / 128) * p.ks_up_sh, st) ||
+                (p.ks_up_sh > 1 && launch_split_finish(s1, nullptr, L, st)));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
             launch_stream_dec(1, 1, s2, nullptr, k, 0.f,
                               sh_rt * (H / 256) * p.ks_dn_sh, st));
