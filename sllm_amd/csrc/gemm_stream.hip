@@ -137,9 +137,17 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 // Streaming (nontemporal) 16-byte load: expert weights are read once per
 // layer and should not evict the gathered activation rows from L2.
+// WNT = false: an ordinary load, for launches whose experts span several
+// row tiles, so that the tiles of one expert (streamed at the same time on
+// one XCD) share the weights through L2.
+template <bool WNT>
 __device__ __forceinline__ uint4 ld_stream(const void* p) {
-  const v4u t = __builtin_nontemporal_load((const v4u*)p);
-  return make_uint4(t.x, t.y, t.z, t.w);
+  if constexpr (WNT) {
+    const v4u t = __builtin_nontemporal_load((const v4u*)p);
+    return make_uint4(t.x, t.y, t.z, t.w);
+  } else {
+    return *(const uint4*)p;
+  }
 }
 
 template <int MODE>
@@ -212,7 +220,7 @@ __device__ __forceinline__ void st_sched_pattern() {
 // block tid % 4), one 4-byte load, a wave touching 16 rows -- which the
 // first step of the next body stores to LDS. Otherwise (PERSTEP) each step
 // loads its own scale, four lanes per row.
-template <int BF, int MODE, bool PERSTEP>
+template <int BF, int MODE, bool PERSTEP, bool WNT>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, int pow2) {
   constexpr int YS = 264;  // bf16 row stride of the down-projection staging
@@ -361,7 +369,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     if constexpr (BF == SF_FP4) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint4 v = ld_stream(base + s * 1024);
+        const uint4 v = ld_stream<WNT>(base + s * 1024);
         b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
       b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
@@ -369,8 +377,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     } else {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint4 lo4 = ld_stream(base + (2 * s) * 1024);
-        const uint4 hi4 = ld_stream(base + (2 * s + 1) * 1024);
+        const uint4 lo4 = ld_stream<WNT>(base + (2 * s) * 1024);
+        const uint4 hi4 = ld_stream<WNT>(base + (2 * s + 1) * 1024);
         b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
@@ -702,7 +710,7 @@ __device__ __forceinline__ float e8m0_f32(uint32_t b) {
                                   : __uint_as_float(b << 23));
 }
 
-template <int BF, int MODE>
+template <int BF, int MODE, bool WNT>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit) {
   __shared__ int4 desc[ST_MAX_ITEMS];
@@ -839,7 +847,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     if constexpr (BF == SF_FP4) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint4 v = ld_stream(base + s * 1024);
+        const uint4 v = ld_stream<WNT>(base + s * 1024);
         b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
       b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
@@ -847,8 +855,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     } else {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint4 lo4 = ld_stream(base + (2 * s) * 1024);
-        const uint4 hi4 = ld_stream(base + (2 * s + 1) * 1024);
+        const uint4 lo4 = ld_stream<WNT>(base + (2 * s) * 1024);
+        const uint4 hi4 = ld_stream<WNT>(base + (2 * s + 1) * 1024);
         b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
                        (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
       }
@@ -1105,12 +1113,21 @@ static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
   const long grid = 8 * nx;
   SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
   SegDesc dummy = s0;
-  if (perstep)
-    moe_stream_kernel<BF, MODE, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-        s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
+  const SegDesc& b = s1 ? *s1 : dummy;
+  const int ns = s1 ? 2 : 1;
+  const bool nt = !s0.wreuse;
+  if (perstep && nt)
+    moe_stream_kernel<BF, MODE, true, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, b, ns, topk, limit, pow2);
+  else if (perstep)
+    moe_stream_kernel<BF, MODE, true, false><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, b, ns, topk, limit, pow2);
+  else if (nt)
+    moe_stream_kernel<BF, MODE, false, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, b, ns, topk, limit, pow2);
   else
-    moe_stream_kernel<BF, MODE, false><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-        s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, pow2);
+    moe_stream_kernel<BF, MODE, false, false><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+        s0, b, ns, topk, limit, pow2);
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1157,7 +1174,7 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   const long grid = 8 * nx;
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   SegDesc dummy = s0;
-  moe_stream_dec_kernel<BF, MODE><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+  moe_stream_dec_kernel<BF, MODE, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
       s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit);
   SLLM_LAUNCHED();
   return 0;

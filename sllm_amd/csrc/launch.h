@@ -98,6 +98,11 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   int ksplit;
   long pstride;
   float* pp;
+  // prefill: 1 when the launch's experts average more rows than one row
+  // tile, so that the weights are loaded through L2 (shared by an expert's
+  // tiles) rather than streamed past it; the first segment decides for the
+  // launch. Decode launches always stream.
+  int wreuse;
 };
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,

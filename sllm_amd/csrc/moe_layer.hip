@@ -37,6 +37,16 @@ struct Plan {
   size_t total;
 };
 
+// Prefill: weights go through L2 (rather than streamed past it) when a
+// launch's experts average more than one row tile: an expert's tiles are
+// consecutive items, run at the same time on one XCD and share them
+// (C4: 5.52 -> 5.33 ms). Decode launches always stream: there the tiles of
+// an expert fall on different XCDs and ordinary loads only cost L2 space
+// (a one-expert MLP at B=32: 150 -> 165 us).
+static int weights_reused(long rows, long experts, int bm) {
+  return rows > (long)bm * experts ? 1 : 0;
+}
+
 static size_t take(size_t& cur, size_t bytes) {
   size_t at = cur;
   cur += align_up(bytes ? bytes : 1, 256);
@@ -371,6 +381,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
                    "sllm_moe_qwen_forward: packed weights incomplete");
       const long sh_rt = sh ? (T + 127) / 128 : 0;
       SegDesc r1{}, s1{};
+      r1.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
       r1.tile_info = tiles; r1.num_tiles = ntiles;
       r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
@@ -382,6 +393,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             launch_stream(0, 0, r1, sh ? &s1 : nullptr, k, 0.f, 0, up1, st));
       SegDesc r2{}, s2{};
+      r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
       r2.tile_info = tiles; r2.num_tiles = ntiles;
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
@@ -592,6 +604,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
                    "sllm_moe_ds_forward: packed weights incomplete");
       const long sh_rt = (T + 127) / 128;
       SegDesc r1{};
+      r1.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
       r1.tile_info = tiles; r1.num_tiles = ntiles;
       r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
@@ -601,6 +614,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
             launch_stream(2, 0, r1, nullptr, k, L, 1,
                           (long)p.max_tiles * (I / 128), st));
       SegDesc r2{};
+      r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
       r2.tile_info = tiles; r2.num_tiles = ntiles;
       r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
@@ -610,6 +624,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
                           (long)p.max_tiles * (H / 256), st));
       if (sh) {
         SegDesc s1{};
+        s1.wreuse = weights_reused(T, 1, PREFILL_BM);
         s1.a = xq; s1.sa = sx; s1.total_rows = T;
         s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
         s1.N = Is; s1.K = H; s1.hq = hq_sh; s1.hs = hs_sh;
@@ -617,6 +632,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
               launch_stream(1, 0, s1, nullptr, k, L, 1, sh_rt * (Is / 128),
                             st));
         SegDesc s2{};
+        s2.wreuse = weights_reused(T, 1, PREFILL_BM);
         s2.a = hq_sh; s2.sa = hs_sh; s2.total_rows = T;
         s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
         s2.N = H; s2.K = Is; s2.y = y_sh;
