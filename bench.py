@@ -17,7 +17,11 @@ a 512 MiB fill between calls), and the CPU baseline (the numpy restatement of
 the quantized layer on this host).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-Prints ONE JSON line.
+Prints ONE JSON line. Other legs, each printing its own line instead:
+--config c4 / c5 (the DeepSeek MXFP4 and skewed-routing prefill configs),
+--device-decode (the decode drop-ins: the MoE hook with host arrays and a
+dense SwiGLU MLP), --loader (FP8 checkpoint to device), --copy-calib MIB
+(the byte-counter calibration copy).
 """
 
 from __future__ import annotations
