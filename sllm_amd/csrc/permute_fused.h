@@ -7,17 +7,31 @@
 
 namespace sllm {
 
+// Inclusive scan of one int per lane through DPP moves: shifts by 1, 2, 4
+// and 8 within each 16-lane row (lanes shifted in from outside the row read
+// 0), then row 0's and row 2's last lanes carried into rows 1 and 3, then
+// lane 31 into rows 2 and 3.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_shifted(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, true);
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += dpp_shifted<0x111>(x);  // row_shr:1
+  x += dpp_shifted<0x112>(x);  // row_shr:2
+  x += dpp_shifted<0x114>(x);  // row_shr:4
+  x += dpp_shifted<0x118>(x);  // row_shr:8
+  x += dpp_shifted<0x142, 0xA>(x);  // row_bcast:15
+  x += dpp_shifted<0x143, 0xC>(x);  // row_bcast:31
+  return x;
+}
+
 // Block-wide exclusive scan of one value per thread (1024 threads, 16
-// waves): a shuffle scan inside each wave, the 16 wave totals through LDS,
+// waves): a DPP scan inside each wave, the 16 wave totals through LDS,
 // two barriers in all. sh needs 16 ints.
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;  // inclusive scan within the wave
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const int x = wave_incl_scan(v);
   if (lane == 63) sh[wave] = x;
   __syncthreads();
   int base = 0, tot = 0;
@@ -113,6 +127,7 @@ __device__ __forceinline__ void permute_fused_body(
     const bool valid = raw >= 0 && raw < E;
     const int e = valid ? raw : 0;
     uint64_t peers = __ballot(valid);
+    if (peers == 0) continue;  // an empty group (uniform across the wave)
     for (int b = 0; b < nbits; ++b) {
       const int bit = (e >> b) & 1;
       const uint64_t m = __ballot(bit);
