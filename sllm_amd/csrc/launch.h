@@ -6,13 +6,16 @@ namespace sllm {
 
 // ks > 1 (T <= 64 only; router_ksplit): the router GEMM writes ks partial
 // logit slices T * E floats apart, and the routing launches given the same
-// ks add them in order (storing the sum into slice 0).
+// ks add them in order (storing the sum into slice 0). Split, the small
+// router's shared-expert gate is left as ks partial logits at gate_out + T
+// (T floats apart); a softmax routing launch given that buffer as gate
+// adds them in order and writes the sigmoid to gate[0, T).
 int router_ksplit(int T, int H);
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
                        int T, int E, int H, hipStream_t st, int ks = 1);
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st,
-                         int ks = 1);
+                         int ks = 1, float* gate = nullptr);
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).
@@ -25,7 +28,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int E, int topk, float eps, int bm,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
-                               int max_tiles, hipStream_t st, int ks = 1);
+                               int max_tiles, hipStream_t st, int ks = 1,
+                               float* gate = nullptr);
 int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,

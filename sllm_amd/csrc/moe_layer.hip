@@ -58,16 +58,22 @@ static bool pick_decode(int mode, int T) {
          (mode == SLLM_MOE_MODE_AUTO && T <= DECODE_MAX_T);
 }
 
-// separate_shared: the shared expert's streamed projections are launches
-// of their own (DeepSeek: other weight format) rather than a second segment
-// of the routed ones.
+// deepseek: the DeepSeek layer, whose shared expert's streamed projections
+// are launches of their own (other weight format) rather than a second
+// segment of the routed ones, and which routes every batch with the
+// multi-workgroup kernels.
 static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
                       bool has_shared, bool need_logits, bool force_gemv,
-                      bool separate_shared = false) {
+                      bool deepseek = false) {
   Plan p{};
   p.ks_up = p.ks_up_sh = p.ks_dn = p.ks_dn_sh = 1;
-  p.ks_r = p.decode && need_logits ? router_ksplit(T, H) : 1;
   p.decode = force_gemv || pick_decode(mode, T);
+  // The Qwen layer routes decode batches that fit one workgroup in one
+  // fused launch (route_permute_small_fits), which would read every logit
+  // slice through one CU: its router stays unsplit there.
+  const bool fused_route =
+      !deepseek && p.decode && route_permute_small_fits(T, E, topk);
+  p.ks_r = p.decode && need_logits && !fused_route ? router_ksplit(T, H) : 1;
   p.N = T * topk;
   if (p.decode) {
     p.bm = DECODE_BM;  // 16-row tiles: a touched expert's rows, mostly one tile
@@ -89,12 +95,13 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.tiles = take(c, (size_t)p.max_tiles * 16);
   p.ntiles = take(c, 4);
   p.pscr = take(c, permute_scratch_bytes(p.N, E));
-  p.gate = take(c, (size_t)T * 4);
+  // shared-expert gate, then (split router) its ks_r partial slices
+  p.gate = take(c, (size_t)(p.ks_r > 1 ? 1 + p.ks_r : 1) * T * 4);
   if (p.decode) {
     if (!force_gemv) {  // the streamed kernels (the GEMV path does not split)
       const long rt = p.max_tiles;
       const long sh_rt = has_shared ? (T + DECODE_BM - 1) / DECODE_BM : 0;
-      if (separate_shared) {
+      if (deepseek) {
         p.ks_up = dec_ksplit_up(rt * (I / 128), H / 128);
         p.ks_dn = dec_ksplit(rt * (H / 256), I / 128);
         if (has_shared) {
@@ -256,7 +263,10 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
                                    H, sh ? (const uint16_t*)a->sgl : nullptr,
                                    sh ? gate : nullptr, st, p.ks_r));
     gate_done = sh;
-  } else {
+  }
+  // split router: the routing launch finishes the gate from its partials
+  float* gate_fin = small_router && sh && p.ks_r > 1 ? gate : nullptr;
+  if (!small_router) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
           a->logits_given ? 0
                           : launch_router_gemm((const uint16_t*)a->x,
@@ -267,11 +277,13 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
-                                     ntiles, p.max_tiles, st, p.ks_r));
+                                     ntiles, p.max_tiles, st, p.ks_r,
+                                     gate_fin));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-          launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r));
+          launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
+                               gate_fin));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st));

@@ -162,10 +162,13 @@ constexpr int RG_SMALL_T = 64;
 // Decode-size router GEMM: workgroup (x, q) computes experts [16 x, +16)
 // over K chunk q of gridDim.y (32-wide K slices split evenly), all NTI
 // 16-token tiles, and writes its partial logits to slice q (q T E floats
-// in); the routing kernels add the slices in order. With gate_out, one
-// extra workgroup (x = E / 16, q = 0, whole K) computes the shared-expert
-// gate sigmoid(x . sgl) of every token (its 16 weight rows all read sgl;
-// column 0 is kept).
+// in); the routing kernels add the slices in order. With gate_out, an
+// extra column of workgroups (x = E / 16) computes the shared-expert gate
+// logit x . sgl of every token over the same K chunks (its 16 weight rows
+// all read sgl; column 0 is kept): unsplit it writes sigmoid(logit) to
+// gate_out[t], split it writes chunk q's partial to gate_out[T + q T + t]
+// and the routing kernel adds the partials in order and applies the
+// sigmoid (route_gate_finish).
 template <int NTI>
 __global__ __launch_bounds__(512) void router_gemm_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
@@ -176,8 +179,7 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
   const int lr = lane & 15, lg = lane >> 4;
   const int e0 = blockIdx.x * 16;
   const bool gate_tile = e0 >= E;
-  if (gate_tile && blockIdx.y > 0) return;  // the gate takes the whole K
-  const int nsl = H / 32, ks = gate_tile ? 1 : gridDim.y, q = blockIdx.y;
+  const int nsl = H / 32, ks = gridDim.y, q = blockIdx.y;
   const int s0 = q * nsl / ks, s1 = (q + 1) * nsl / ks;
   const uint16_t* brow = (gate_tile ? sgl : w + (size_t)min(e0 + lr, E - 1) * H) + lg * 8;
   const uint16_t* arow[NTI];
@@ -220,7 +222,10 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
 #pragma unroll
     for (int wv = 0; wv < 8; ++wv) s += part[wv][r][c];
     if (gate_tile) {
-      if (c == 0) gate_out[r] = sigmoid_f32(s);
+      if (c == 0) {
+        if (ks == 1) gate_out[r] = sigmoid_f32(s);
+        else gate_out[T + q * T + r] = s;
+      }
     } else if (e0 + c < E) {
       out[(size_t)r * E + e0 + c] = s;
     }
@@ -321,18 +326,45 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
   return mine;
 }
 
-// Logit e of a row held as ks K-chunk slices kstride floats apart (the
-// split decode router GEMM), added in slice order. With several slices the
-// owning wave (store) writes the sum back into slice 0, which then holds
-// the logits the routing used (the debug copy reads slice 0).
-__device__ __forceinline__ float logit_sum(float* row, int e, int ks,
-                                           long kstride, bool store = true) {
-  float v = row[e];
-  if (ks > 1) {
-    for (int q = 1; q < ks; ++q) v += row[q * kstride + e];
-    if (store) row[e] = v;
+// The calling wave's logits of one row (lane holds experts lane + 64 i;
+// fill past E) when the row is held as ks K-chunk slices kstride floats
+// apart (the split decode router GEMM): slices are added in order, the
+// loads of G slices in flight together. With several slices
+// the owning wave (store) writes the sums back into slice 0, which then
+// holds the logits the routing used (the debug copy reads slice 0).
+// G: slices whose loads are in flight together (registers: G * EPL).
+template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
+__device__ __forceinline__ void logit_sums(float* row, int ks, long kstride,
+                                           int E, bool store, float fill,
+                                           float (&v)[EPL]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : fill;
   }
-  return v;
+  if (ks <= 1) return;
+  for (int q0 = 1; q0 < ks; q0 += G) {
+    float t[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const int e = lane + 64 * i;
+        t[g][i] = q0 + g < ks && e < E ? row[(q0 + g) * kstride + e] : 0.f;
+      }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) v[i] += t[g][i];
+  }
+  if (store) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) row[e] = v[i];
+    }
+  }
 }
 
 // One token's softmax top-k on the calling wave: row = the token's E logits;
@@ -341,19 +373,16 @@ __device__ __forceinline__ float logit_sum(float* row, int e, int ks,
 // probability is exp(l - max) / sum recomputed from its key, and the
 // weights are those probabilities over their sum in pick order plus eps
 // (ref/qwen4_exp.py:118-140).
-template <int EPL>
+template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
 __device__ __forceinline__ void route_softmax_token(
     float* row, int ks, long kstride, int E, int topk, float eps,
     float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
   const int lane = threadIdx.x & 63;
   float v[EPL];
+  logit_sums<EPL, G>(row, ks, kstride, E, true, -INFINITY, v);
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + 64 * i;
-    v[i] = e < E ? logit_sum(row, e, ks, kstride) : -INFINITY;
-    m = fmaxf(m, v[i]);
-  }
+  for (int i = 0; i < EPL; ++i) m = fmaxf(m, v[i]);
   m = wave_max(m);
   float s = 0.f;
   uint64_t key[EPL];
@@ -377,15 +406,25 @@ __device__ __forceinline__ void route_softmax_token(
   }
 }
 
+// Token t's shared-expert gate from the split router GEMM's ks partial
+// logits (gate[T + q T + t]): added in chunk order, sigmoid into gate[t].
+__device__ __forceinline__ void route_gate_finish(float* gate, int T, int t,
+                                                  int ks) {
+  float g = gate[T + t];
+  for (int q = 1; q < ks; ++q) g += gate[T + q * T + t];
+  gate[t] = sigmoid_f32(g);
+}
+
 template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
     float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
-    int E, int topk, float eps, int ks) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    int E, int topk, float eps, int ks, float* __restrict__ gate) {
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
   route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
                            w_out + (size_t)t * topk, id_out + (size_t)t * topk,
                            nullptr);
+  if (gate && (threadIdx.x & 63) == 0) route_gate_finish(gate, T, t, ks);
 }
 
 // Decode (T * topk <= PERM_FUSED_MAX_N, E <= PERM_FUSED_MAX_E): softmax
@@ -397,15 +436,19 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
     int E, int topk, float eps, int nbits, int bm, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted_idx,
     int* __restrict__ inv_pos, int* __restrict__ tile_info,
-    int* __restrict__ num_tiles, int max_tiles, int ks) {
+    int* __restrict__ num_tiles, int max_tiles, int ks,
+    float* __restrict__ gate) {
   __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
   __shared__ int sh[1024];
   __shared__ int ids_lds[PERM_FUSED_MAX_N];
   const int wave = threadIdx.x >> 6;
-  for (int t = wave; t < T; t += PERM_FUSED_WAVES)
-    route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk,
-                             eps, w_out + (size_t)t * topk,
-                             id_out + (size_t)t * topk, ids_lds + t * topk);
+  for (int t = wave; t < T; t += PERM_FUSED_WAVES) {
+    // fewer slice loads in flight: 16 waves share the register file
+    route_softmax_token<EPL, (EPL >= 32 ? 1 : (32 / EPL < 8 ? 32 / EPL : 8))>(
+        logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
+        w_out + (size_t)t * topk, id_out + (size_t)t * topk, ids_lds + t * topk);
+    if (gate && (threadIdx.x & 63) == 0) route_gate_finish(gate, T, t, ks);
+  }
   __syncthreads();
   permute_fused_body(ids_lds, T * topk, E, nbits, bm, counts, offsets,
                      sorted_idx, inv_pos, tile_info, num_tiles, max_tiles,
@@ -427,13 +470,15 @@ __device__ __forceinline__ void gate_scores_row(float* row, int ks,
                                                 int E, int scoring,
                                                 float (&sc)[EPL]) {
   const int lane = threadIdx.x & 63;
+  float lv[EPL];
+  logit_sums<EPL>(row, ks, kstride, E, store, 0.f, lv);
   if (scoring == SCORE_SOFTMAX) {
     double m = -INFINITY;
     double xv[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       int e = lane + 64 * i;
-      xv[i] = e < E ? (double)logit_sum(row, e, ks, kstride, store) : -INFINITY;
+      xv[i] = e < E ? (double)lv[i] : -INFINITY;
       m = xv[i] > m ? xv[i] : m;
     }
 #pragma unroll
@@ -455,7 +500,7 @@ __device__ __forceinline__ void gate_scores_row(float* row, int ks,
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       int e = lane + 64 * i;
-      double xv = e < E ? (double)logit_sum(row, e, ks, kstride, store) : 0.0;
+      double xv = e < E ? (double)lv[i] : 0.0;
       if (scoring == SCORE_SIGMOID) {
         sc[i] = (float)(1.0 / (1.0 + exp(-xv)));
       } else {
@@ -475,7 +520,7 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
   __shared__ float scl[4][EPL * 64];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int t_raw = blockIdx.x * 4 + wv;
+  const int t_raw = blockIdx.x * (blockDim.x >> 6) + wv;
   const bool active = t_raw < T;
   const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
   float sc[EPL];
@@ -558,7 +603,7 @@ __global__ __launch_bounds__(256) void route_hash_kernel(
   __shared__ float sb[4][EPL * 64];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int t_raw = blockIdx.x * 4 + wv;
+  const int t_raw = blockIdx.x * (blockDim.x >> 6) + wv;
   const bool active = t_raw < T;
   const int t = active ? t_raw : T - 1;
   float sc[EPL];
@@ -590,6 +635,11 @@ static int epl_for(int E) {
   while (epl * 64 < E) epl *= 2;
   return epl;
 }
+
+// Tokens (waves) per workgroup of the multi-workgroup routing kernels: 4,
+// or 1 over split logits, whose ks slices per row are then read through T
+// CUs rather than T / 4 (the reads are bound by per-CU bandwidth).
+static int route_tokens_per_block(int ks) { return ks > 1 ? 1 : 4; }
 
 int router_ksplit(int T, int H) {
   if (T > RG_SMALL_T) return 1;
@@ -652,8 +702,10 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int E, int topk, float eps, int bm,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
-                               int max_tiles, hipStream_t st, int ks) {
-  SLLM_REQUIRE(ks >= 1, "route_permute_small: bad logit slices %d", ks);
+                               int max_tiles, hipStream_t st, int ks,
+                               float* gate) {
+  SLLM_REQUIRE(ks >= 1 && (!gate || ks > 1),
+               "route_permute_small: bad logit slices %d", ks);
   SLLM_REQUIRE(logits && w && ids && route_permute_small_fits(T, E, topk) &&
                    topk > 0 && topk <= E && topk <= 64 && T > 0,
                "route_permute_small: bad sizes (T=%d E=%d k=%d)", T, E, topk);
@@ -664,7 +716,7 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
   case n:                                                                     \
     route_permute_small_kernel<n><<<1, 1024, 0, st>>>(                        \
         (float*)logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,  \
-        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks);            \
+        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks, gate);      \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16)
 #undef CASE
@@ -676,18 +728,21 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
 }
 
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
-                         int E, int topk, float eps, hipStream_t st, int ks) {
-  SLLM_REQUIRE(logits && w && ids && ks >= 1, "route_softmax: null pointer");
+                         int E, int topk, float eps, hipStream_t st, int ks,
+                         float* gate) {
+  SLLM_REQUIRE(logits && w && ids && ks >= 1 && (!gate || ks > 1),
+               "route_softmax: null pointer or bad logit slices");
   SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
                    topk <= 64,
                "route_softmax: need 0<topk<=E<=2048, topk<=64 (E=%d k=%d)",
                E, topk);
-  dim3 grid(ceil_div(T, 4));
+  const int tpb = route_tokens_per_block(ks);
+  dim3 grid(ceil_div(T, tpb));
   switch (epl_for(E)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
-    route_softmax_kernel<n><<<grid, 256, 0, st>>>((float*)logits, w, ids, T,  \
-                                                  E, topk, eps, ks);          \
+    route_softmax_kernel<n><<<grid, 64 * tpb, 0, st>>>(                       \
+        (float*)logits, w, ids, T, E, topk, eps, ks, gate);                   \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE
@@ -713,11 +768,12 @@ int launch_route_grouped(const float* logits, const float* bias, float* w,
                  "route_grouped: bad group config (E=%d G=%d kg=%d k=%d)", E,
                  n_group, topk_group, topk);
   }
-  dim3 grid(ceil_div(T, 4));
+  const int tpb = route_tokens_per_block(ks);
+  dim3 grid(ceil_div(T, tpb));
   switch (epl_for(E)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
-    route_grouped_kernel<n><<<grid, 256, 0, st>>>(                            \
+    route_grouped_kernel<n><<<grid, 64 * tpb, 0, st>>>(                       \
         (float*)logits, bias, w, ids, T, E, topk, n_group, topk_group,        \
         scoring, route_scale, ks);                                            \
     break;
@@ -738,11 +794,12 @@ int launch_route_hash(const float* logits, const int* token_ids,
                    topk <= E && vocab > 0 && scoring >= 0 && scoring <= 2,
                "route_hash: bad sizes (T=%d E=%d k=%d vocab=%d scoring=%d)",
                T, E, topk, vocab, scoring);
-  const int grid = ceil_div(T, 4);
+  const int tpb = route_tokens_per_block(ks);
+  const int grid = ceil_div(T, tpb);
   switch (epl_for(E)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
-    route_hash_kernel<n><<<grid, 256, 0, st>>>((float*)logits, token_ids,     \
+    route_hash_kernel<n><<<grid, 64 * tpb, 0, st>>>((float*)logits, token_ids, \
                                                tid2eid, vocab, w, ids, T, E,  \
                                                topk, scoring, route_scale,    \
                                                ks);                           \

@@ -89,3 +89,25 @@ def test_host_bf16_rounding_matches_python():
     got = np.empty(x.size, np.uint16)
     _lib.check(_lib.lib().sllm_host_f32_to_bf16(got.ctypes.data, x.ctypes.data, x.size))
     np.testing.assert_array_equal(got, to_bf16(x))
+
+
+def test_decode_workspace_holds_split_router_slices():
+    """Host plan, no GPU: a decode call that computes its own logits splits
+    the router GEMM's K over 8 workgroups (H = 2048) when its batch is routed
+    by the multi-workgroup kernels (17 <= T <= 64 here), so its workspace
+    holds 8 partial-logit slices of T * E floats and 8 partial gate slices
+    of T floats beyond a call given the logits. Batches routed in one fused
+    workgroup (T <= 16) and prefill keep one slice."""
+    from sllm_amd.moe import qwen_workspace_bytes as wsb
+
+    def up256(n):
+        return -(-n // 256) * 256
+    H, E, I, Is, k = 2048, 512, 512, 512, 10
+    for T, mode, split in ((1, "decode", False), (16, "decode", False),
+                           (17, "decode", True), (32, "decode", True),
+                           (64, "decode", True), (128, "prefill", False)):
+        own = wsb(T, H, E, I, Is, k, mode)
+        given = wsb(T, H, E, I, Is, k, mode, logits_given=True)
+        want = (up256(8 * T * E * 4) + up256(9 * T * 4) - up256(T * 4)
+                if split else up256(T * E * 4))
+        assert own - given == want, T
