@@ -92,7 +92,9 @@ __global__ __launch_bounds__(64 * CF_WAVES) void combine_f32_kernel(
   __shared__ int pos[64];
   __shared__ float4 part[CF_WAVES][64];
   const int t = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (threadIdx.x < topk) pos[threadIdx.x] = inv_pos[(size_t)t * topk + threadIdx.x];
+  if (threadIdx.x < topk)  // null inv_pos: the identity permutation
+    pos[threadIdx.x] = inv_pos ? inv_pos[(size_t)t * topk + threadIdx.x]
+                               : t * topk + threadIdx.x;
   __syncthreads();
   const int c = min(blockIdx.x * CF_COLS + lane * 4, H - 4);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -159,7 +161,7 @@ int launch_combine_split(const float* y, const int* inv_pos, int topk,
                          const float* y_shared, int T, int H, int out_f32,
                          void* out, int ks, long kstride, int ks_sh,
                          long kstride_sh, hipStream_t st) {
-  SLLM_REQUIRE(y && inv_pos && out, "combine: null pointer");
+  SLLM_REQUIRE(y && out, "combine: null pointer");
   SLLM_REQUIRE(T > 0 && T < 65536 && H % 4 == 0 && H >= 4 && topk > 0 &&
                    topk <= 64 &&
                    ks >= 1 && ks_sh >= 1 && kstride % 4 == 0 &&

@@ -654,7 +654,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
 // ---------------------------------------------------------------------------
 // Same items, packed weights, persistent XCD-aware dealing and prefetch
 // pipeline as moe_stream_kernel, for the decode regime (a handful of rows
-// per expert): 16-row tiles, activations kept unquantized. Each lane's
+// per expert): 16- or 32-row tiles, activations kept unquantized. Each lane's
 // weight bytes (32 consecutive K of its row) are converted to bf16 in
 // registers -- exact for e4m3 and for e2m1 times its e8m0 scale -- and fed to
 // four v_mfma_f32_16x16x32_bf16 per subtile and K step, slice m taking K
@@ -662,7 +662,6 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
 // the fp32 h of the down projection is split into bf16 hi + lo halves (two
 // MFMAs), which keeps ~16 mantissa bits. fp8 block scales multiply the
 // step's fp32 partial.
-constexpr int SD_BM = 16;
 constexpr int SD_LS = 136;  // bf16 row stride of the LDS activation tile
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -710,14 +709,18 @@ __device__ __forceinline__ float e8m0_f32(uint32_t b) {
                                   : __uint_as_float(b << 23));
 }
 
-template <int BF, int MODE, bool WNT>
+// BM: rows per tile, 16 or 32 (RB = BM / 16 row blocks; each weight
+// fragment feeds one MFMA per row block).
+template <int BF, int MODE, bool WNT, int BM>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit) {
+  constexpr int RB = BM / 16;
+  static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
-  __shared__ int rsrc[ST_MAX_ITEMS][SD_BM];
-  __shared__ float rwl[ST_MAX_ITEMS][SD_BM];
-  __shared__ __attribute__((aligned(16))) uint16_t a_hi[2][SD_BM * SD_LS];
-  __shared__ __attribute__((aligned(16))) uint16_t a_lo[MODE == 1 ? 2 : 1][MODE == 1 ? SD_BM * SD_LS : 8];
+  __shared__ int rsrc[ST_MAX_ITEMS][BM];
+  __shared__ float rwl[ST_MAX_ITEMS][BM];
+  __shared__ __attribute__((aligned(16))) uint16_t a_hi[2][BM * SD_LS];
+  __shared__ __attribute__((aligned(16))) uint16_t a_lo[MODE == 1 ? 2 : 1][MODE == 1 ? BM * SD_LS : 8];
 
   constexpr int NTW = MODE == 0 ? 128 : 256;
   constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
@@ -725,7 +728,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   const int lg = lane >> 4, lc = lane & 15;
 
   auto seg_items_dec = [&](const SegDesc& S) {
-    const int rt = S.tile_info ? *S.num_tiles : (S.total_rows + SD_BM - 1) / SD_BM;
+    const int rt = S.tile_info ? *S.num_tiles : (S.total_rows + BM - 1) / BM;
     return rt * (S.N / NTW) * S.ksplit;
   };
   const int n0 = seg_items_dec(S0);
@@ -751,17 +754,17 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       const int4 d = *(const int4*)(S.tile_info + 4 * rt);
       e = d.x;
       rb = d.y;
-      rows = min(SD_BM, d.z);
+      rows = min(BM, d.z);
     } else {
-      rb = rt * SD_BM;
-      rows = min(SD_BM, S.total_rows - rb);
+      rb = rt * BM;
+      rows = min(BM, S.total_rows - rb);
     }
     // x: segment (bit 0), column slab (bits 1-15), K chunk (bits 16-30)
     desc[tid] = make_int4(seg | (nt << 1) | (kc << 16), e, rb, rows);
   }
   __syncthreads();
-  for (int q = tid; q < nitems * SD_BM; q += ST_THREADS) {
-    const int i = q / SD_BM, r = q % SD_BM;
+  for (int q = tid; q < nitems * BM; q += ST_THREADS) {
+    const int i = q / BM, r = q % BM;
     const int4 d = desc[i];
     const SegDesc& S = (d.x & 1) ? S1 : S0;
     int src = 0;
@@ -791,12 +794,12 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     total_steps += nkb;
   }
 
-  // activation tile of a K step: 16 rows x 128 values; thread tid takes row
-  // tid / 32 and values [4 (tid % 32), +4)
+  // activation tile of a K step: BM rows x 128 values; thread tid takes
+  // rows tid / 32 + 16 r and values [4 (tid % 32), +4)
   const int a_row = tid >> 5, a_col = (tid & 31) * 4;
   typedef typename std::conditional<MODE == 0, u32x2, v4uv>::type AVec;
   struct ASet {
-    AVec v;
+    AVec v[RB];
   };
   struct BSetD {
     v8i v[2];
@@ -805,7 +808,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   };
 
   int pi = 0, pkb = 0, pKB = 1;
-  const uint8_t* pa = nullptr;
+  const uint8_t* pa[RB];
   const uint8_t* pb = nullptr;
   const float *ps0 = nullptr, *ps1 = nullptr;
   const uint16_t* ps4 = nullptr;
@@ -816,7 +819,10 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
     int kb0;
     kchunk(i, kb0, pKB);
-    pa = S.a + ((size_t)rsrc[i][a_row] * K + kb0 * 128 + a_col) * (MODE == 0 ? 2 : 4);
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      pa[r] = S.a + ((size_t)rsrc[i][a_row + 16 * r] * K + kb0 * 128 + a_col) *
+                        (MODE == 0 ? 2 : 4);
     const size_t blk0 = ((size_t)d.y * NT + nt) * KB + kb0;
     if constexpr (BF == SF_FP4) {
       pb = S.wp + blk0 * BLK + (wave * 2) * 1024 + lane * 16;
@@ -842,7 +848,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     }
   };
   auto prefetch = [&](ASet& af, BSetD& b) {
-    af.v = *(const AVec*)(pa + (size_t)pkb * 128 * (MODE == 0 ? 2 : 4));
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      af.v[r] = *(const AVec*)(pa[r] + (size_t)pkb * 128 * (MODE == 0 ? 2 : 4));
     const uint8_t* base = pb + (size_t)pkb * BLK;
     if constexpr (BF == SF_FP4) {
 #pragma unroll
@@ -867,8 +875,12 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     p_advance();
   };
 
-  f32x4 acc[2];
-  acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[RB][2];
+  auto clear_acc = [&]() {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+  clear_acc();
 
   int ci = 0, ckb = 0, cKB = 1, crows = 0;
   auto c_enter = [&](int i) {
@@ -877,101 +889,115 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     crows = desc[i].w;
   };
 
-  // acc[s][v]: token lc of the tile, output column 4 lg + v of subtile s
+  // acc[r][s][v]: row 16 r + lc of the tile, output column 4 lg + v of
+  // subtile s
   auto epilogue = [&](int i) {
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF, kc = d.x >> 16;
     const SegDesc& S = seg ? S1 : S0;
-    if (lc < d.w) {  // K chunk kc's slice (kc = 0 unsplit)
-      const float rw = rwl[i][lc];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int row = 16 * r + lc;
+      if (row >= d.w) continue;  // K chunk kc's slice (kc = 0 unsplit)
+      const float rw = rwl[i][row];
       if constexpr (MODE == 0) {
         if (S.ksplit > 1) {  // chunk sums; launch_split_finish applies SwiGLU
-          float* pg = S.pp + kc * S.pstride + (size_t)(d.z + lc) * S.N +
+          float* pg = S.pp + kc * S.pstride + (size_t)(d.z + row) * S.N +
                       nt * 128 + wave * 16 + lg * 4;
-          *(float4*)pg = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+          *(float4*)pg = make_float4(acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
           *(float4*)(pg + S.ksplit * S.pstride) =
-              make_float4(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
-          acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-          return;
+              make_float4(acc[r][1][0], acc[r][1][1], acc[r][1][2], acc[r][1][3]);
+          continue;
         }
         float h[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          float g = acc[0][v], u = acc[1][v];
+          float g = acc[r][0][v], u = acc[r][1][v];
           if (limit > 0.f) {
             u = fminf(fmaxf(u, -limit), limit);
             g = fminf(g, limit);
           }
           h[v] = silu_f32(g) * u * rw;
         }
-        float* out = (float*)S.hq + (size_t)(d.z + lc) * S.N + nt * 128 + wave * 16 + lg * 4;
+        float* out = (float*)S.hq + (size_t)(d.z + row) * S.N + nt * 128 + wave * 16 + lg * 4;
         *(float4*)out = make_float4(h[0], h[1], h[2], h[3]);
       } else {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          float* out = (float*)S.y + kc * S.pstride + (size_t)(d.z + lc) * S.N +
-                       nt * 256 + wave * 32 + s * 16 + lg * 4;
-          *(float4*)out = make_float4(acc[s][0] * rw, acc[s][1] * rw,
-                                      acc[s][2] * rw, acc[s][3] * rw);
+        for (int sb = 0; sb < 2; ++sb) {
+          float* out = (float*)S.y + kc * S.pstride + (size_t)(d.z + row) * S.N +
+                       nt * 256 + wave * 32 + sb * 16 + lg * 4;
+          *(float4*)out = make_float4(acc[r][sb][0] * rw, acc[r][sb][1] * rw,
+                                      acc[r][sb][2] * rw, acc[r][sb][3] * rw);
         }
       }
     }
-    acc[0] = acc[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    clear_acc();
   };
 
   auto step = [&](int st, ASet& acur, ASet& aload, BSetD& bcur, BSetD& bload) {
     const int buf = st & 1;
-    {  // activations -> LDS as bf16 (mode 1: hi and lo halves), rows past
-       // the tile zeroed
-      const uint32_t m = a_row < crows ? ~0u : 0u;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {  // activations -> LDS as bf16 (mode 1: hi
+                                    // and lo halves), rows past the tile zeroed
+      const int row = a_row + 16 * r;
+      const uint32_t m = row < crows ? ~0u : 0u;
       if constexpr (MODE == 0) {
-        *(u32x2*)(a_hi[buf] + a_row * SD_LS + a_col) =
-            (u32x2){acur.v.x & m, acur.v.y & m};
+        *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
+            (u32x2){acur.v[r].x & m, acur.v[r].y & m};
       } else {
-        float f[4] = {__uint_as_float(acur.v.x & m), __uint_as_float(acur.v.y & m),
-                      __uint_as_float(acur.v.z & m), __uint_as_float(acur.v.w & m)};
+        float f[4] = {__uint_as_float(acur.v[r].x & m), __uint_as_float(acur.v[r].y & m),
+                      __uint_as_float(acur.v[r].z & m), __uint_as_float(acur.v[r].w & m)};
         uint32_t hb[4], lb[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           hb[j] = f32_to_bf16(f[j]);
           lb[j] = f32_to_bf16(f[j] - __uint_as_float(hb[j] << 16));
         }
-        *(u32x2*)(a_hi[buf] + a_row * SD_LS + a_col) =
+        *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
             (u32x2){hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-        *(u32x2*)(a_lo[buf] + a_row * SD_LS + a_col) =
+        *(u32x2*)(a_lo[buf] + row * SD_LS + a_col) =
             (u32x2){lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
       }
     }
     __syncthreads();
     prefetch(aload, bload);
-    f32x4 part[2];
-    part[0] = part[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    f32x4 part[RB][2];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) part[r][0] = part[r][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
       const int ko = lg * 32 + mm * 8;
-      const bf16x8 xh = *(const bf16x8*)(a_hi[buf] + lc * SD_LS + ko);
-      bf16x8 xl;
-      if constexpr (MODE == 1) xl = *(const bf16x8*)(a_lo[buf] + lc * SD_LS + ko);
+      bf16x8 xh[RB], xl[RB];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+      for (int r = 0; r < RB; ++r) {
+        xh[r] = *(const bf16x8*)(a_hi[buf] + (16 * r + lc) * SD_LS + ko);
+        if constexpr (MODE == 1) xl[r] = *(const bf16x8*)(a_lo[buf] + (16 * r + lc) * SD_LS + ko);
+      }
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
         bf16x8 wv;
         if constexpr (BF == SF_FP4) {
-          wv = fp4x8_to_bf16((uint32_t)bcur.v[s][mm], e8m0_f32((bcur.sc >> (8 * s)) & 0xFF));
+          wv = fp4x8_to_bf16((uint32_t)bcur.v[sb][mm], e8m0_f32((bcur.sc >> (8 * sb)) & 0xFF));
         } else {
-          wv = fp8x8_to_bf16((uint32_t)bcur.v[s][2 * mm], (uint32_t)bcur.v[s][2 * mm + 1]);
+          wv = fp8x8_to_bf16((uint32_t)bcur.v[sb][2 * mm], (uint32_t)bcur.v[sb][2 * mm + 1]);
         }
-        f32x4& tgt = BF == SF_FP4 ? acc[s] : part[s];
-        tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xh, tgt, 0, 0, 0);
-        if constexpr (MODE == 1)
-          tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xl, tgt, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          f32x4& tgt = BF == SF_FP4 ? acc[r][sb] : part[r][sb];
+          tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xh[r], tgt, 0, 0, 0);
+          if constexpr (MODE == 1)
+            tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xl[r], tgt, 0, 0, 0);
+        }
       }
     }
     if constexpr (BF != SF_FP4) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        acc[0][v] = fmaf(part[0][v], bcur.sb0, acc[0][v]);
-        acc[1][v] = fmaf(part[1][v], bcur.sb1, acc[1][v]);
-      }
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          acc[r][0][v] = fmaf(part[r][0][v], bcur.sb0, acc[r][0][v]);
+          acc[r][1][v] = fmaf(part[r][1][v], bcur.sb1, acc[r][1][v]);
+        }
     }
     if (++ckb == cKB) {
       epilogue(ci);
@@ -999,20 +1025,60 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
 }
 
-// Decode down projections cut each item's K range into chunks until the
-// launch has about DEC_TARGET_ITEMS items (two per CU), so that a few long
-// items (one expert: a dense MLP, a single token) do not leave most CUs
-// idle; the chunk results are summed by the combine.
+static int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+// Decode K split. A launch's items (upper_items at most) of KB K steps each
+// are cut into ks chunks and dealt over the persistent grid (G workgroups,
+// #CUs rounded up to a multiple of 8); its time goes with the largest
+// number of K steps one workgroup streams, ceil(items ks / G) ceil(KB / ks).
+// Few long items (one expert: a dense MLP, a single token) would leave most
+// CUs idle, and equal items that do not divide evenly over the grid leave a
+// tail (136 items of 40 steps: 40 steps unsplit, 30 at ks = 4, 24 at 5).
+static long dec_split_steps(long items, int KB, int ks) {
+  const long G = 8L * ((num_cus() + 7) / 8);
+  return (items * ks + G - 1) / G * ((KB + ks - 1) / ks);
+}
+
+// The ks in [1, cap] of fewest steps, each split charged `extra` steps and
+// required to save at least `min_gain` of the unsplit steps (ties: smaller).
+static int dec_best_split(long items, int KB, int cap, long extra,
+                          double min_gain) {
+  const long base = dec_split_steps(items, KB, 1);
+  int best = 1;
+  long bcost = base;
+  for (int ks = 2; ks <= cap; ++ks) {
+    const long c = dec_split_steps(items, KB, ks) + extra;
+    if (c < bcost && c <= (1.0 - min_gain) * base) {
+      best = ks;
+      bcost = c;
+    }
+  }
+  return best;
+}
+
 constexpr long DEC_TARGET_ITEMS = 512;
 constexpr int DEC_MAX_KSPLIT = 32;
+// a finish launch costs about as much as streaming three K steps per CU
+constexpr long DEC_FINISH_STEPS = 3;
 
-// Gate/up: split only launches with fewer than two items per CU, into
-// chunks of at least four K steps, at most 8 (the finish reads every slice).
+// Gate/up: only launches with fewer than two items per CU (upper_items is
+// a bound from the tile count, well above the routed count at larger
+// batches), into chunks of at least four K steps, at most 8 (the finish
+// reads every slice).
 int dec_ksplit_up(long upper_items, int KB) {
   if (upper_items <= 0 || upper_items >= DEC_TARGET_ITEMS) return 1;
-  long ks = (DEC_TARGET_ITEMS + upper_items - 1) / upper_items;
-  ks = std::min<long>(ks, std::min(KB / 4, 8));
-  return (int)std::max<long>(ks, 1);
+  return dec_best_split(upper_items, KB, std::max(1, std::min(KB / 4, 8)),
+                        DEC_FINISH_STEPS, 0.0);
 }
 
 // h = silu(g) * u from the K-chunk slices of split mode-0 segments, rows
@@ -1078,24 +1144,13 @@ int launch_split_finish(const SegDesc& s0, const SegDesc* s1, float limit,
   return 0;
 }
 
+// Down: the combine adds the slices, so a split costs no launch; it must
+// save a fifth of the steps (the bound overstates routed items).
 int dec_ksplit(long upper_items, int KB) {
   if (upper_items <= 0 || KB <= 1) return 1;
-  long ks = (DEC_TARGET_ITEMS + upper_items - 1) / upper_items;
-  ks = std::min<long>(ks, std::min(KB, DEC_MAX_KSPLIT));
-  return (int)std::max<long>(ks, 1);
+  return dec_best_split(upper_items, KB, std::min(KB, DEC_MAX_KSPLIT), 0, 0.2);
 }
 
-static int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-            hipSuccess || n <= 0)
-      n = 256;
-  }
-  return n;
-}
 
 // upper_items: an upper bound of the total item count (sizes the grid so
 // that no workgroup receives more than ST_MAX_ITEMS items).
@@ -1164,7 +1219,7 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 #undef GO
 }
 
-template <int BF, int MODE>
+template <int BF, int MODE, int BM>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st) {
   const long per_xcd = (upper_items + 7) / 8;
@@ -1174,7 +1229,7 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   const long grid = 8 * nx;
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   SegDesc dummy = s0;
-  moe_stream_dec_kernel<BF, MODE, true><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+  moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
       s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit);
   SLLM_LAUNCHED();
   return 0;
@@ -1182,9 +1237,10 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
 
 int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
-                      long upper_items, hipStream_t st) {
-  SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1),
-               "stream decode gemm: bad format");
+                      long upper_items, hipStream_t st, int bm) {
+  SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
+                   (bm == 16 || bm == 32),
+               "stream decode gemm: bad format or tile rows %d", bm);
   const int ntw = mode == 0 ? 128 : 256;
   SegDesc seg[2] = {s0_in, s1_in ? *s1_in : s0_in};
   for (int i = 0; i < (s1_in ? 2 : 1); ++i) {
@@ -1199,6 +1255,8 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                  "stream decode gemm: missing W3 scales");
     SLLM_REQUIRE((!s->gather && !s->row_w_by_idx) || s->sorted_idx,
                  "stream decode gemm: gather / row_w_by_idx need sorted_idx");
+    SLLM_REQUIRE(s->tile_info ? s->num_tiles != nullptr : s->total_rows > 0,
+                 "stream decode gemm: identity rows need total_rows > 0");
     SLLM_REQUIRE(s->ksplit <= s->K / 128 && s->ksplit < 32768 &&
                      (s->ksplit == 1 ||
                       (s->pstride > 0 && s->pstride % 4 == 0 &&
@@ -1208,7 +1266,9 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
   }
   const SegDesc& s0 = seg[0];
   const SegDesc* s1 = s1_in ? &seg[1] : nullptr;
-#define GO(B, M) return go_stream_dec<B, M>(s0, s1, topk, limit, upper_items, st)
+#define GO(B, M)                                                         \
+  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st) \
+                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st)
   if (mode == 0) {
     if (bf == SF_FP4) GO(SF_FP4, 0);
     GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales

@@ -111,15 +111,15 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
                   hipStream_t st);
-// Decode variant over the same packed weights: 16-row tiles, weights
-// converted to bf16 in registers and multiplied by unquantized activations
-// with bf16 MFMAs. mode 0 reads bf16 rows (a, row stride K elements) and
+// Decode variant over the same packed weights: bm-row tiles (16 or 32; the
+// tile_info rows must fit), weights converted to bf16 in registers and
+// multiplied by unquantized activations with bf16 MFMAs. mode 0 reads bf16 rows (a, row stride K elements) and
 // writes fp32 h rows to hq (as float*); mode 1 reads fp32 h rows (a as
 // float*, split into bf16 hi + lo) and writes fp32 rows to y (as float*).
 // bf: 0 / 1 fp8 (block scales applied in fp32), 2 MXFP4.
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
-                      hipStream_t st);
+                      hipStream_t st, int bm = 16);
 // K chunks for a decode launch whose item count is at most upper_items
 // over KB 128-wide K steps: down launches (dec_ksplit) and gate/up launches
 // (dec_ksplit_up, which needs a finish launch and so splits only launches
@@ -144,7 +144,8 @@ int launch_combine(const void* y, int y_f32, const int* inv_pos, int topk,
                    const void* y_shared, int T, int H, int out_f32, void* out,
                    hipStream_t st);
 // fp32 rows held as ks / ks_sh K-chunk slices kstride / kstride_sh
-// elements apart (split-K decode); summed slice by slice in order.
+// elements apart (split-K decode); summed slice by slice in order. A null
+// inv_pos is the identity permutation (slot j of token t at row t k + j).
 int launch_combine_split(const float* y, const int* inv_pos, int topk,
                          const float* y_shared, int T, int H, int out_f32,
                          void* out, int ks, long kstride, int ks_sh,

@@ -23,12 +23,12 @@ namespace sllm {
 
 constexpr int PREFILL_BM = 128;
 constexpr int DECODE_MAX_T = 64;
-constexpr int DECODE_BM = 16;
 
 struct Plan {
   bool decode;
   int N;          // T * topk
   int bm, max_tiles;
+  int bm_sh;  // decode: rows per tile of the shared expert's launches
   // decode: K chunks of the streamed gate/up and down launches (routed /
   // shared) and partial-logit slices of the router GEMM
   int ks_up, ks_up_sh, ks_dn, ks_dn_sh, ks_r;
@@ -76,10 +76,14 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.ks_r = p.decode && need_logits && !fused_route ? router_ksplit(T, H) : 1;
   p.N = T * topk;
   if (p.decode) {
-    p.bm = DECODE_BM;  // 16-row tiles: a touched expert's rows, mostly one tile
+    // 16-row tiles (a touched expert's rows, mostly one tile), or 32 when
+    // the experts average more than 16 rows (a dense MLP at 17-64 tokens),
+    // so that each weight block is streamed once per 32 rows, not per 16
+    p.bm = p.N > 16 * std::min(E, p.N) ? 32 : 16;
+    p.bm_sh = deepseek ? (T > 16 ? 32 : 16) : p.bm;  // Qwen: same launches
     // tiles = sum over touched experts of ceil(n_e / bm)
     //       <= touched + floor((N - 1) / bm) <= ceil(N / bm) + min(E, N) - 1
-    p.max_tiles = (p.N + DECODE_BM - 1) / DECODE_BM + (E < p.N ? E : p.N) - 1;
+    p.max_tiles = (p.N + p.bm - 1) / p.bm + (E < p.N ? E : p.N) - 1;
   } else {
     p.bm = PREFILL_BM;
     p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N) - 1;
@@ -100,7 +104,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   if (p.decode) {
     if (!force_gemv) {  // the streamed kernels (the GEMV path does not split)
       const long rt = p.max_tiles;
-      const long sh_rt = has_shared ? (T + DECODE_BM - 1) / DECODE_BM : 0;
+      const long sh_rt = has_shared ? (T + p.bm_sh - 1) / p.bm_sh : 0;
       if (deepseek) {
         p.ks_up = dec_ksplit_up(rt * (I / 128), H / 128);
         p.ks_dn = dec_ksplit(rt * (H / 256), I / 128);
@@ -249,6 +253,16 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const float eps = a->renorm_eps;
 
   const StageClock clk{a->stage_events, st};
+  // One expert, top-1, logits given, streamed decode (a dense MLP run as the
+  // layer): the softmax of one logit is 1 and 1 / (1 + eps) rounds to 1, so
+  // every token's route weight is exactly 1 and the permutation is the
+  // identity. Routing and permutation are skipped and the expert launches
+  // read rows in token order (when no routing output is asked for; the
+  // logits are not read, so a non-finite logit does not reach the output).
+  const bool one_expert = p.decode && a->wgu_packed && E == 1 && k == 1 &&
+                          a->logits_given && 1.0f + eps == 1.0f &&
+                          !a->logits_out && !a->w_out && !a->ids_out &&
+                          !a->counts_out;
   // Decode-size routing: the router GEMM also computes the shared-expert
   // gate, and softmax top-k runs fused with the permutation (two launches
   // instead of four). Stages a call does not run are recorded with zero
@@ -256,7 +270,9 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool small_route = p.decode && route_permute_small_fits(T, E, k);
   bool gate_done = false;
-  if (small_router) {
+  if (one_expert) {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM, 0);
+  } else if (small_router) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
           launch_router_small_gate((const uint16_t*)a->x,
                                    (const uint16_t*)a->router_w, logits, T, E,
@@ -266,14 +282,17 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   }
   // split router: the routing launch finishes the gate from its partials
   float* gate_fin = small_router && sh && p.ks_r > 1 ? gate : nullptr;
-  if (!small_router) {
+  if (!small_router && !one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
           a->logits_given ? 0
                           : launch_router_gemm((const uint16_t*)a->x,
                                                (const uint16_t*)a->router_w,
                                                logits, T, E, H, st));
   }
-  if (small_route) {
+  if (one_expert) {
+    STAGE(clk, SLLM_MOE_STAGE_ROUTE, 0);
+    STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
+  } else if (small_route) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
@@ -305,7 +324,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
                    "sllm_moe_qwen_forward: packed weights incomplete");
       float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
       y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
-      const long sh_rt = sh ? (T + DECODE_BM - 1) / DECODE_BM : 0;
+      const long sh_rt = sh ? (T + p.bm - 1) / p.bm : 0;
       SegDesc r1{}, s1{};
       r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
       r1.tile_info = tiles; r1.num_tiles = ntiles;
@@ -313,6 +332,10 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       r1.N = I; r1.K = H; r1.hq = (uint8_t*)h; r1.total_rows = p.N;
       r1.ksplit = p.ks_up; r1.pp = (float*)(ws + p.gu);
       r1.pstride = (long)p.N * I;
+      if (one_expert) {  // rows in token order (N = T)
+        r1.sorted_idx = nullptr; r1.gather = 0;
+        r1.tile_info = nullptr; r1.num_tiles = nullptr;
+      }
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
       s1.wp = (const uint8_t*)a->sgu_packed; s1.s0 = a->sg_s; s1.s1 = a->su_s;
       s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
@@ -322,7 +345,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
             launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k, 0.f,
                               (long)p.max_tiles * (I / 128) * p.ks_up +
                                   sh_rt * (Is / 128) * p.ks_up_sh,
-                              st) ||
+                              st, p.bm) ||
                 (p.ks_up > 1 &&
                  launch_split_finish(r1, sh ? &s1 : nullptr, 0.f, st)));
       SegDesc r2{}, s2{};
@@ -331,6 +354,11 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
       r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
       r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
+      if (one_expert) {  // route weights are exactly 1
+        r2.total_rows = p.N;
+        r2.sorted_idx = nullptr; r2.tile_info = nullptr; r2.num_tiles = nullptr;
+        r2.row_w = nullptr; r2.row_w_by_idx = 0;
+      }
       s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
       s2.wp = (const uint8_t*)a->sd_packed; s2.s0 = a->sd_s; s2.N = H;
       s2.K = Is; s2.row_w = gate; s2.y = (uint16_t*)y_sh;
@@ -339,11 +367,12 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
             launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
                               (long)p.max_tiles * (H / 256) * p.ks_dn +
                                   sh_rt * (H / 256) * p.ks_dn_sh,
-                              st));
+                              st, p.bm));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
       STAGE(clk, SLLM_MOE_STAGE_COMBINE,
-            launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32, a->out,
+            launch_combine_split(y, one_expert ? nullptr : inv, k, y_sh, T, H,
+                                 a->out_f32, a->out,
                                  p.ks_dn, (long)p.N * H, p.ks_dn_sh,
                                  (long)T * H, st));
     } else {
@@ -521,7 +550,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     float* y = (float*)(ws + p.y);
     float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
     float* y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
-    const long sh_rt = (T + DECODE_BM - 1) / DECODE_BM;
+    const long sh_rt = (T + p.bm_sh - 1) / p.bm_sh;
     SegDesc r1{};
     r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
     r1.tile_info = tiles; r1.num_tiles = ntiles;
@@ -537,11 +566,13 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_stream_dec(2, 0, r1, nullptr, k, L,
-                            (long)p.max_tiles * (I / 128) * p.ks_up, st) ||
+                            (long)p.max_tiles * (I / 128) * p.ks_up, st,
+                            p.bm) ||
               (p.ks_up > 1 && launch_split_finish(r1, nullptr, L, st)));
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
           launch_stream_dec(2, 1, r2, nullptr, k, 0.f,
-                            (long)p.max_tiles * (H / 256) * p.ks_dn, st));
+                            (long)p.max_tiles * (H / 256) * p.ks_dn, st,
+                            p.bm));
     if (sh) {
       SegDesc s1{};
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
@@ -556,11 +587,13 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
             launch_stream_dec(1, 0, s1, nullptr, k, L,
-                              sh_rt * (Is / 128) * p.ks_up_sh, st) ||
+                              sh_rt * (Is / 128) * p.ks_up_sh, st,
+                              p.bm_sh) ||
                 (p.ks_up_sh > 1 && launch_split_finish(s1, nullptr, L, st)));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
             launch_stream_dec(1, 1, s2, nullptr, k, 0.f,
-                              sh_rt * (H / 256) * p.ks_dn_sh, st));
+                              sh_rt * (H / 256) * p.ks_dn_sh, st,
+                              p.bm_sh));
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32, a->out,

@@ -118,7 +118,7 @@ def test_moe_stack_from_fp8_checkpoint(tmp_path):
         np.testing.assert_array_equal(stack.moe(x, i), want)
 
 
-@pytest.mark.parametrize("n", [1, 3, 16])
+@pytest.mark.parametrize("n", [1, 3, 16, 17, 32, 50, 64])
 def test_dense_swiglu_bf16(n):
     from sllm_amd.decode import DenseSwiGLU
     rng = np.random.default_rng(60 + n)

@@ -91,6 +91,21 @@ def test_qwen_decode_c3_shapes(B):
     assert rel < 1e-4
 
 
+@pytest.mark.parametrize("B,E,k", [(17, 2, 2), (40, 4, 2), (64, 4, 2)])
+def test_qwen_decode_32_row_tiles(B, E, k):
+    """Decode with experts averaging more than 16 rows: 32-row tiles for the
+    routed and shared segments (ragged last tiles, experts of 17-32 and of
+    more than 32 rows)."""
+    H, I = 1024, 256
+    x, W = qwen_fp8(seed=120 + B, T=B, H=H, E=E, I=I, Is=I)
+    layer = qwen_layer(W, k)
+    y, r = layer.forward(x, mode="decode", return_routing=True)
+    _check_routing(r, E, k)
+    want = qm.moe_layer_fp8_dequant(x, r["logits"], W, k)
+    rel, mabs, scale = _report(f"qwen decode 32-row B={B} E={E}", y, want)
+    assert rel < 1e-4
+
+
 def test_qwen_logits_given_and_auto_mode():
     x, W = qwen_fp8(seed=5, T=96, H=512, E=8, I=256, Is=256)
     layer = qwen_layer(W, 3)
@@ -265,7 +280,7 @@ def test_deepseek_prefill_c4_shapes():
     assert rel < 3e-3
 
 
-@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("B", [1, 8, 24, 64])
 def test_deepseek_decode(B):
     x, W = deepseek_mxfp4(seed=50 + B, T=B, H=1024, E=16, I=512, Is=512)
     route = dict(n_group=4, topk_group=2, scoring="sigmoid", route_scale=2.5,
