@@ -12,8 +12,9 @@ GEMVs, combine; all on the device, one upload and one download).
 MLP as three GEMMs with a host SwiGLU between them. `DenseSwiGLU` computes
 down(silu(gate x) * up x) as the same fused layer with one expert and top-1
 routing on zero logits: softmax over one logit is exactly 1 and the
-renormalisation 1 / (1 + 1e-20) rounds to 1 in fp32, so the combine scales
-the expert output by exactly 1.
+renormalisation 1 / (1 + 1e-20) rounds to 1 in fp32, so every route weight
+is exactly 1; the layer recognises this case and runs only the expert
+launches (gate/up, down, slice sum) over the rows in token order.
 
 Both keep their staging buffers, workspace and argument blocks between
 calls, so a decode step allocates nothing after its first call at a given
