@@ -641,9 +641,12 @@ static int epl_for(int E) {
 // CUs rather than T / 4 (the reads are bound by per-CU bandwidth).
 static int route_tokens_per_block(int ks) { return ks > 1 ? 1 : 4; }
 
+// Two chunks: the routing kernel's reads of every further slice cost about
+// what the router saves (C3 B=32, layer: unsplit 155-157 us, 2 chunks
+// 153-155, 4 chunks 153-156, 8 chunks 156-157).
 int router_ksplit(int T, int H) {
   if (T > RG_SMALL_T) return 1;
-  return std::max(1, std::min(8, H / 256));
+  return std::max(1, std::min(2, H / 256));
 }
 
 static int launch_router_small(const uint16_t* x, const uint16_t* w,

@@ -93,10 +93,10 @@ def test_host_bf16_rounding_matches_python():
 
 def test_decode_workspace_holds_split_router_slices():
     """Host plan, no GPU: a decode call that computes its own logits splits
-    the router GEMM's K over 8 workgroups (H = 2048) when its batch is routed
-    by the multi-workgroup kernels (17 <= T <= 64 here), so its workspace
-    holds 8 partial-logit slices of T * E floats and 8 partial gate slices
-    of T floats beyond a call given the logits. Batches routed in one fused
+    the router GEMM's K over 2 workgroups when its batch is routed by the
+    multi-workgroup kernels (17 <= T <= 64 here), so its workspace holds 2
+    partial-logit slices of T * E floats and 2 partial gate slices of T
+    floats beyond a call given the logits. Batches routed in one fused
     workgroup (T <= 16) and prefill keep one slice."""
     from sllm_amd.moe import qwen_workspace_bytes as wsb
 
@@ -108,6 +108,6 @@ def test_decode_workspace_holds_split_router_slices():
                            (64, "decode", True), (128, "prefill", False)):
         own = wsb(T, H, E, I, Is, k, mode)
         given = wsb(T, H, E, I, Is, k, mode, logits_given=True)
-        want = (up256(8 * T * E * 4) + up256(9 * T * 4) - up256(T * 4)
+        want = (up256(2 * T * E * 4) + up256(3 * T * 4) - up256(T * 4)
                 if split else up256(T * E * 4))
         assert own - given == want, T
