@@ -11,11 +11,18 @@ namespace sllm {
 // (T floats apart); a softmax routing launch given that buffer as gate
 // adds them in order and writes the sigmoid to gate[0, T).
 int router_ksplit(int T, int H);
+// Prefill (T > 64) may also zero zero_n ints at zero: the permutation's
+// chunk histograms, which a softmax routing launch given them as
+// chunk_hist then fills (integer atomics: the counts do not depend on
+// order), so that launch_permute(..., hist_ready = true) skips its
+// histogram pass.
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
-                       int T, int E, int H, hipStream_t st, int ks = 1);
+                       int T, int E, int H, hipStream_t st, int ks = 1,
+                       int* zero = nullptr, long zero_n = 0);
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st,
-                         int ks = 1, float* gate = nullptr);
+                         int ks = 1, float* gate = nullptr,
+                         int* chunk_hist = nullptr);
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).
@@ -38,11 +45,16 @@ int launch_route_hash(const float* logits, const int* token_ids,
                       const int* tid2eid, int vocab, float* w, int* ids,
                       int T, int E, int topk, int scoring, float route_scale,
                       hipStream_t st, int ks = 1);
+// Multi-workgroup permutation: histograms of PERM_CHUNK assignments per
+// chunk (chunk c, expert e at scratch int c E + e), used when
+// permute_uses_chunk_hist(N, E) (otherwise one workgroup permutes).
+constexpr int PERM_CHUNK = 1024;
+bool permute_uses_chunk_hist(int N, int E);
 size_t permute_scratch_bytes(int N, int E);
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,
                    int* tile_info, int* num_tiles, int max_tiles,
-                   void* scratch, hipStream_t st);
+                   void* scratch, hipStream_t st, bool hist_ready = false);
 int launch_act_quant(const uint16_t* x, int T, int H, int pow2, uint8_t* q,
                      float* s, const uint16_t* gate_w, float* gate_out,
                      hipStream_t st);

@@ -282,12 +282,22 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   }
   // split router: the routing launch finishes the gate from its partials
   float* gate_fin = small_router && sh && p.ks_r > 1 ? gate : nullptr;
+  // Prefill router GEMM + softmax routing + multi-workgroup permutation: the
+  // router zeroes the permutation's chunk histograms and the routing launch
+  // fills them, which saves the permutation's histogram launch.
+  const bool route_hist = !small_router && !one_expert && !small_route &&
+                          !a->logits_given && T > 64 &&
+                          permute_uses_chunk_hist(p.N, E);
+  int* chunk_hist = route_hist ? (int*)(ws + p.pscr) : nullptr;
+  const long hist_n =
+      route_hist ? (long)((p.N + PERM_CHUNK - 1) / PERM_CHUNK) * E : 0;
   if (!small_router && !one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
           a->logits_given ? 0
                           : launch_router_gemm((const uint16_t*)a->x,
                                                (const uint16_t*)a->router_w,
-                                               logits, T, E, H, st));
+                                               logits, T, E, H, st, 1,
+                                               chunk_hist, hist_n));
   }
   if (one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE, 0);
@@ -302,10 +312,11 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
           launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
-                               gate_fin));
+                               gate_fin, chunk_hist));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
-                         tiles, ntiles, p.max_tiles, ws + p.pscr, st));
+                         tiles, ntiles, p.max_tiles, ws + p.pscr, st,
+                         route_hist));
   }
 
   if (p.decode) {

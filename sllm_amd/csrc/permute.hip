@@ -28,7 +28,6 @@
 
 namespace sllm {
 
-constexpr int PERM_CHUNK = 1024;
 constexpr int PERM_SCAN_REG = 48;  // chunk counts an expert keeps in registers
 
 __global__ __launch_bounds__(256) void permute_hist_kernel(
@@ -276,6 +275,10 @@ __global__ __launch_bounds__(1024) void permute_fused_kernel(
                      inv_pos, tile_info, num_tiles, max_tiles, hist, sh);
 }
 
+bool permute_uses_chunk_hist(int N, int E) {
+  return !(N <= PERM_FUSED_MAX_N && E <= PERM_FUSED_MAX_E);
+}
+
 size_t permute_scratch_bytes(int N, int E) {
   int nchunks = N > 0 ? (N + PERM_CHUNK - 1) / PERM_CHUNK : 1;
   return align_up((size_t)nchunks * E * sizeof(int), 256);
@@ -286,7 +289,7 @@ size_t permute_scratch_bytes(int N, int E) {
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,
                    int* tile_info, int* num_tiles, int max_tiles,
-                   void* scratch, hipStream_t st) {
+                   void* scratch, hipStream_t st, bool hist_ready) {
   SLLM_REQUIRE(ids && counts && offsets && sorted_idx && inv_pos &&
                    tile_info && num_tiles && scratch,
                "permute: null pointer");
@@ -295,7 +298,7 @@ int launch_permute(const int* ids, int N, int E, int bm, int* counts,
   const int nchunks = (N + PERM_CHUNK - 1) / PERM_CHUNK;
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
-  if (N <= PERM_FUSED_MAX_N && E <= PERM_FUSED_MAX_E) {
+  if (!permute_uses_chunk_hist(N, E)) {
     permute_fused_kernel<<<1, 1024, 0, st>>>(ids, N, E, nbits, bm, counts,
                                              offsets, sorted_idx, inv_pos,
                                              tile_info, num_tiles, max_tiles);
@@ -304,8 +307,10 @@ int launch_permute(const int* ids, int N, int E, int bm, int* counts,
   }
   int* chunk_hist = (int*)scratch;
   const size_t lds = (size_t)E * sizeof(int);
-  permute_hist_kernel<<<nchunks, 256, lds, st>>>(ids, N, E, chunk_hist);
-  SLLM_LAUNCHED();
+  if (!hist_ready) {  // else filled by the routing launch
+    permute_hist_kernel<<<nchunks, 256, lds, st>>>(ids, N, E, chunk_hist);
+    SLLM_LAUNCHED();
+  }
   if (E <= PERM_FUSED_MAX_E) {
     static_assert(PERM_CHUNK == PERM_FUSED_WAVES * 64, "one group per wave");
     permute_chunk_kernel<<<nchunks, 1024, 0, st>>>(

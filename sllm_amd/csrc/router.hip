@@ -51,10 +51,17 @@ constexpr int RG_NS = 3;  // register stages (prefetch distance in chunks)
 
 __global__ __launch_bounds__(512, 1) void router_gemm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    float* __restrict__ logits, int T, int E, int H) {
+    float* __restrict__ logits, int T, int E, int H, int* __restrict__ zero,
+    long zero_n) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][RG_TT * RG_LS];
   __shared__ __attribute__((aligned(16))) uint16_t ws[2][RG_TE * RG_LS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  {  // the permutation's chunk histograms, filled by the routing launch
+    const long nthr = (long)gridDim.x * gridDim.y * 512;
+    for (long i = ((long)blockIdx.y * gridDim.x + blockIdx.x) * 512 + tid;
+         i < zero_n; i += nthr)
+      zero[i] = 0;
+  }
   const int lr = lane & 15, lg = lane >> 4;
   const int wm = wave >> 2, we = wave & 3;
   const int t0 = blockIdx.x * RG_TT, e0 = blockIdx.y * RG_TE;
@@ -420,13 +427,19 @@ __device__ __forceinline__ void route_gate_finish(float* gate, int T, int t,
 template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
     float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
-    int E, int topk, float eps, int ks, float* __restrict__ gate) {
+    int E, int topk, float eps, int ks, float* __restrict__ gate,
+    int* __restrict__ chunk_hist) {
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (t >= T) return;
   route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
                            w_out + (size_t)t * topk, id_out + (size_t)t * topk,
                            nullptr);
-  if (gate && (threadIdx.x & 63) == 0) route_gate_finish(gate, T, t, ks);
+  if (gate && lane == 0) route_gate_finish(gate, T, t, ks);
+  if (chunk_hist && lane < topk) {  // lane reads back its own id
+    const int a = t * topk + lane;
+    atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + id_out[a]], 1);
+  }
 }
 
 // Decode (T * topk <= PERM_FUSED_MAX_N, E <= PERM_FUSED_MAX_E): softmax
@@ -668,18 +681,22 @@ static int launch_router_small(const uint16_t* x, const uint16_t* w,
 }
 
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
-                       int T, int E, int H, hipStream_t st, int ks) {
+                       int T, int E, int H, hipStream_t st, int ks,
+                       int* zero, long zero_n) {
   SLLM_REQUIRE(x && w && logits, "router_gemm: null pointer");
   SLLM_REQUIRE(T > 0 && E > 0 && H > 0 && H % 128 == 0,
                "router_gemm: need T,E>0 and H %% 128 == 0 (T=%d E=%d H=%d)",
                T, E, H);
   SLLM_REQUIRE(ks == 1 || T <= RG_SMALL_T, "router_gemm: K split needs T <= %d",
                RG_SMALL_T);
+  SLLM_REQUIRE(zero_n == 0 || (zero && T > RG_SMALL_T),
+               "router_gemm: zeroing needs the prefill kernel");
   if (T <= RG_SMALL_T) {
     return launch_router_small(x, w, logits, T, E, H, nullptr, nullptr, ks, st);
   } else {
     dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
-    router_gemm_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H);
+    router_gemm_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, zero,
+                                             zero_n);
   }
   SLLM_LAUNCHED();
   return 0;
@@ -734,7 +751,7 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
 
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st, int ks,
-                         float* gate) {
+                         float* gate, int* chunk_hist) {
   SLLM_REQUIRE(logits && w && ids && ks >= 1 && (!gate || ks > 1),
                "route_softmax: null pointer or bad logit slices");
   SLLM_REQUIRE(T > 0 && E > 0 && topk > 0 && topk <= E && E <= 2048 &&
@@ -747,7 +764,7 @@ int launch_route_softmax(const float* logits, float* w, int* ids, int T,
 #define CASE(n)                                                               \
   case n:                                                                     \
     route_softmax_kernel<n><<<grid, 64 * tpb, 0, st>>>(                       \
-        (float*)logits, w, ids, T, E, topk, eps, ks, gate);                   \
+        (float*)logits, w, ids, T, E, topk, eps, ks, gate, chunk_hist);       \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE
