@@ -186,6 +186,14 @@ class DeviceLayerDS:
         self.rng = rng
 
 
+def c4_inputs(layer):
+    """The C4 activations: N(0, 1) rows from the layer's rng (drawn right
+    after the router weights and bias), as float32; uploaded as bf16
+    (rounded to nearest even, so the layer sees to_bf16_values of them)."""
+    c = layer.cfg
+    return layer.rng.standard_normal((c["T"], c["H"])).astype("float32")
+
+
 def ds_call(layer, x, out, ws, T, mode, debug=None, stage_events=None):
     from sllm_amd.moe import deepseek_forward_dev
     c = layer.cfg
@@ -233,7 +241,7 @@ def run_c4(args):
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     t0 = time.perf_counter()
     layer = DeviceLayerDS(c, seed=args.seed)
-    x = to_device_raw(to_bf16(layer.rng.standard_normal((T, H)).astype(np.float32)))
+    x = to_device_raw(to_bf16(c4_inputs(layer)))
     out = DeviceBuffer(T * H * 2)
     ws = DeviceBuffer(deepseek_workspace_bytes(T, H, E, I, Is, k, "prefill"))
     cnt = DeviceBuffer(E * 4)
@@ -465,6 +473,49 @@ def _c4_routing_us(c, rng, reps=20):
     return out
 
 
+def c2_inputs(layer):
+    """The C2 / C3 activations: bf16 N(0, 1) rows from the layer's rng (drawn
+    right after the weights, as the headline run does)."""
+    c = layer.cfg
+    return to_bf16_values(layer.rng.standard_normal((c["T"], c["H"])).astype("float32"))
+
+
+C5_EMPTY_FRAC = 20   # the lowest-ranked E / 20 experts receive no tokens
+
+
+def c5_inputs(layer):
+    """C5 activations and skewed router logits: x as c2_inputs, logits =
+    x . router_w^T - beta ln(rank_e) with ranks a seeded permutation of
+    1..E and beta calibrated (bisection on the first 2048 tokens) so that the
+    top 10% of experts receive 60% of the assignments; the E / 20 experts of
+    the lowest ranks get a further -64 (a softmax weight below 1e-27 of the
+    others), so that they receive no tokens. Returns (x, logits, beta) on
+    the host."""
+    import numpy as np
+    c = layer.cfg
+    E, k = c["E"], c["k"]
+    xh = c2_inputs(layer)
+    rwh = to_bf16_values(layer.router_w_host)
+    logits0 = (xh @ rwh.T).astype(np.float32)
+    rank = layer.rng.permutation(E) + 1
+    off = np.where(rank > E - E // C5_EMPTY_FRAC, 64.0, 0.0)
+    top = E // 10
+
+    def share(beta, n=2048):
+        lg = logits0[:n] - beta * np.log(rank)[None, :] - off[None, :]
+        ids = np.argpartition(-lg, k, axis=1)[:, :k]
+        cnt = np.bincount(ids.ravel(), minlength=E)
+        return np.sort(cnt)[::-1][:top].sum() / cnt.sum()
+
+    lo, hi = 0.0, 10.0
+    for _ in range(40):
+        mid = 0.5 * (lo + hi)
+        lo, hi = (mid, hi) if share(mid) < 0.6 else (lo, mid)
+    beta = 0.5 * (lo + hi)
+    logits = (logits0 - beta * np.log(rank)[None, :] - off[None, :]).astype(np.float32)
+    return xh, logits, beta
+
+
 def run_c5(args):
     """C5: C2 shapes at T=16384 with Zipf-skewed routing (logit bias
     -beta ln(rank_e), ranks a seeded permutation of 1..E, beta calibrated so
@@ -477,24 +528,8 @@ def run_c5(args):
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     t0 = time.perf_counter()
     layer = DeviceLayer(c, seed=args.seed)
-    xh = to_bf16_values(layer.rng.standard_normal((T, H)).astype(np.float32))
-    rwh = to_bf16_values(layer.router_w_host)
-    logits0 = (xh @ rwh.T).astype(np.float32)
-    rank = layer.rng.permutation(E) + 1
+    xh, logits, beta = c5_inputs(layer)
     top = E // 10
-
-    def share(beta, n=2048):
-        lg = logits0[:n] - beta * np.log(rank)[None, :]
-        ids = np.argpartition(-lg, k, axis=1)[:, :k]
-        cnt = np.bincount(ids.ravel(), minlength=E)
-        return np.sort(cnt)[::-1][:top].sum() / cnt.sum()
-
-    lo, hi = 0.0, 10.0
-    for _ in range(40):
-        mid = 0.5 * (lo + hi)
-        lo, hi = (mid, hi) if share(mid) < 0.6 else (lo, mid)
-    beta = 0.5 * (lo + hi)
-    logits = (logits0 - beta * np.log(rank)[None, :]).astype(np.float32)
     x = to_device_raw(to_bf16(xh))
     lg = to_device_raw(logits)
     out = DeviceBuffer(T * H * 2)
@@ -701,7 +736,7 @@ def main(argv=None) -> int:
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     t_setup = time.perf_counter()
     layer = DeviceLayer(c, seed=args.seed)
-    x_host = to_bf16_values(layer.rng.standard_normal((T, H)).astype(np.float32))
+    x_host = c2_inputs(layer)
     x = to_device_raw(to_bf16(x_host))
     out = DeviceBuffer(T * H * 2)
     ws = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, "prefill"))

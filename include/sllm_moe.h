@@ -168,7 +168,13 @@ int sllm_moe_route_grouped(const float* logits, const float* bias,
  * ref/hf_sources/dsv4/model.py:620-627): ids = tid2eid[clip(token_ids[t],
  * 0, vocab-1)] (tid2eid (vocab, topk) int32, table order, no bias), weights
  * = those experts' scores, renormalized unless softmax, times route_scale.
- * scoring as in sllm_moe_route_grouped; E <= 2048, topk <= 64. */
+ * scoring as in sllm_moe_route_grouped; E <= 2048, topk <= 64.
+ * Contract: every tid2eid entry lies in [0, E) (the reference raises
+ * IndexError for larger ids). The kernel does not read out of bounds for a
+ * bad entry: it writes the id through with a NaN weight (so the token's
+ * renormalized weights are NaN), the permutation drops that assignment
+ * (inv_pos -1) and the combine skips it. sllm_amd.moe.DeepseekMoE rejects
+ * such tables on the host. */
 int sllm_moe_route_hash(const float* logits, const int* token_ids,
                         const int* tid2eid, int vocab, float* w_out,
                         int* id_out, int T, int E, int topk, int scoring,
@@ -205,6 +211,19 @@ long sllm_moe_packed_scale_bytes(int up, int E, int N, int K);
 int sllm_moe_pack_weights(int fp4, int up, const void* w0, const void* w1,
                           const void* s0, const void* s1, int E, int N, int K,
                           void* out, void* out_scales, void* stream);
+/* Streamed-GEMM health (new: no reference counterpart; the reference's
+ * kernels have no work-item bound). The layer sizes each streamed launch's
+ * persistent grid from a host bound of its work items, and a launch whose
+ * bound is too small is refused (rc -2) before it runs. A workgroup that
+ * still receives more items than it holds marks a per-device word and
+ * leaves them undone; sllm_moe_stream_status synchronizes `stream`, returns
+ * -2 (and clears the mark) if any launch did so since the last call, else 0.
+ * sllm_moe_tile_bound is the bound of sum_e ceil(n_e / bm) for N
+ * assignments over E experts; sllm_moe_stream_grid is the grid used for an
+ * item bound on num_cus CUs (host-only queries). */
+int sllm_moe_stream_status(void* stream);
+long sllm_moe_tile_bound(long N, int E, int bm);
+long sllm_moe_stream_grid(long upper_items, int num_cus);
 /* Synthetic-weight quantizers (data preparation): FP8 128x128 block
  * (s = amax/448, optionally its power-of-two ceiling) and MXFP4 per 32. */
 int sllm_quantize_weight_fp8(const float* w, int N, int K, int pow2,
@@ -287,6 +306,13 @@ typedef struct sllm_moe_qwen_args {
   const void* wd_packed;  /* pack(up=0, wd, E, H, I) */
   const void* sgu_packed; /* pack(up=1, sg, su, 1, Is, H) */
   const void* sd_packed;  /* pack(up=0, sd, 1, H, Is) */
+  /* Optional debug copies of the permutation the layer ran (N = T*k
+   * assignments, flat index t*k + j): sorted_out (N) i32 the assignment at
+   * each expert-major position, inv_pos_out (N) i32 each assignment's
+   * position. Like the other debug outputs, asking for them keeps a
+   * one-expert top-1 call on the routed path (which writes them). */
+  int* sorted_out;
+  int* inv_pos_out;
 } sllm_moe_qwen_args;
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
@@ -346,6 +372,9 @@ typedef struct sllm_moe_ds_args {
   const int* token_ids;
   const int* tid2eid;
   int vocab;
+  /* Optional debug copies of the permutation, as in sllm_moe_qwen_args. */
+  int* sorted_out;
+  int* inv_pos_out;
 } sllm_moe_ds_args;
 
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a);

@@ -124,13 +124,25 @@ def decode_ue8m0(u8) -> np.ndarray:
     return out.astype(np.float32)
 
 
+def _fp4_pair_table() -> np.ndarray:
+    # byte b -> the two float32 values (low nibble, high nibble), as one
+    # 8-byte word so a single gather decodes a byte
+    b = np.arange(256)
+    pair = np.stack([FP4_TABLE[b & 0x0F], FP4_TABLE[b >> 4]], axis=1)
+    return np.ascontiguousarray(pair.astype(np.float32)).view(np.uint64).reshape(256)
+
+
+_FP4_PAIRS = None
+
+
 def decode_fp4_packed(packed) -> np.ndarray:
     """(N, K/2) packed E2M1 bytes -> (N, K) float32, low nibble = even k."""
+    global _FP4_PAIRS
+    if _FP4_PAIRS is None:
+        _FP4_PAIRS = _fp4_pair_table()
     p = np.asarray(packed, dtype=np.uint8)
-    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.float32)
-    out[..., 0::2] = FP4_TABLE[p & 0x0F]
-    out[..., 1::2] = FP4_TABLE[p >> 4]
-    return out
+    out = _FP4_PAIRS[p].view(np.float32)
+    return out.reshape(p.shape[:-1] + (p.shape[-1] * 2,))
 
 
 def encode_e2m1_rne(x) -> np.ndarray:

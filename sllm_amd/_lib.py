@@ -38,6 +38,7 @@ class QwenArgs(Structure):
         ("ids_out", P), ("counts_out", P), ("workspace", P),
         ("workspace_bytes", c_long), ("stream", P), ("stage_events", P),
         ("wgu_packed", P), ("wd_packed", P), ("sgu_packed", P), ("sd_packed", P),
+        ("sorted_out", P), ("inv_pos_out", P),
     ]
 
 
@@ -58,6 +59,7 @@ class DeepseekArgs(Structure):
         ("w13_packed", P), ("w13_s_packed", P), ("w2_packed", P),
         ("w2_s_packed", P), ("s13_packed", P), ("s2_packed", P),
         ("token_ids", P), ("tid2eid", P), ("vocab", c_int),
+        ("sorted_out", P), ("inv_pos_out", P),
     ]
 
 
@@ -124,6 +126,9 @@ SIGNATURES = {
     "sllm_moe_packed_scale_bytes": (c_long, [c_int, c_int, c_int, c_int]),
     "sllm_moe_pack_weights": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int,
                                       c_int, P, P, P]),
+    "sllm_moe_stream_status": (c_int, [P]),
+    "sllm_moe_tile_bound": (c_long, [c_long, c_int, c_int]),
+    "sllm_moe_stream_grid": (c_long, [c_long, c_int]),
     "sllm_quantize_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P, P]),
     "sllm_quantize_weight_mxfp4": (c_int, [P, c_int, c_int, P, P, P]),
     "sllm_moe_qwen_workspace_bytes": (c_long, [POINTER(QwenArgs)]),

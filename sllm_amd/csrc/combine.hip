@@ -47,6 +47,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
   for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < topk; ++j) {
+      if (pos[j] < 0) continue;  // a dropped assignment (expert id outside [0, E))
       float v[8];
       load8<TY>(y + (size_t)pos[j] * H + c, v);
 #pragma unroll
@@ -104,14 +105,17 @@ __global__ __launch_bounds__(64 * CF_WAVES) void combine_f32_kernel(
 #pragma unroll
     for (int u = 0; u < CF_BATCH; ++u) {
       const int sl = min(b + u * CF_WAVES, nsl - 1);
+      // a dropped assignment (expert id outside [0, E)) has position -1: it
+      // reads row 0 and is not added
       const float* src =
-          sl < nr ? y + (sl % ks) * kstride + (size_t)pos[sl / ks] * H
+          sl < nr ? y + (sl % ks) * kstride + (size_t)max(pos[sl / ks], 0) * H
                   : y_shared + (sl - nr) * kstride_sh + (size_t)t * H;
       v[u] = *(const float4*)(src + c);
     }
 #pragma unroll
     for (int u = 0; u < CF_BATCH; ++u) {
-      if (b + u * CF_WAVES < nsl) {
+      const int sl = b + u * CF_WAVES;
+      if (sl < nsl && (sl >= nr || pos[sl / ks] >= 0)) {
         acc.x += v[u].x;
         acc.y += v[u].y;
         acc.z += v[u].z;

@@ -38,6 +38,15 @@ const char* last_error();
     }                                                                         \
   } while (0)
 
+// A capacity bound (the reference's rc -2, qwen4.cu:582, 661).
+#define SLLM_CAPACITY(cond, ...)                                              \
+  do {                                                                        \
+    if (!(cond)) {                                                            \
+      ::sllm::set_error(__VA_ARGS__);                                         \
+      return -2;                                                              \
+    }                                                                         \
+  } while (0)
+
 // Checks the launch that was just issued.
 #define SLLM_LAUNCHED()                                                       \
   do {                                                                        \

@@ -150,6 +150,12 @@ __device__ __forceinline__ uint4 ld_stream(const void* p) {
   }
 }
 
+// Set (to 1) by a streamed launch whose workgroup was dealt more than
+// ST_MAX_ITEMS items, which it then leaves undone: the host sizes the grid
+// from a bound of the item count, so this marks a host sizing error. One
+// word per device (zero at load); sllm_moe_stream_status reads and clears it.
+__device__ int stream_item_overflow;
+
 template <int MODE>
 __device__ __forceinline__ int seg_items(const SegDesc& s) {
   const int ntn = MODE == 0 ? s.N / 128 : s.N / 256;
@@ -247,7 +253,11 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   const int xbeg = (int)((long)total * xcd / 8);
   const int xend = (int)((long)total * (xcd + 1) / 8);
   const int nitems = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
-  if (nitems == 0 || nitems > ST_MAX_ITEMS) return;  // host sizes the grid
+  if (nitems > ST_MAX_ITEMS) {  // host sizes the grid: a sizing error
+    if (tid == 0) stream_item_overflow = 1;
+    return;
+  }
+  if (nitems == 0) return;
   auto item_at = [&](int m) { return xbeg + jx + m * nx; };
 
   // ---- phase 0: descriptors and gathered row indices -> LDS ---------------
@@ -739,7 +749,11 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   const int xbeg = (int)((long)total * xcd / 8);
   const int xend = (int)((long)total * (xcd + 1) / 8);
   const int nitems = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
-  if (nitems == 0 || nitems > ST_MAX_ITEMS) return;  // host sizes the grid
+  if (nitems > ST_MAX_ITEMS) {  // host sizes the grid: a sizing error
+    if (tid == 0) stream_item_overflow = 1;
+    return;
+  }
+  if (nitems == 0) return;
 
   if (tid < nitems) {
     const int it = xbeg + jx + tid * nx;
@@ -1152,20 +1166,38 @@ int dec_ksplit(long upper_items, int KB) {
 }
 
 
+// Host bound of a launch's item count: per segment, (row tiles: the tile
+// table's bound, or ceil(total_rows / bm) for identity rows) x column slabs
+// x K chunks. Refuses (rc -2) a caller's upper_items below it, since the grid
+// sized from upper_items could then deal a workgroup more than ST_MAX_ITEMS.
+static int check_item_bound(const SegDesc& s0, const SegDesc* s1, int ntw,
+                            int bm, long upper_items, const char* who) {
+  long bound = 0;
+  for (const SegDesc* s : {&s0, s1}) {
+    if (!s) continue;
+    SLLM_REQUIRE(!s->tile_info || s->max_tiles > 0,
+                 "%s: a tile-table segment needs its max_tiles bound", who);
+    const long rt = s->tile_info ? s->max_tiles : (s->total_rows + bm - 1) / bm;
+    bound += rt * (s->N / ntw) * std::max(1, s->ksplit);
+  }
+  SLLM_CAPACITY(upper_items >= bound,
+                "%s: upper_items %ld below the item bound %ld", who,
+                upper_items, bound);
+  return 0;
+}
+
 // upper_items: an upper bound of the total item count (sizes the grid so
 // that no workgroup receives more than ST_MAX_ITEMS items).
 template <int BF, int MODE>
 static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
                      float limit, int pow2, long upper_items, hipStream_t st) {
   const bool perstep = s0.K % 512 != 0 || (s1 && s1->K % 512 != 0);
-  // workgroups per XCD: at least one per CU, and enough that no workgroup
-  // receives more than ST_MAX_ITEMS items (an XCD's range holds at most
-  // ceil(upper / 8) items, dealt round-robin over its workgroups)
-  const long per_xcd = (upper_items + 7) / 8;
-  long nx = (num_cus() + 7) / 8;
-  const long need = (per_xcd + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
-  if (need > nx) nx = need;
-  const long grid = 8 * nx;
+  {
+    const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, ST_BM,
+                                    upper_items, "stream gemm");
+    if (rc) return rc;
+  }
+  const long grid = stream_grid(upper_items, num_cus(), ST_MAX_ITEMS);
   SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
   SegDesc dummy = s0;
   const SegDesc& b = s1 ? *s1 : dummy;
@@ -1222,11 +1254,12 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 template <int BF, int MODE, int BM>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st) {
-  const long per_xcd = (upper_items + 7) / 8;
-  long nx = (num_cus() + 7) / 8;
-  const long need = (per_xcd + ST_MAX_ITEMS - 1) / ST_MAX_ITEMS;
-  if (need > nx) nx = need;
-  const long grid = 8 * nx;
+  {
+    const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, BM,
+                                    upper_items, "stream decode gemm");
+    if (rc) return rc;
+  }
+  const long grid = stream_grid(upper_items, num_cus(), ST_MAX_ITEMS);
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
@@ -1294,6 +1327,42 @@ long packed_scale_bytes(int up, int E, int N, int K) {
 using namespace sllm;
 
 extern "C" {
+
+// 0 when no streamed launch on this device has overflowed its workgroup
+// item bound since the last call; otherwise clears the mark and returns -2.
+// Synchronizes `stream` first (every launch before the call is covered).
+int sllm_moe_stream_status(void* stream) {
+  SLLM_HIP(hipStreamSynchronize((hipStream_t)stream));
+  int v = 0;
+  SLLM_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(stream_item_overflow), sizeof v));
+  if (v) {
+    const int zero = 0;
+    SLLM_HIP(hipMemcpyToSymbol(HIP_SYMBOL(stream_item_overflow), &zero, sizeof zero));
+    set_error("a streamed expert GEMM workgroup was dealt more than %d items "
+              "and left them undone (host item bound too small)",
+              ST_MAX_ITEMS);
+    return -2;
+  }
+  return 0;
+}
+
+// Host planning queries (no device work): the ragged tile-count bound and
+// the persistent grid the streamed launches use for an item bound.
+long sllm_moe_tile_bound(long N, int E, int bm) {
+  if (N < 0 || E <= 0 || bm <= 0) {
+    set_error("sllm_moe_tile_bound: bad args");
+    return -1;
+  }
+  return tile_bound(N, E, bm);
+}
+
+long sllm_moe_stream_grid(long upper_items, int num_cus) {
+  if (upper_items < 0 || num_cus <= 0) {
+    set_error("sllm_moe_stream_grid: bad args");
+    return -1;
+  }
+  return stream_grid(upper_items, num_cus, ST_MAX_ITEMS);
+}
 
 // Size in bytes of the packed weight (and, for fp4, of the packed scales).
 long sllm_moe_packed_bytes(int fp4, int up, int E, int N, int K) {

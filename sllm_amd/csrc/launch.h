@@ -87,6 +87,27 @@ int launch_gemm2_mx(int b_fp4, const uint8_t* hq, const float* hs,
 // Persistent weight-streaming grouped GEMM over packed weights
 // (gemm_stream.hip). bf: 0 fp8 + fp32 scales, 1 fp8 + power-of-two scales,
 // 2 MXFP4; mode 0: gate/up + SwiGLU + e4m3 re-quant, 1: down -> bf16 rows.
+// Maximum of the ragged tile count sum_e ceil(n_e / bm) over N
+// assignments to at most E experts: with t >= 1 touched experts,
+// sum_e ceil(n_e / bm) = t + sum_e floor((n_e - 1) / bm) <= t + floor((N - t) / bm),
+// which grows with t, so the maximum is m + floor((N - m) / bm) at
+// m = min(E, N); m - 1 experts with one row and one with the rest reach it.
+inline long tile_bound(long N, long E, int bm) {
+  const long m = E < N ? E : N;
+  return N <= 0 ? 0 : m + (N - m) / bm;
+}
+// Persistent grid of a streamed launch with at most upper_items items:
+// #CUs rounded up to a multiple of 8 (one XCD slot each), grown until no
+// workgroup is dealt more than max_items (an XCD's range holds at most
+// ceil(upper / 8) items, dealt round-robin over its workgroups).
+inline long stream_grid(long upper_items, int num_cus, int max_items) {
+  const long per_xcd = (upper_items + 7) / 8;
+  long nx = (num_cus + 7) / 8;
+  const long need = (per_xcd + max_items - 1) / max_items;
+  if (need > nx) nx = need;
+  return 8 * nx;
+}
+
 struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   const uint8_t* a;        // A rows (row stride K bytes)
   const float* sa;         // A scales (row stride K / 128)
@@ -95,6 +116,7 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   const int* tile_info;    // int4 per tile: expert, first row, rows, 0;
                            // null: identity rows [0, total_rows)
   const int* num_tiles;
+  int max_tiles;           // host bound of *num_tiles (tile_info segments)
   int total_rows;
   const uint8_t* wp;       // packed weights
   const void* s0;          // fp8: fp32 scales of W1 / W2 (reference layout);

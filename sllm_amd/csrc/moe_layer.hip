@@ -81,13 +81,10 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     // so that each weight block is streamed once per 32 rows, not per 16
     p.bm = p.N > 16 * std::min(E, p.N) ? 32 : 16;
     p.bm_sh = deepseek ? (T > 16 ? 32 : 16) : p.bm;  // Qwen: same launches
-    // tiles = sum over touched experts of ceil(n_e / bm)
-    //       <= touched + floor((N - 1) / bm) <= ceil(N / bm) + min(E, N) - 1
-    p.max_tiles = (p.N + p.bm - 1) / p.bm + (E < p.N ? E : p.N) - 1;
   } else {
     p.bm = PREFILL_BM;
-    p.max_tiles = (p.N + PREFILL_BM - 1) / PREFILL_BM + (E < p.N ? E : p.N) - 1;
   }
+  p.max_tiles = (int)tile_bound(p.N, E, p.bm);
   size_t c = 0;
   p.logits = need_logits ? take(c, (size_t)p.ks_r * T * E * 4) : 0;
   p.w = take(c, (size_t)p.N * 4);
@@ -157,10 +154,11 @@ struct StageClock {
   }
 };
 
+// a failing stage's code (-1 error, -2 capacity) is the entry point's
 #define STAGE(clk, s, call)                                                   \
   do {                                                                        \
     if ((clk).begin(s)) return -1;                                            \
-    if (call) return -1;                                                      \
+    if (const int _rc = (call)) return _rc < 0 ? _rc : -1;                    \
     if ((clk).end(s)) return -1;                                              \
   } while (0)
 
@@ -184,9 +182,15 @@ static int check_common(const A* a, const char* who) {
 }
 
 static int copy_debug(const float* logits, const float* w, const int* ids,
-                      const int* counts, int T, int E, int N, float* logits_out,
-                      float* w_out, int* ids_out, int* counts_out,
-                      hipStream_t st) {
+                      const int* counts, const int* sorted, const int* inv,
+                      int T, int E, int N, float* logits_out, float* w_out,
+                      int* ids_out, int* counts_out, int* sorted_out,
+                      int* inv_out, hipStream_t st) {
+  if (sorted_out)
+    SLLM_HIP(hipMemcpyAsync(sorted_out, sorted, (size_t)N * 4,
+                            hipMemcpyDeviceToDevice, st));
+  if (inv_out)
+    SLLM_HIP(hipMemcpyAsync(inv_out, inv, (size_t)N * 4, hipMemcpyDeviceToDevice, st));
   if (logits_out)
     SLLM_HIP(hipMemcpyAsync(logits_out, logits, (size_t)T * E * 4,
                             hipMemcpyDeviceToDevice, st));
@@ -262,7 +266,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const bool one_expert = p.decode && a->wgu_packed && E == 1 && k == 1 &&
                           a->logits_given && 1.0f + eps == 1.0f &&
                           !a->logits_out && !a->w_out && !a->ids_out &&
-                          !a->counts_out;
+                          !a->counts_out && !a->sorted_out && !a->inv_pos_out;
   // Decode-size routing: the router GEMM also computes the shared-expert
   // gate, and softmax top-k runs fused with the permutation (two launches
   // instead of four). Stages a call does not run are recorded with zero
@@ -338,7 +342,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       const long sh_rt = sh ? (T + p.bm - 1) / p.bm : 0;
       SegDesc r1{}, s1{};
       r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
-      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
       r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
       r1.N = I; r1.K = H; r1.hq = (uint8_t*)h; r1.total_rows = p.N;
       r1.ksplit = p.ks_up; r1.pp = (float*)(ws + p.gu);
@@ -361,7 +365,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
                  launch_split_finish(r1, sh ? &s1 : nullptr, 0.f, st)));
       SegDesc r2{}, s2{};
       r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
-      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
       r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
       r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
@@ -435,7 +439,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       SegDesc r1{}, s1{};
       r1.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
-      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
       r1.wp = (const uint8_t*)a->wgu_packed; r1.s0 = a->wg_s; r1.s1 = a->wu_s;
       r1.N = I; r1.K = H; r1.hq = hq; r1.hs = hs;
       s1.a = xq; s1.sa = sx; s1.total_rows = T;
@@ -447,7 +451,7 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
       SegDesc r2{}, s2{};
       r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
-      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
       r2.row_w = w; r2.row_w_by_idx = 1; r2.y = y;
       s2.a = hq_sh; s2.sa = hs_sh; s2.total_rows = T;
@@ -484,8 +488,9 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
-  return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
-                    a->ids_out, a->counts_out, st);
+  return copy_debug(logits, w, ids, counts, sorted, inv, T, E, p.N,
+                    a->logits_out, a->w_out, a->ids_out, a->counts_out,
+                    a->sorted_out, a->inv_pos_out, st);
 }
 
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
@@ -564,14 +569,14 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     const long sh_rt = (T + p.bm_sh - 1) / p.bm_sh;
     SegDesc r1{};
     r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
-    r1.tile_info = tiles; r1.num_tiles = ntiles;
+    r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
     r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
     r1.N = I; r1.K = H; r1.hq = (uint8_t*)h; r1.total_rows = p.N;
     r1.ksplit = p.ks_up; r1.pp = (float*)(ws + p.gu);
     r1.pstride = (long)p.N * I;
     SegDesc r2{};
     r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
-    r2.tile_info = tiles; r2.num_tiles = ntiles;
+    r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
     r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
     r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
@@ -662,7 +667,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       SegDesc r1{};
       r1.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r1.a = xq; r1.sa = sx; r1.sorted_idx = sorted; r1.gather = 1;
-      r1.tile_info = tiles; r1.num_tiles = ntiles;
+      r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
       r1.wp = (const uint8_t*)a->w13_packed; r1.s0 = a->w13_s_packed;
       r1.N = I; r1.K = H; r1.row_w = w; r1.row_w_by_idx = 1;
       r1.hq = hq; r1.hs = hs;
@@ -672,7 +677,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       SegDesc r2{};
       r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
-      r2.tile_info = tiles; r2.num_tiles = ntiles;
+      r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
       r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
       r2.N = H; r2.K = I; r2.y = y;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
@@ -721,8 +726,9 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
-  return copy_debug(logits, w, ids, counts, T, E, p.N, a->logits_out, a->w_out,
-                    a->ids_out, a->counts_out, st);
+  return copy_debug(logits, w, ids, counts, sorted, inv, T, E, p.N,
+                    a->logits_out, a->w_out, a->ids_out, a->counts_out,
+                    a->sorted_out, a->inv_pos_out, st);
 }
 
 }  // extern "C"

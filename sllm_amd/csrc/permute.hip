@@ -174,6 +174,8 @@ __global__ __launch_bounds__(64) void permute_scatter_kernel(
       const int pos = run[e] + rank;
       sorted_idx[pos] = a;
       inv_pos[a] = pos;
+    } else if (a < a1) {
+      inv_pos[a] = -1;  // a dropped assignment: the combine skips it
     }
     __syncthreads();  // every lane has read run[] before it advances
     if (valid && (peers >> lane) == 1ull) run[e] += __popcll(peers);
@@ -261,6 +263,8 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(
     const int pos = hist[wave][e] + __popcll(peers & ((1ull << lane) - 1ull));
     sorted_idx[pos] = a;
     inv_pos[a] = pos;
+  } else if (a < N) {
+    inv_pos[a] = -1;  // a dropped assignment: the combine skips it
   }
 }
 

@@ -126,6 +126,7 @@ __device__ __forceinline__ void permute_fused_body(
     const int raw = idv[g];
     const bool valid = raw >= 0 && raw < E;
     const int e = valid ? raw : 0;
+    if (!valid && a < a1) inv_pos[a] = -1;  // dropped: the combine skips it
     uint64_t peers = __ballot(valid);
     if (peers == 0) continue;  // an empty group (uniform across the wave)
     for (int b = 0; b < nbits; ++b) {

@@ -30,7 +30,7 @@ def fp8_gemm(A, B, scale_inv, block_h=128, block_w=128) -> np.ndarray:
     M, K = A.shape
     N = B.shape[0]
     if B.shape != (N, K):
-        raise ValueError(f"B {B.shape} must be (N,K) matching A (M,K) = {(M, K)}")
+        raise ValueError(f"fp8_gemm: weight codes {B.shape} do not have the activation's K={K} columns")
     want = (-(-N // block_h), -(-K // block_w))
     if scale_inv.shape != want:
         raise ValueError(f"scale_inv {scale_inv.shape} != {want}")

@@ -286,9 +286,17 @@ def load_deepseek_moe(ckpt: Checkpoint, prefix: str, top_k: int, n_group=1,
     (N, K/2)) with F8_E8M0 (N, K/32) scales, shared experts as F8_E4M3 with
     F8_E8M0 128x128 scales; optional `ffn.gate.bias`. A hash layer
     (hash_layer, the first n_hash_layers) also loads its token-id table."""
-    from .moe import DeepseekMoE
+    from .moe import DeepseekMoE, check_tid2eid
     g = f"{prefix}ffn.gate"
     E, H = ckpt.spec(f"{g}.weight")[1]
+    tid2eid = None
+    if hash_layer:  # checked before any weight is uploaded
+        for n in (f"{g}.tid2eid", "tid2eid"):
+            if ckpt.has(n):
+                tid2eid = check_tid2eid(np.array(ckpt.array(n)), E, top_k)
+                break
+        if tid2eid is None:
+            raise CheckpointError(f"{prefix}: hash layer without a tid2eid table")
     ep = lambda e, w: f"{prefix}ffn.experts.{e}.{w}"  # noqa: E731
     I = ckpt.spec(ep(0, "w1.weight"))[1][0]
     fp4 = ("I8", "U8")
@@ -307,14 +315,6 @@ def load_deepseek_moe(ckpt: Checkpoint, prefix: str, top_k: int, n_group=1,
                               ("w2", "s2", (H, Is))):
             b[key] = _stack(ckpt, [f"{sp}.{w}.weight"], ("F8_E4M3",), shape)
             b[key + "_s"] = to_device_raw(scale_f32(ckpt, f"{sp}.{w}.scale"))
-    tid2eid = None
-    if hash_layer:
-        for n in (f"{g}.tid2eid", "tid2eid"):
-            if ckpt.has(n):
-                tid2eid = np.array(ckpt.array(n), np.int32)
-                break
-        if tid2eid is None:
-            raise CheckpointError(f"{prefix}: hash layer without a tid2eid table")
     return DeepseekMoE.from_device(
         b, E=E, I=I, H=H, Is=Is, top_k=top_k, n_group=n_group,
         topk_group=topk_group, scoring=scoring, route_scale=route_scale,

@@ -69,7 +69,8 @@ def _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
         setattr(a, k, ptr(w.get(k)))
     a.out = ptr(out)
     debug = debug or {}
-    for k in ("logits_out", "w_out", "ids_out", "counts_out"):
+    for k in ("logits_out", "w_out", "ids_out", "counts_out", "sorted_out",
+              "inv_pos_out"):
         setattr(a, k, ptr(debug.get(k)))
     a.workspace = ptr(workspace)
     a.workspace_bytes = int(workspace_bytes or 0)
@@ -89,6 +90,13 @@ def qwen_workspace_bytes(T, H, E, I, Is, topk, mode="auto", has_shared=True,
     return int(n)
 
 
+def stream_status(stream=None) -> None:
+    """Raises RuntimeError (rc -2) if a streamed expert GEMM left work items
+    undone since the last check (synchronizes ``stream``)."""
+    _lib.check(_lib.lib().sllm_moe_stream_status(stream_handle(stream)),
+               "sllm_moe_stream_status")
+
+
 def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
                      mode="auto", out_f32=False, wdtype=0, eps=1e-20,
                      logits=None, workspace=None, workspace_bytes=None,
@@ -96,7 +104,8 @@ def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
     """One Qwen-style MoE layer on device buffers (see include/sllm_moe.h
     sllm_moe_qwen_args for shapes). `weights` maps router_w, wg, wg_s, wu,
     wu_s, wd, wd_s [, sg, sg_s, su, su_s, sd, sd_s, sgl] to device buffers;
-    `debug` may map logits_out / w_out / ids_out / counts_out."""
+    `debug` may map logits_out / w_out / ids_out / counts_out / sorted_out /
+    inv_pos_out."""
     if workspace_bytes is None:
         workspace_bytes = getattr(workspace, "nbytes", None)
         if workspace_bytes is None and hasattr(workspace, "numel"):
@@ -137,7 +146,8 @@ def _ds_args(T, H, E, I, Is, topk, mode, out_f32, n_group, topk_group,
         setattr(a, k, ptr(w.get(k)))
     a.out = ptr(out)
     debug = debug or {}
-    for k in ("logits_out", "w_out", "ids_out", "counts_out"):
+    for k in ("logits_out", "w_out", "ids_out", "counts_out", "sorted_out",
+              "inv_pos_out"):
         setattr(a, k, ptr(debug.get(k)))
     a.workspace = ptr(workspace)
     a.workspace_bytes = int(workspace_bytes or 0)
@@ -314,6 +324,7 @@ class QwenMoE:
                          wdtype=self.wdtype, eps=self.eps, logits=lg,
                          workspace=ws, debug=dbg)
         y = out.copy_host().reshape(T, self.H)
+        stream_status()
         if not return_routing:
             return y
         r = {"logits": dbg["logits_out"].copy_host().reshape(T, self.E),
@@ -321,6 +332,23 @@ class QwenMoE:
              "ids": dbg["ids_out"].copy_host_raw(np.int32, (T, self.top_k)),
              "counts": dbg["counts_out"].copy_host_raw(np.int32, (self.E,))}
         return y, r
+
+
+def check_tid2eid(table, E: int, top_k: int) -> np.ndarray:
+    """A hash layer's expert table as (vocab, top_k) int32, every entry an
+    expert id in [0, E). The reference's take_along_axis
+    (ref/deepseek_v4.py:558) raises IndexError for ids >= E; the kernels
+    would drop such slots from the output, so they are refused here."""
+    t = np.asarray(table)
+    if t.ndim != 2 or t.shape[1] != top_k or t.shape[0] < 1:
+        raise ValueError(f"tid2eid must be (vocab >= 1, top_k={top_k}), got {t.shape}")
+    if not np.issubdtype(t.dtype, np.integer):
+        raise TypeError(f"tid2eid must hold integer expert ids, got {t.dtype}")
+    bad = (t < 0) | (t >= E)
+    if bad.any():
+        r, c = np.argwhere(bad)[0]
+        raise IndexError(f"tid2eid[{r}, {c}] = {t[r, c]} is not an expert id in [0, {E})")
+    return np.ascontiguousarray(t, np.int32)
 
 
 class DeepseekMoE:
@@ -335,6 +363,8 @@ class DeepseekMoE:
         E, I = np.asarray(w1).shape[:2]
         H = np.asarray(w2).shape[1]
         Is = 0 if s1 is None else np.asarray(s1).shape[0]
+        if tid2eid is not None:  # before any upload
+            tid2eid = check_tid2eid(tid2eid, E, top_k)
         b = {"router_w": _up(to_bf16(router_w)),
              "bias": _up(np.asarray(bias, np.float32)) if bias is not None else None}
         for k, v in (("w1", w1), ("w1_s", w1_s), ("w3", w3), ("w3_s", w3_s),
@@ -380,8 +410,7 @@ class DeepseekMoE:
         self.vocab = 0
         if tid2eid is not None:
             t = np.ascontiguousarray(tid2eid, np.int32)
-            if t.ndim != 2 or t.shape[1] != self.top_k:
-                raise ValueError("tid2eid must be (vocab, top_k)")
+            check_tid2eid(t, self.E, self.top_k)
             self.vocab = t.shape[0]
             b["tid2eid"] = _up(t)
         self._w = b
@@ -419,6 +448,7 @@ class DeepseekMoE:
                              workspace=self._ws, debug=dbg, token_ids=tok,
                              vocab=self.vocab)
         y = out.copy_host().reshape(T, self.H)
+        stream_status()
         if not return_routing:
             return y
         r = {"logits": dbg["logits_out"].copy_host().reshape(T, self.E),

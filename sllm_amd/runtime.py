@@ -9,8 +9,8 @@ libsllm_moe.so.
 
 from __future__ import annotations
 
-import ctypes
-from ctypes import POINTER, c_float, c_void_p
+import weakref
+from ctypes import c_void_p
 
 import numpy as np
 
@@ -56,81 +56,99 @@ def sync() -> None:
     _lib.check(_lib.lib().sllm_sync(), "sllm_sync")
 
 
+def _byte_count(n) -> int:
+    """A strictly positive Python int (bools rejected), else ValueError."""
+    if isinstance(n, bool) or not isinstance(n, int) or n < 1:
+        raise ValueError(f"device allocation size must be an int >= 1, got {n!r}")
+    return n
+
+
+def _release(addr: int) -> None:
+    # weakref.finalize callback: runs once, at free() or at collection
+    try:
+        _lib.lib().sllm_buf_free(c_void_p(addr))
+    except Exception:
+        pass
+
+
 class DeviceBuffer:
-    """Owning device allocation (ref kernels/_sllm_cuda.py:200-258)."""
+    """Device allocation owned by a Python object.
+
+    Interface of ref kernels/_sllm_cuda.py:200-258 (``.ptr``, ``.nbytes``,
+    ``upload``, ``upload_raw``, ``copy_host``, ``free``); the allocation is
+    released by a ``weakref.finalize`` hook, so an explicit ``free()`` and
+    garbage collection share one release path and it runs exactly once.
+    """
 
     def __init__(self, nbytes: int):
-        if not isinstance(nbytes, int) or nbytes <= 0:
-            raise ValueError("nbytes must be a positive int")
-        self.nbytes = nbytes
-        self._ptr = _lib.lib().sllm_buf_new(nbytes)
-        if not self._ptr:
-            raise RuntimeError("sllm_buf_new failed: " + _lib.last_error())
-        self._closed = False
+        self.nbytes = _byte_count(nbytes)
+        addr = _lib.lib().sllm_buf_new(self.nbytes)
+        if not addr:
+            raise RuntimeError(
+                f"could not allocate {self.nbytes} device bytes ({_lib.last_error()})")
+        self._addr = int(addr)
+        self._release = weakref.finalize(self, _release, self._addr)
 
-    def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
+    @property
+    def alive(self) -> bool:
+        return self._release.alive
 
     @property
     def ptr(self) -> int:
-        if self._closed:
-            raise RuntimeError("DeviceBuffer already freed")
-        return self._ptr
+        if not self._release.alive:
+            raise RuntimeError(f"use of a released {self.nbytes}-byte device buffer")
+        return self._addr
 
     def free(self) -> None:
-        if not getattr(self, "_closed", True):
-            _lib.check(_lib.lib().sllm_buf_free(c_void_p(self._ptr)), "sllm_buf_free")
-            self._closed = True
+        """Release the device memory now (later calls are no-ops)."""
+        if self._release.alive:
+            self._release.detach()
+            _lib.check(_lib.lib().sllm_buf_free(c_void_p(self._addr)), "sllm_buf_free")
 
-    def copy_host(self) -> np.ndarray:
-        """float32 copy of the device bytes."""
-        if self.nbytes % 4:
-            raise ValueError("non-float32-sized buffer")
-        y = np.empty(self.nbytes // 4, np.float32)
-        _lib.check(_lib.lib().sllm_buf_d2h(y.ctypes.data_as(POINTER(c_float)),
-                                           c_void_p(self.ptr), self.nbytes),
-                   "sllm_buf_d2h")
-        return y
+    def _host_to_device(self, arr: np.ndarray, fn: str) -> None:
+        if arr.nbytes != self.nbytes:
+            raise ValueError(f"{fn}: host array holds {arr.nbytes} bytes, the device "
+                             f"buffer {self.nbytes}")
+        _lib.check(getattr(_lib.lib(), fn)(c_void_p(self.ptr), arr.ctypes.data_as(c_void_p),
+                                          arr.nbytes), fn)
 
     def copy_host_raw(self, dtype, shape=None) -> np.ndarray:
-        """Copy of the device bytes viewed as `dtype` (e.g. uint8, int32)."""
-        y = np.empty(self.nbytes, np.uint8)
-        _lib.check(_lib.lib().sllm_buf_d2h_raw(y.ctypes.data_as(c_void_p),
+        """The device bytes, copied to the host and viewed as ``dtype``."""
+        host = np.empty(self.nbytes, np.uint8)
+        _lib.check(_lib.lib().sllm_buf_d2h_raw(host.ctypes.data_as(c_void_p),
                                                c_void_p(self.ptr), self.nbytes),
                    "sllm_buf_d2h_raw")
-        y = y.view(dtype)
-        return y.reshape(shape) if shape is not None else y
+        host = host.view(dtype)
+        return host if shape is None else host.reshape(shape)
+
+    def copy_host(self) -> np.ndarray:
+        """The device bytes as a flat float32 array."""
+        if self.nbytes & 3:
+            raise ValueError(f"{self.nbytes} bytes is not a whole number of float32")
+        return self.copy_host_raw(np.float32)
 
     def upload(self, arr: np.ndarray) -> None:
-        arr = np.ascontiguousarray(arr, dtype=np.float32)
-        if arr.nbytes != self.nbytes:
-            raise ValueError(f"size mismatch: {arr.nbytes} != {self.nbytes}")
-        _lib.check(_lib.lib().sllm_buf_h2d(c_void_p(self.ptr),
-                                           arr.ctypes.data_as(POINTER(c_float)),
-                                           arr.nbytes), "sllm_buf_h2d")
+        """Overwrite the buffer with ``arr`` converted to float32."""
+        self._host_to_device(np.ascontiguousarray(arr, dtype=np.float32), "sllm_buf_h2d_raw")
 
     def upload_raw(self, arr: np.ndarray) -> None:
-        arr = np.ascontiguousarray(arr)
-        if arr.nbytes != self.nbytes:
-            raise ValueError(f"size mismatch: {arr.nbytes} != {self.nbytes}")
-        _lib.check(_lib.lib().sllm_buf_h2d_raw(c_void_p(self.ptr),
-                                               arr.ctypes.data_as(c_void_p),
-                                               arr.nbytes), "sllm_buf_h2d_raw")
+        """Overwrite the buffer with the bytes of ``arr`` (any dtype)."""
+        self._host_to_device(np.ascontiguousarray(arr), "sllm_buf_h2d_raw")
 
 
 class DeviceView:
-    """Non-owning byte window into a DeviceBuffer (ref :261-280)."""
+    """Window ``[off_bytes, off_bytes + nbytes)`` of a DeviceBuffer, not owning
+    it (interface of ref kernels/_sllm_cuda.py:261-280). It holds a reference
+    to the buffer, and its ``ptr`` goes through the buffer's, so a window on
+    a released buffer raises instead of yielding a stale address."""
 
     def __init__(self, base: DeviceBuffer, off_bytes: int, nbytes: int):
-        if off_bytes < 0 or nbytes < 0 or off_bytes + nbytes > base.nbytes:
-            raise ValueError("view out of range")
-        self._base = base
-        self._off = off_bytes
-        self.nbytes = nbytes
-        base.ptr
+        if not base.alive:
+            raise RuntimeError("window on a released device buffer")
+        if min(off_bytes, nbytes) < 0 or off_bytes + nbytes > base.nbytes:
+            raise ValueError(f"window [{off_bytes}, {off_bytes + nbytes}) exceeds "
+                             f"the {base.nbytes}-byte buffer")
+        self._base, self._off, self.nbytes = base, off_bytes, nbytes
 
     @property
     def ptr(self) -> int:
@@ -146,22 +164,20 @@ def to_bf16(arr: np.ndarray) -> np.ndarray:
 
 
 def to_device(arr: np.ndarray) -> DeviceBuffer:
-    """Upload a float32 array (ref :290-296)."""
-    arr = np.ascontiguousarray(arr, dtype=np.float32)
-    buf = DeviceBuffer(max(arr.nbytes, 4))
-    if arr.nbytes:
-        buf.upload(arr)
-    return buf
+    """A new device buffer holding ``arr`` as float32 (interface of ref
+    kernels/_sllm_cuda.py:290-296; an empty array gets a 4-byte buffer)."""
+    host = np.ascontiguousarray(arr, dtype=np.float32)
+    return to_device_raw(host)
 
 
 def to_device_raw(arr: np.ndarray) -> DeviceBuffer:
-    """Upload the raw bytes of any array (uint8 codes, bf16 bits, ...)."""
-    arr = np.ascontiguousarray(arr)
-    buf = DeviceBuffer(max(arr.nbytes, 4))
-    if arr.nbytes:
-        _lib.check(_lib.lib().sllm_buf_h2d_raw(c_void_p(buf.ptr),
-                                               arr.ctypes.data_as(c_void_p),
-                                               arr.nbytes), "sllm_buf_h2d_raw")
+    """A new device buffer holding the bytes of ``arr`` (uint8 codes, bf16
+    bits, ...); arrays under 4 bytes fill the front of a 4-byte buffer."""
+    host = np.ascontiguousarray(arr)
+    buf = DeviceBuffer(max(host.nbytes, 4))
+    if host.nbytes:
+        _lib.check(_lib.lib().sllm_buf_h2d_raw(c_void_p(buf.ptr), host.ctypes.data_as(c_void_p),
+                                               host.nbytes), "sllm_buf_h2d_raw")
     return buf
 
 

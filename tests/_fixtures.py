@@ -210,19 +210,41 @@ def rel_l2(got, want) -> float:
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-def certified_route_ties(ids_dev, ids_ref, p_ref) -> int:
-    """Count positions where device and oracle ids differ but the oracle's
-    fp32 probabilities of the two experts are bitwise equal (a rounding
-    tie that only the logit order can break). Raises on any other
-    mismatch."""
+def certified_tie_tokens(ids_dev, ids_ref, p_ref) -> np.ndarray:
+    """Tokens whose device and oracle ids differ only where the oracle's
+    fp32 probabilities of the two experts are bitwise equal (a rounding tie
+    of the probabilities that the device, selecting on the logits, breaks by
+    the logit order). Raises on any other mismatch. Returns the sorted token
+    indices with at least one such tie."""
     bad = np.argwhere(ids_dev != ids_ref)
-    ties = 0
+    tied = set()
     for t, j in bad:
         a, b = int(ids_dev[t, j]), int(ids_ref[t, j])
-        if p_ref[t, a] == p_ref[t, b]:
-            ties += 1
-        else:
+        if p_ref[t, a] != p_ref[t, b]:
             raise AssertionError(
                 f"routing mismatch at token {t} slot {j}: device {a} "
                 f"(p={p_ref[t, a]!r}) vs oracle {b} (p={p_ref[t, b]!r})")
-    return ties
+        tied.add(int(t))
+    return np.array(sorted(tied), np.int64)
+
+
+def certified_route_ties(ids_dev, ids_ref, p_ref) -> int:
+    """Number of mismatching (token, slot) positions that are certified
+    ties (see certified_tie_tokens); raises on any other mismatch."""
+    bad = np.argwhere(ids_dev != ids_ref)
+    certified_tie_tokens(ids_dev, ids_ref, p_ref)
+    return len(bad)
+
+
+def check_qwen_routing(logits, ids, w, k, eps=1e-20, name="routing"):
+    """Device routing (ids, w) against the oracle's moe_route of the same
+    fp32 logits: ids bit-exact except certified ties (printed), weights
+    rtol 1e-5 on every token without a tie. Returns the tied tokens."""
+    from oracle import qwen_moe as qm
+    w_ref, ids_ref = qm.moe_route(logits, k, eps)
+    tied = certified_tie_tokens(ids, ids_ref.astype(np.int32), qm.softmax_rows(logits))
+    print(f"{name}: {len(tied)} tokens with a certified probability tie")
+    keep = np.ones(len(ids), bool)
+    keep[tied] = False
+    np.testing.assert_allclose(w[keep], w_ref[keep], rtol=1e-5, atol=1e-7)
+    return tied

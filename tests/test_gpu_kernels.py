@@ -10,7 +10,7 @@ from oracle import deepseek_moe as dm
 from oracle import qwen_moe as qm
 from oracle.permute import permute as oracle_permute
 
-from tests._fixtures import certified_route_ties
+from tests._fixtures import check_qwen_routing
 
 pytestmark = pytest.mark.gpu
 
@@ -160,13 +160,13 @@ def test_route_softmax_matches_oracle(L, T, E, k):
     w, ids = empty(T * k * 4), empty(T * k * 4)
     L.check(L.lib().sllm_moe_route_softmax(dev(logits).ptr, w.ptr, ids.ptr, T, E,
                                            k, np.float32(1e-20), None))
-    wr, ir = qm.moe_route(logits, k)
-    ih = host(ids, np.int32, (T, k))
-    p = qm.softmax_rows(logits)
-    ties = certified_route_ties(ih, ir.astype(np.int32), p)
-    assert ties <= 2
-    if ties == 0:
-        np.testing.assert_allclose(host(w, np.float32, (T, k)), wr, rtol=1e-5, atol=1e-7)
+    tied = check_qwen_routing(logits, host(ids, np.int32, (T, k)),
+                              host(w, np.float32, (T, k)), k,
+                              name=f"route_softmax T={T} E={E} k={k}")
+    # rows 0 and 1 hold exact logit ties (decided by the lower id, which the
+    # oracle's stable sort matches): a certified tie needs distinct logits
+    # with equal fp32 probabilities, rare at this scale
+    assert len(tied) <= 2
 
 
 @pytest.mark.parametrize("G,kg,scoring", [(1, 1, "sigmoid"), (8, 4, "sigmoid"),

@@ -126,3 +126,29 @@ def test_scale_decoding_matches_codecs(tmp_path):
     np.testing.assert_array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
     np.testing.assert_array_equal(loader.scale_f32(ck, "bf"), codecs.decode_bf16(bits))
     np.testing.assert_array_equal(loader.scale_f32(ck, "f"), f32)
+
+
+@pytest.mark.parametrize("bad", [16, -1, 1000])
+def test_hash_table_out_of_range_is_refused(tmp_path, bad):
+    """A hash layer's tid2eid entry outside [0, E) raises before any weight
+    reaches the device (ref/deepseek_v4.py:558 raises IndexError for ids >= E;
+    the kernels would silently drop the slot)."""
+    from sllm_amd.moe import check_tid2eid
+    E, k = 16, 4
+    rng = np.random.default_rng(5)
+    t = np.stack([rng.permutation(E)[:k] for _ in range(30)]).astype(np.int32)
+    np.testing.assert_array_equal(check_tid2eid(t, E, k), t)
+    t[7, 2] = bad
+    with pytest.raises(IndexError, match=r"tid2eid\[7, 2\]"):
+        check_tid2eid(t, E, k)
+    with pytest.raises(ValueError):
+        check_tid2eid(t[:, :3], E, k)
+    # through the loader: the table is read and checked first, so a CPU-only
+    # process gets the IndexError (not a device error)
+    p = str(tmp_path / "h.safetensors")
+    H = 256
+    loader.write_safetensors(p, {
+        "ffn.gate.weight": ("F32", (E, H), np.zeros((E, H), np.float32)),
+        "ffn.gate.tid2eid": ("I32", t.shape, t)})
+    with pytest.raises(IndexError):
+        loader.load_deepseek_moe(loader.Checkpoint(p), "", top_k=k, hash_layer=True)
