@@ -317,6 +317,18 @@ typedef struct sllm_moe_qwen_args {
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
 int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): sllm_moe_qwen_forward with the library's own per-device
+ * scratch (a fixed device array of sllm_moe_qwen_forward_noalloc_max_bytes()
+ * = 32 MiB, held by every device the library runs on until the process
+ * ends) in place of a workspace; a->workspace must be NULL and
+ * a->workspace_bytes 0. Calls no hipMalloc / hipFree. A call whose
+ * workspace (sllm_moe_qwen_workspace_bytes) exceeds the scratch returns -2
+ * before any launch. Calls that overlap on one device share the scratch and
+ * race: order them on one stream (or synchronize) per device. */
+long sllm_moe_qwen_forward_noalloc_max_bytes(void);
+int sllm_moe_qwen_forward_noalloc(const sllm_moe_qwen_args* a);
 
 /* DeepSeek-style layer (ref/deepseek_v4.py:522-570 with the upstream
  * combine of ref/hf_sources/dsv4/model.py:684-699): scored routing with a

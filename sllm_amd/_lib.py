@@ -133,6 +133,8 @@ SIGNATURES = {
     "sllm_quantize_weight_mxfp4": (c_int, [P, c_int, c_int, P, P, P]),
     "sllm_moe_qwen_workspace_bytes": (c_long, [POINTER(QwenArgs)]),
     "sllm_moe_qwen_forward": (c_int, [POINTER(QwenArgs)]),
+    "sllm_moe_qwen_forward_noalloc_max_bytes": (c_long, []),
+    "sllm_moe_qwen_forward_noalloc": (c_int, [POINTER(QwenArgs)]),
     "sllm_moe_ds_workspace_bytes": (c_long, [POINTER(DeepseekArgs)]),
     "sllm_moe_ds_forward": (c_int, [POINTER(DeepseekArgs)]),
 }

@@ -15,6 +15,7 @@
 //  decode:  fp32 activations against dequantized weights in a
 //           bandwidth-bound GEMV over the touched experts only.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/sllm_moe.h"
 #include "launch.h"
@@ -175,7 +176,7 @@ static int check_common(const A* a, const char* who) {
                a->H, a->I);
   SLLM_REQUIRE((long)a->T * a->topk < (1L << 30), "%s: T*topk too large", who);
   SLLM_REQUIRE(a->mode >= 0 && a->mode <= 2, "%s: bad mode %d", who, a->mode);
-  SLLM_REQUIRE(a->x && a->out && a->workspace, "%s: null x/out/workspace", who);
+  SLLM_REQUIRE(a->x && a->out, "%s: null x/out", who);
   SLLM_REQUIRE(a->logits_given ? a->logits != nullptr : a->router_w != nullptr,
                "%s: need logits (logits_given) or router_w", who);
   return 0;
@@ -221,8 +222,15 @@ long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a) {
       .total;
 }
 
-int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
-  if (check_common(a, "sllm_moe_qwen_forward")) return -1;
+}  // extern "C"
+
+namespace sllm {
+
+// The Qwen layer on the workspace ws (ws_bytes bytes): the body of both
+// sllm_moe_qwen_forward (caller's workspace) and
+// sllm_moe_qwen_forward_noalloc (the library's per-device scratch).
+static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
+                           long ws_bytes) {
   const bool sh = a->su != nullptr;
   SLLM_REQUIRE(a->wdtype == 0 || a->wdtype == 1,
                "sllm_moe_qwen_forward: wdtype must be 0 (fp8) or 1 (bf16)");
@@ -239,11 +247,10 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   const int wf = bf16w ? 2 : 0;  // gemv weight format
   const Plan p = make_plan(T, H, E, I, Is, k, a->mode, sh, !a->logits_given,
                            bf16w);
-  SLLM_REQUIRE(a->workspace_bytes >= (long)p.total,
-               "sllm_moe_qwen_forward: workspace %ld < %zu bytes",
-               a->workspace_bytes, p.total);
+  SLLM_REQUIRE(ws_bytes >= (long)p.total,
+               "sllm_moe_qwen_forward: workspace %ld < %zu bytes", ws_bytes,
+               p.total);
   hipStream_t st = (hipStream_t)a->stream;
-  char* ws = (char*)a->workspace;
   float* logits = a->logits_given ? (float*)a->logits : (float*)(ws + p.logits);
   float* w = (float*)(ws + p.w);
   int* ids = (int*)(ws + p.ids);
@@ -493,6 +500,69 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
                     a->sorted_out, a->inv_pos_out, st);
 }
 
+// ---------------------------------------------------------------------------
+// Workspace of the no-allocation entry point: one array per device (each
+// device's code object holds its own copy at its own address), kept until
+// the process ends. Its device address comes from hipGetSymbolAddress, once
+// per device, with that device current; host code uses only that address
+// (the array's name is a host-side stand-in). Calls that overlap on one
+// device share (and race on) it. The layer writes every workspace word it
+// reads within the call, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr long SCRATCH_BYTES = 32L << 20;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static std::once_flag scratch_once[SCRATCH_MAX_DEVICES];
+static void* scratch_addr[SCRATCH_MAX_DEVICES];
+static hipError_t scratch_rc[SCRATCH_MAX_DEVICES];
+
+static int scratch_of_current_device(char** out) {
+  int dev = -1;
+  SLLM_HIP(hipGetDevice(&dev));
+  SLLM_REQUIRE(dev >= 0 && dev < SCRATCH_MAX_DEVICES,
+               "no-alloc layer: device %d beyond %d", dev, SCRATCH_MAX_DEVICES);
+  std::call_once(scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    scratch_rc[dev] = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    scratch_addr[dev] = ptr;
+  });
+  SLLM_REQUIRE(scratch_rc[dev] == hipSuccess && scratch_addr[dev] != nullptr,
+               "no-alloc layer: hipGetSymbolAddress(scratch) on device %d: %s",
+               dev, hipGetErrorString(scratch_rc[dev]));
+  *out = (char*)scratch_addr[dev];
+  return 0;
+}
+
+}  // namespace sllm
+
+extern "C" {
+
+int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
+  if (check_common(a, "sllm_moe_qwen_forward")) return -1;
+  SLLM_REQUIRE(a->workspace, "sllm_moe_qwen_forward: null workspace");
+  return qwen_forward_ws(a, (char*)a->workspace, a->workspace_bytes);
+}
+
+long sllm_moe_qwen_forward_noalloc_max_bytes(void) { return SCRATCH_BYTES; }
+
+int sllm_moe_qwen_forward_noalloc(const sllm_moe_qwen_args* a) {
+  if (check_common(a, "sllm_moe_qwen_forward_noalloc")) return -1;
+  SLLM_REQUIRE(!a->workspace && a->workspace_bytes == 0,
+               "sllm_moe_qwen_forward_noalloc: pass no workspace (the "
+               "library's per-device scratch is used)");
+  const long need = sllm_moe_qwen_workspace_bytes(a);
+  if (need < 0) return -1;
+  SLLM_CAPACITY(need <= SCRATCH_BYTES,
+                "sllm_moe_qwen_forward_noalloc: this call needs %ld workspace "
+                "bytes, above the %ld-byte scratch (T=%d H=%d E=%d I=%d k=%d "
+                "mode %d); use sllm_moe_qwen_forward with a workspace",
+                need, SCRATCH_BYTES, a->T, a->H, a->E, a->I, a->topk, a->mode);
+  char* ws = nullptr;
+  if (scratch_of_current_device(&ws)) return -1;
+  return qwen_forward_ws(a, ws, SCRATCH_BYTES);
+}
+
 long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
   if (!a || a->T <= 0 || a->E <= 0 || a->topk <= 0) {
     set_error("sllm_moe_ds_workspace_bytes: bad args");
@@ -506,6 +576,7 @@ long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
 
 int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   if (check_common(a, "sllm_moe_ds_forward")) return -1;
+  SLLM_REQUIRE(a->workspace, "sllm_moe_ds_forward: null workspace");
   SLLM_REQUIRE(!a->tid2eid || (a->token_ids && a->vocab > 0),
                "sllm_moe_ds_forward: hash routing needs token_ids and vocab");
   const bool sh = a->s1 != nullptr;

@@ -119,6 +119,24 @@ def qwen_forward_dev(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
     _lib.check(_lib.lib().sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
 
 
+def qwen_forward_noalloc(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
+                         mode="auto", out_f32=False, wdtype=0, eps=1e-20,
+                         logits=None, stream=None, debug=None) -> None:
+    """qwen_forward_dev on the library's per-device scratch instead of a
+    workspace (sllm_moe_qwen_forward_noalloc: no device allocation; calls
+    whose workspace exceeds noalloc_max_bytes() raise with rc -2; calls that
+    overlap on one device race on the scratch)."""
+    a = _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
+                   weights, out, debug, None, 0, stream)
+    _lib.check(_lib.lib().sllm_moe_qwen_forward_noalloc(a),
+               "sllm_moe_qwen_forward_noalloc")
+
+
+def noalloc_max_bytes() -> int:
+    """Size of the per-device scratch of qwen_forward_noalloc."""
+    return int(_lib.lib().sllm_moe_qwen_forward_noalloc_max_bytes())
+
+
 # ---------------------------------------------------------------------------
 # DeepSeek-style layer
 # ---------------------------------------------------------------------------
