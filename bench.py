@@ -233,7 +233,14 @@ def _stage_times(call_with_events, nstages, reps=10):
 
 
 def run_c4(args):
-    """C4 prefill: one JSON line for this configuration (not the headline)."""
+    """C4 prefill: one JSON line for this configuration."""
+    print(json.dumps(c4_result(args)), flush=True)
+    return 0
+
+
+def c4_result(args):
+    """C4 prefill (DeepSeek MXFP4) timed like the headline: layer ms and
+    tokens/s, roofline fractions, per-stage ms, touched experts."""
     import numpy as np
     from sllm_amd.moe import STAGES, deepseek_workspace_bytes
     from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
@@ -272,8 +279,9 @@ def run_c4(args):
                          "TFLOPs": round(up_flops / t_up / 1e12, 1),
                          "mfma_frac_fp8_rate": round(up_flops / t_up / (PEAK_FP8_TFLOPS * 1e12), 4)},
            "routing_us": routing_us}
-    print(json.dumps(res), flush=True)
-    return 0
+    del layer
+    sync()
+    return res
 
 
 def run_loader(args):
@@ -517,6 +525,11 @@ def c5_inputs(layer):
 
 
 def run_c5(args):
+    print(json.dumps(c5_result(args)), flush=True)
+    return 0
+
+
+def c5_result(args):
     """C5: C2 shapes at T=16384 with Zipf-skewed routing (logit bias
     -beta ln(rank_e), ranks a seeded permutation of 1..E, beta calibrated so
     the top 10% of experts take ~60% of assignments); logits are computed on
@@ -563,9 +576,11 @@ def run_c5(args):
            "layer": {"flops": flops, "bytes": bytes_,
                      "mfma_frac": round(flops / (ms / 1e3) / (PEAK_FP8_TFLOPS * 1e12), 4),
                      "hbm_frac": round(bytes_ / (ms / 1e3) / (PEAK_HBM_GBPS * 1e9), 4),
-                     "stage_ms": st, "touched_experts": touched}}
-    print(json.dumps(res), flush=True)
-    return 0
+                     "stage_ms": st, "touched_experts": touched,
+                     "empty_experts": E - touched}}
+    del layer
+    sync()
+    return res
 
 
 # --------------------------------------------------------------------------
@@ -605,7 +620,13 @@ def decode_bytes(c, B, touched):
 # --------------------------------------------------------------------------
 # CPU baseline: numpy restatement of the quantized layer, bounded sample
 # --------------------------------------------------------------------------
-def cpu_baseline(layer, x_host, ids, wts, sample_experts=64):
+def cpu_baseline(layer, x_host):
+    """The whole C2 layer on this host's cores: the numpy restatement of the
+    quantized layer in expert-grouped form (oracle act_quant, fp32 BLAS),
+    router GEMM and softmax top-k, activation quant, all routed experts with
+    their tokens, the shared expert and its gate. Weights are dequantized to
+    fp32 outside the timed region (SURVEY's plan: 6.4 GB for C2). One warm-up,
+    then the median of 3 runs; no extrapolation."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -613,13 +634,13 @@ def cpu_baseline(layer, x_host, ids, wts, sample_experts=64):
     c = layer.cfg
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     cores = len(os.sched_getaffinity(0))
-    # weights dequantized to fp32 outside the timed region
-    deq = {}
-    for e in range(sample_experts):
-        deq[e] = tuple(codecs.dequant_fp8_block(*layer.host_expert(n, e, r, cc))
-                       for n, r, cc in (("wg", I, H), ("wu", I, H), ("wd", H, I)))
+    t0 = time.perf_counter()
+    deq = [tuple(codecs.dequant_fp8_block(*layer.host_expert(n, e, r, cc))
+                 for n, r, cc in (("wg", I, H), ("wu", I, H), ("wd", H, I)))
+           for e in range(E)]
     sh = tuple(codecs.dequant_fp8_block(*layer.host_expert(n, 0, r, cc))
                for n, r, cc in (("sg", Is, H), ("su", Is, H), ("sd", H, Is)))
+    t_deq = time.perf_counter() - t0
     rw = codecs.round_bf16(layer.router_w_host)
     sgl = codecs.round_bf16(layer.sgl_host)
 
@@ -632,7 +653,6 @@ def cpu_baseline(layer, x_host, ids, wts, sample_experts=64):
 
     def run():
         t0 = time.perf_counter()
-        # full router (all tokens): logits, softmax top-k
         logits = x_host @ rw.T
         p = np.exp(logits - logits.max(-1, keepdims=True))
         p /= p.sum(-1, keepdims=True)
@@ -641,35 +661,63 @@ def cpu_baseline(layer, x_host, ids, wts, sample_experts=64):
         w /= w.sum(-1, keepdims=True) + np.float32(1e-20)
         xd = quant.act_dequant(*quant.act_quant(x_host))
         out = np.zeros((T, H), np.float32)
-        t_fixed = time.perf_counter()
-        # routed experts of the sample (using the device routing, identical)
-        for e in range(sample_experts):
-            t, j = np.nonzero(ids == e)
-            if t.size:
-                out[t] += wts[t, j][:, None] * expert(xd[t], *deq[e])
-        t_routed = time.perf_counter()
+        order = np.argsort(sel.ravel(), kind="stable")
+        bounds = np.searchsorted(sel.ravel()[order], np.arange(E + 1))
+        for e in range(E):
+            a = order[bounds[e]:bounds[e + 1]]
+            if a.size:
+                t, j = a // k, a % k
+                out[t] += w[t, j][:, None] * expert(xd[t], *deq[e])
         gate = 1.0 / (1.0 + np.exp(-(x_host @ sgl)))
         out += gate[:, None] * expert(xd, *sh)
-        t_end = time.perf_counter()
-        return (t_fixed - t0) + (t_end - t_routed), t_routed - t_fixed
+        return time.perf_counter() - t0
 
     with threadpool_limits(limits=cores):
         run()                                  # warm-up
         runs = [run() for _ in range(3)]
-    fixed = statistics.median(r[0] for r in runs)
-    routed = statistics.median(r[1] for r in runs)
-    est = fixed + routed * (E / sample_experts)
+    sec = statistics.median(runs)
     return {
-        "value": round(T / est, 2), "unit": "tokens/s", "cores": cores,
+        "value": round(T / sec, 2), "unit": "tokens/s", "cores": cores,
         "kind": "port",
-        "sample": (f"numpy restatement of the quantized C2 layer (oracle "
-                   f"act_quant + fp32 BLAS on pre-dequantized weights): router, "
-                   f"activation quant and shared expert over all {T} tokens, "
-                   f"routed experts 0-{sample_experts - 1} of {E} with all "
-                   f"their tokens, scaled x{E // sample_experts}; median of 3 "
-                   f"after a warm-up; {cores} BLAS threads"),
-        "seconds_per_layer_estimate": round(est, 3),
+        "sample": (f"the whole C2 layer ({T} tokens, all {E} experts, shared "
+                   f"expert), numpy restatement of the quantized layer (oracle "
+                   f"act_quant + fp32 BLAS on weights dequantized beforehand, "
+                   f"{t_deq:.0f} s, untimed); median of 3 after a warm-up; "
+                   f"{cores} BLAS threads"),
+        "seconds_per_layer": round(sec, 3),
+        "runs_s": [round(r, 3) for r in runs],
     }
+
+
+def cpu_c1_literal_loop():
+    """The reference's literal per-token loop (ref/qwen4_exp.py:175-179, as
+    oracle.qwen_moe.moe_block_forward) on C1: 64 tokens, H 1024, 16 experts,
+    top-4, I 512, bf16-valued fp32 weights, seed 0. Median of 3 after a
+    warm-up, single-threaded BLAS (the loop is GEMV-bound)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import codecs
+    from oracle import qwen_moe as qm
+    rng = np.random.default_rng(0)
+    T, H, E, k, I = 64, 1024, 16, 4, 512
+    bf = codecs.round_bf16
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    eg = bf((rng.standard_normal((E, I, H)) * 0.02).astype(np.float32))
+    eu = bf((rng.standard_normal((E, I, H)) * 0.02).astype(np.float32))
+    ed = bf((rng.standard_normal((E, H, I)) * 0.02).astype(np.float32))
+    times = []
+    with threadpool_limits(limits=1):
+        for it in range(4):
+            t0 = time.perf_counter()
+            qm.moe_block_forward(x, rw, eg, eu, ed, None, None, None, None, k)
+            if it:
+                times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    return {"config": "C1 (64 tokens, H 1024, E 16, top-4, I 512, bf16 weights)",
+            "ms": round(ms, 2), "tokens_per_s": round(T / (ms / 1e3), 1),
+            "cores": 1, "note": "median of 3 after a warm-up"}
 
 
 # --------------------------------------------------------------------------
@@ -681,6 +729,8 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-iters", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="leave the C4 and C5 legs out of the default line")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", choices=("c2", "c4", "c5"), default="c2",
                     help="c2 (default): the headline line; c4 / c5: one line "
@@ -794,10 +844,25 @@ def main(argv=None) -> int:
         "touched_experts": touched,
     }
 
+    # ---- the same layer with L2 and MALL flushed before every call -------
+    flush = DeviceBuffer(512 << 20)
+    fl = []
+    a0, a1 = Event(), Event()
+    for it in range(13):
+        memset(flush, it & 0xFF, flush.nbytes)
+        a0.record()
+        layer_call(layer, x, out, ws, T, "prefill")
+        a1.record()
+        a1.synchronize()
+        if it >= 3:
+            fl.append(a0.elapsed_ms(a1))
+    layer_info["ms_flushed"] = round(statistics.median(fl), 4)
+    layer_info["flush"] = "512 MiB fill before each of 10 timed calls (median)"
+    log(f"prefill with caches flushed: {layer_info['ms_flushed']} ms")
+
     # ---- decode batches (C3) -------------------------------------------
     decode = {}
     if not args.no_decode:
-        flush = DeviceBuffer(512 << 20)
         for B in (1, 8, 32, 64):
             xb_host = to_bf16_values(layer.rng.standard_normal((B, H)).astype(np.float32))
             xb = to_device_raw(to_bf16(xb_host))
@@ -837,13 +902,28 @@ def main(argv=None) -> int:
                 f"{decode[str(B)]['GBps']} GB/s")
 
     # ---- CPU baseline -----------------------------------------------------
-    cpu = None
+    cpu = c1_loop = None
     if not args.no_cpu:
-        ids = dbg["ids_out"].copy_host_raw(np.int32, (T, k))
-        wts = dbg["w_out"].copy_host().reshape(T, k)
         tc = time.perf_counter()
-        cpu = cpu_baseline(layer, x_host, ids, wts)
+        cpu = cpu_baseline(layer, x_host)
         log(f"cpu baseline {cpu['value']} tok/s ({time.perf_counter() - tc:.1f}s)")
+        c1_loop = cpu_c1_literal_loop()
+        log(f"cpu C1 literal loop {c1_loop['ms']} ms")
+
+    # ---- C4 and C5 (their own layers; the C2 layer is freed first) --------
+    extra = {}
+    if not args.no_extra_configs:
+        del layer, x, out, ws, dbg
+        sync()
+        for name, fn in (("c4", c4_result), ("c5", c5_result)):
+            r = fn(args)
+            extra[name] = {"ms": r["ms_per_step"], "tokens_per_s": r["value"],
+                           "config": r["config"], "layer": r["layer"]}
+            if "expert_up" in r:
+                extra[name]["expert_up"] = r["expert_up"]
+            if "routing_us" in r:
+                extra[name]["routing_us"] = r["routing_us"]
+            log(f"{name}: {r['ms_per_step']} ms, {r['value']} tok/s")
 
     res = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s",
@@ -866,6 +946,8 @@ def main(argv=None) -> int:
         "decode": decode,
         "decode_us_at_32": decode.get("32", {}).get("us"),
         "cpu_baseline": cpu,
+        "cpu_c1_literal_loop": c1_loop,
+        **extra,
     }
     print(json.dumps(res), flush=True)
     return 0
