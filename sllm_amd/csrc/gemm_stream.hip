@@ -150,10 +150,11 @@ __device__ __forceinline__ uint4 ld_stream(const void* p) {
   }
 }
 
-// Set (to 1) by a streamed launch whose workgroup was dealt more than
-// ST_MAX_ITEMS items, which it then leaves undone: the host sizes the grid
-// from a bound of the item count, so this marks a host sizing error. One
-// word per device (zero at load); sllm_moe_stream_status reads and clears it.
+// Set (to 1) by a decode streamed launch whose workgroup was dealt more
+// than ST_MAX_ITEMS items, which it then leaves undone: the host sizes the
+// grid from a bound of the item count, so this marks a host sizing error
+// (the prefill kernel takes any item count, in chunks). One word per device
+// (zero at load); sllm_moe_stream_status reads and clears it.
 __device__ int stream_item_overflow;
 
 template <int MODE>
@@ -252,13 +253,13 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
   const int xbeg = (int)((long)total * xcd / 8);
   const int xend = (int)((long)total * (xcd + 1) / 8);
-  const int nitems = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
-  if (nitems > ST_MAX_ITEMS) {  // host sizes the grid: a sizing error
-    if (tid == 0) stream_item_overflow = 1;
-    return;
-  }
-  if (nitems == 0) return;
-  auto item_at = [&](int m) { return xbeg + jx + m * nx; };
+  const int nall = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
+  // The items are taken ST_MAX_ITEMS at a time (the LDS holds the row
+  // indices and weights of that many): one pipeline per chunk, so that the
+  // grid stays at one workgroup per CU whatever the item count.
+  for (int cbase = 0; cbase < nall; cbase += ST_MAX_ITEMS) {
+  const int nitems = min(ST_MAX_ITEMS, nall - cbase);
+  auto item_at = [&](int m) { return xbeg + jx + (cbase + m) * nx; };
 
   // ---- phase 0: descriptors and gathered row indices -> LDS ---------------
   if (tid < nitems) {
@@ -657,6 +658,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   if (st < total_steps) step(st, 0, a0, a3, b0, b3);
   if (st + 1 < total_steps) step(st + 1, 1, a1, a0, b1, b0);
   if (st + 2 < total_steps) step(st + 2, 2, a2, a1, b2, b1);
+  __syncthreads();  // the next chunk restages desc / rsrc / rwl
+  }  // chunks
 }
 
 // ---------------------------------------------------------------------------
@@ -1197,7 +1200,9 @@ static int go_stream(const SegDesc& s0, const SegDesc* s1, int topk,
                                     upper_items, "stream gemm");
     if (rc) return rc;
   }
-  const long grid = stream_grid(upper_items, num_cus(), ST_MAX_ITEMS);
+  // one workgroup per CU: a workgroup with more than ST_MAX_ITEMS items
+  // takes them in chunks
+  const long grid = stream_grid(upper_items, num_cus(), 1 << 30);
   SLLM_REQUIRE(grid < (1L << 31), "stream gemm: grid too large");
   SegDesc dummy = s0;
   const SegDesc& b = s1 ? *s1 : dummy;
