@@ -757,7 +757,7 @@ def main(argv=None) -> int:
     import numpy as np
 
     from sllm_amd import _lib
-    from sllm_amd.moe import STAGES, qwen_workspace_bytes
+    from sllm_amd.moe import STAGES, LayerGraph, qwen_workspace_bytes
     from sllm_amd.runtime import (DeviceBuffer, Event, memset, sync, to_bf16,
                                   to_device_raw)
     if not _lib.available():
@@ -882,9 +882,24 @@ def main(argv=None) -> int:
                 a1.synchronize()
                 if it >= 3:
                     times.append(a0.elapsed_ms(a1) * 1e3)
-            us = statistics.median(times)
+            us_eager = statistics.median(times)
+            # the same call captured once as a HIP graph, replayed
+            g = LayerGraph(xb, ob, layer.w, T=B, H=H, E=E, I=I, Is=Is, topk=k,
+                           mode="decode", out_f32=False, workspace=wsb)
+            gt = []
+            for it in range(args.decode_iters + 3):
+                memset(flush, it & 0xFF, flush.nbytes)
+                a0.record()
+                g.launch()
+                a1.record()
+                a1.synchronize()
+                if it >= 3:
+                    gt.append(a0.elapsed_ms(a1) * 1e3)
+            g.free()
+            us = statistics.median(gt)
             nb = decode_bytes(c, B, tb)
-            decode[str(B)] = {"us": round(us, 2), "touched_experts": tb,
+            decode[str(B)] = {"us": round(us, 2), "us_eager": round(us_eager, 2),
+                              "touched_experts": tb,
                               "bytes": nb, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
                               "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
             if B == 32:  # per-stage breakdown (flushed like the timed calls)
@@ -898,7 +913,7 @@ def main(argv=None) -> int:
                         per[s_].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3)
                 decode[str(B)]["stage_us"] = {s_: round(statistics.median(v), 2)
                                               for s_, v in per.items()}
-            log(f"decode B={B}: {us:.1f} us, touched {tb}, "
+            log(f"decode B={B}: {us:.1f} us graph, {us_eager:.1f} us eager, touched {tb}, "
                 f"{decode[str(B)]['GBps']} GB/s")
 
     # ---- CPU baseline -----------------------------------------------------

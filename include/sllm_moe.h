@@ -317,6 +317,17 @@ typedef struct sllm_moe_qwen_args {
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);
 int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a);
+/* One layer call captured as a HIP graph and replayed (new; replaces the
+ * 3k+5 launches and host round trips per layer and token of
+ * kernels/q4_device_decode.py:316-339 for decode loops): the graph holds
+ * every pointer and size of *a (x, out, workspace, weights; stream
+ * ignored), so each replay runs the layer on the current contents of those
+ * buffers. For decode batches the layer's launches dominate its time.
+ * graph_new returns NULL on error (message in sllm_moe_last_error); stage
+ * events cannot be captured. Launch orders a replay on `stream`. */
+void* sllm_moe_qwen_graph_new(const sllm_moe_qwen_args* a);
+int sllm_moe_graph_launch(void* graph, void* stream);
+int sllm_moe_graph_free(void* graph);
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): sllm_moe_qwen_forward with the library's own per-device

@@ -133,6 +133,9 @@ SIGNATURES = {
     "sllm_quantize_weight_mxfp4": (c_int, [P, c_int, c_int, P, P, P]),
     "sllm_moe_qwen_workspace_bytes": (c_long, [POINTER(QwenArgs)]),
     "sllm_moe_qwen_forward": (c_int, [POINTER(QwenArgs)]),
+    "sllm_moe_qwen_graph_new": (c_void_p, [POINTER(QwenArgs)]),
+    "sllm_moe_graph_launch": (c_int, [P, P]),
+    "sllm_moe_graph_free": (c_int, [P]),
     "sllm_moe_qwen_forward_noalloc_max_bytes": (c_long, []),
     "sllm_moe_qwen_forward_noalloc": (c_int, [POINTER(QwenArgs)]),
     "sllm_moe_ds_workspace_bytes": (c_long, [POINTER(DeepseekArgs)]),

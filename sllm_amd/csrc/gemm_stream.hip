@@ -724,9 +724,99 @@ __device__ __forceinline__ float e8m0_f32(uint32_t b) {
 
 // BM: rows per tile, 16 or 32 (RB = BM / 16 row blocks; each weight
 // fragment feeds one MFMA per row block).
+// Device-scope accesses of the fused gate/up finish's chunk sums (buffer
+// instructions with the sc1 cache policy): stores write through the XCD's
+// L2 to the device's coherence point and loads do not take a line from the
+// reading XCD's L2, so the sums cross XCDs without the whole-L2 write-back
+// and invalidate of device-scope fences (a fence pair per workgroup made a
+// B=32 layer 1.3x slower). `base` must be the same in every lane of the
+// wave.
+constexpr int CP_SC1 = 16;  // buffer cache policy bit of device scope
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float* base) {
+  const uint64_t a = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(((uint64_t)hi << 32) | lo), 0, 0x7FFFFFF0, 0x00020000);
+}
+
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, long off,
+                                        float a, float b, float c, float d) {
+  const v4uv v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c),
+                  __float_as_uint(d)};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(off * 4), 0, CP_SC1);
+}
+
+__device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, long off) {
+  const v4uv v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off * 4), 0, CP_SC1);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
+                     __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
+// Fused finish of a K-split gate/up decode launch (DecFuse, launch.h), run
+// by every workgroup after its last item. Its chunk sums were stored at
+// device scope; each thread waits for its own stores to complete (vmcnt 0:
+// written through to the coherence point) before the barrier, after which
+// one thread per item counts the arrival of its chunk. The workgroup that
+// brings an item's count to ksplit reads the item's chunk sums at device
+// scope and computes h as split_finish_kernel does (chunks added in order,
+// then the clamps and SiLU). An item's sums are read only there, so no XCD
+// holds an older copy of them from this launch; earlier launches' copies
+// are gone with the L2 invalidation at every launch's start.
+template <int BM>
+__device__ __forceinline__ void dec_fused_finish(
+    const SegDesc& S0, const SegDesc& S1, float limit, const DecFuse& F,
+    const int4* desc, int nitems, int* jobs, int& njob) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores done
+  if (tid == 0) njob = 0;
+  __syncthreads();
+  for (int i = tid; i < nitems; i += ST_THREADS) {
+    const int4 d = desc[i];
+    const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF;
+    const SegDesc& S = seg ? S1 : S0;
+    if (S.ksplit <= 1) continue;  // finished in the item's epilogue
+    int* c = F.cnt + (seg ? F.cnt1 : 0) + (long)d.z * (S.N / 128) + nt;
+    if (atomicAdd(c, 1) == S.ksplit - 1) jobs[atomicAdd(&njob, 1)] = i;
+  }
+  __syncthreads();
+  const int nj = njob;
+  // a wave per finished item: its rows x 128 columns, four columns per lane
+  for (int j = wave; j < nj; j += ST_THREADS / 64) {
+    const int4 d = desc[__builtin_amdgcn_readfirstlane(jobs[j])];
+    const int nt = (d.x >> 1) & 0x7FFF;
+    const SegDesc& S = (d.x & 1) ? S1 : S0;
+    const __amdgpu_buffer_rsrc_t rp = dev_rsrc(S.pp);
+    const int ks = S.ksplit;
+    for (int q = lane; q < d.w * 32; q += 64) {
+      const int row = q / 32, c4 = q % 32;
+      const long o = (long)(d.z + row) * S.N + nt * 128 + c4 * 4;
+      float gs[4] = {0.f, 0.f, 0.f, 0.f}, us[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < ks; ++k) {
+        const float4 g = ld_dev4(rp, k * S.pstride + o);
+        const float4 u = ld_dev4(rp, (ks + k) * S.pstride + o);
+        gs[0] += g.x; gs[1] += g.y; gs[2] += g.z; gs[3] += g.w;
+        us[0] += u.x; us[1] += u.y; us[2] += u.z; us[3] += u.w;
+      }
+      float h[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float gv = gs[v], uv = us[v];
+        if (limit > 0.f) {
+          uv = fminf(fmaxf(uv, -limit), limit);
+          gv = fminf(gv, limit);
+        }
+        h[v] = silu_f32(gv) * uv;
+      }
+      *(float4*)((float*)S.hq + o) = make_float4(h[0], h[1], h[2], h[3]);
+    }
+  }
+}
+
 template <int BF, int MODE, bool WNT, int BM>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
-    SegDesc S0, SegDesc S1, int nseg, int topk, float limit) {
+    SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F) {
   constexpr int RB = BM / 16;
   static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
@@ -918,12 +1008,20 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       if (row >= d.w) continue;  // K chunk kc's slice (kc = 0 unsplit)
       const float rw = rwl[i][row];
       if constexpr (MODE == 0) {
-        if (S.ksplit > 1) {  // chunk sums; launch_split_finish applies SwiGLU
-          float* pg = S.pp + kc * S.pstride + (size_t)(d.z + row) * S.N +
-                      nt * 128 + wave * 16 + lg * 4;
-          *(float4*)pg = make_float4(acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
-          *(float4*)(pg + S.ksplit * S.pstride) =
-              make_float4(acc[r][1][0], acc[r][1][1], acc[r][1][2], acc[r][1][3]);
+        if (S.ksplit > 1) {  // chunk sums; SwiGLU in the finish
+          const long og = kc * S.pstride + (long)(d.z + row) * S.N +
+                          nt * 128 + wave * 16 + lg * 4;
+          float* pg = S.pp + og;
+          float* pu = pg + S.ksplit * S.pstride;
+          if (F.cnt) {
+            const __amdgpu_buffer_rsrc_t rp = dev_rsrc(S.pp);
+            st_dev4(rp, og, acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
+            st_dev4(rp, og + S.ksplit * S.pstride, acc[r][1][0], acc[r][1][1],
+                    acc[r][1][2], acc[r][1][3]);
+          } else {
+            *(float4*)pg = make_float4(acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
+            *(float4*)pu = make_float4(acc[r][1][0], acc[r][1][1], acc[r][1][2], acc[r][1][3]);
+          }
           continue;
         }
         float h[4];
@@ -1040,6 +1138,13 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   if (st < total_steps) step(st, a0, a3, b0, b3);
   if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
   if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+  if constexpr (MODE == 0) {
+    if (F.cnt) {
+      __shared__ int jobs[ST_MAX_ITEMS];
+      __shared__ int njob;
+      dec_fused_finish<BM>(S0, S1, limit, F, desc, nitems, jobs, njob);
+    }
+  }
 }
 
 static int num_cus() {
@@ -1258,7 +1363,8 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 
 template <int BF, int MODE, int BM>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
-                         float limit, long upper_items, hipStream_t st) {
+                         float limit, long upper_items, hipStream_t st,
+                         const DecFuse& fuse) {
   {
     const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, BM,
                                     upper_items, "stream decode gemm");
@@ -1268,14 +1374,15 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit);
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse);
   SLLM_LAUNCHED();
   return 0;
 }
 
 int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
-                      long upper_items, hipStream_t st, int bm) {
+                      long upper_items, hipStream_t st, int bm,
+                      const DecFuse* fuse_in) {
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
                    (bm == 16 || bm == 32),
                "stream decode gemm: bad format or tile rows %d", bm);
@@ -1304,9 +1411,21 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
   }
   const SegDesc& s0 = seg[0];
   const SegDesc* s1 = s1_in ? &seg[1] : nullptr;
+  DecFuse fuse{};
+  if (fuse_in && fuse_in->cnt) {
+    fuse = *fuse_in;
+    SLLM_REQUIRE(mode == 0, "stream decode gemm: only gate/up launches fuse");
+    SLLM_REQUIRE(!s1 || fuse.cnt1 > 0, "stream decode gemm: no second counter range");
+    for (int i = 0; i < (s1 ? 2 : 1); ++i)
+      SLLM_REQUIRE(seg[i].ksplit == 1 ||
+                       (seg[i].hq && seg[i].pp && (seg[i].tile_info || i == 1) &&
+                        2L * seg[i].ksplit * seg[i].pstride < (1L << 29)),
+                   "stream decode gemm: a fused finish needs h, chunk slices "
+                   "under 2 GiB, and tile rows for the routed segment");
+  }
 #define GO(B, M)                                                         \
-  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st) \
-                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st)
+  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse) \
+                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse)
   if (mode == 0) {
     if (bf == SF_FP4) GO(SF_FP4, 0);
     GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales

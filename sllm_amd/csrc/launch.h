@@ -31,12 +31,15 @@ int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
                              const uint16_t* sgl, float* gate_out,
                              hipStream_t st, int ks = 1);
 bool route_permute_small_fits(int T, int E, int topk);
+// zero / nzero (both permutation launches, one-workgroup path only): ints
+// to clear on the way, the counters of the fused decode launches after it.
 int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int E, int topk, float eps, int bm,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
                                int max_tiles, hipStream_t st, int ks = 1,
-                               float* gate = nullptr);
+                               float* gate = nullptr, int* zero = nullptr,
+                               int nzero = 0);
 int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,
@@ -54,7 +57,8 @@ size_t permute_scratch_bytes(int N, int E);
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,
                    int* tile_info, int* num_tiles, int max_tiles,
-                   void* scratch, hipStream_t st, bool hist_ready = false);
+                   void* scratch, hipStream_t st, bool hist_ready = false,
+                   int* zero = nullptr, int nzero = 0);
 int launch_act_quant(const uint16_t* x, int T, int H, int pow2, uint8_t* q,
                      float* s, const uint16_t* gate_w, float* gate_out,
                      hipStream_t st);
@@ -151,9 +155,26 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 // writes fp32 h rows to hq (as float*); mode 1 reads fp32 h rows (a as
 // float*, split into bf16 hi + lo) and writes fp32 rows to y (as float*).
 // bf: 0 / 1 fp8 (block scales applied in fp32), 2 MXFP4.
+//
+// A mode-0 decode launch may also finish its K-split items itself
+// (DecFuse.cnt non-null): every workgroup, after its last item, counts its
+// items' arrivals in cnt (zeroed earlier on the same stream) at
+// cnt[row_begin (N / 128) + slab] (the second segment's from cnt1 on), and
+// the workgroup whose arrival completes an item's K chunks computes its
+// SwiGLU of the chunk sums as launch_split_finish does -- same arithmetic
+// in the same order, so h equals that launch's bit for bit.
+struct DecFuse {
+  int* cnt;
+  long cnt1;
+};
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
-                      hipStream_t st, int bm = 16);
+                      hipStream_t st, int bm = 16,
+                      const DecFuse* fuse = nullptr);
+// Counter ints of a fused gate/up launch: N routed rows, T shared rows.
+inline long dec_fuse_counters(long N, long T, int I, int Is) {
+  return N * (I / 128) + T * (Is / 128);
+}
 // K chunks for a decode launch whose item count is at most upper_items
 // over KB 128-wide K steps: down launches (dec_ksplit) and gate/up launches
 // (dec_ksplit_up, which needs a finish launch and so splits only launches

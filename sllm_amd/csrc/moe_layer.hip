@@ -24,6 +24,7 @@ namespace sllm {
 
 constexpr int PREFILL_BM = 128;
 constexpr int DECODE_MAX_T = 64;
+constexpr int DEC_FUSE_MAX_T = 4;  // decode batches whose gate/up finishes in-launch
 
 struct Plan {
   bool decode;
@@ -35,6 +36,7 @@ struct Plan {
   int ks_up, ks_up_sh, ks_dn, ks_dn_sh, ks_r;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
+  size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters
   size_t total;
 };
 
@@ -125,6 +127,8 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.gu = p.ks_up > 1 ? take(c, (size_t)2 * p.ks_up * p.N * I * 4) : 0;
     p.gu_sh = has_shared && p.ks_up_sh > 1
                   ? take(c, (size_t)2 * p.ks_up_sh * T * Is * 4) : 0;
+    if (!deepseek && !force_gemv && T <= DEC_FUSE_MAX_T)
+      p.fcnt = take(c, (size_t)dec_fuse_counters(p.N, T, I, has_shared ? Is : 0) * 4);
   } else {
     p.xq = take(c, (size_t)T * H);
     p.sx = take(c, (size_t)T * (H / 128) * 4);
@@ -278,6 +282,17 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   // gate, and softmax top-k runs fused with the permutation (two launches
   // instead of four). Stages a call does not run are recorded with zero
   // length, so every stage's events exist on every call.
+  // Streamed decode of a routed layer at a few tokens: the gate/up launch
+  // finishes its K-split items itself (DecFuse) on counters the
+  // permutation launch clears, which saves the finish launch (B=1: 44 ->
+  // 42 us). From B=8 on the separate finish launch is as fast, and a fused
+  // combine in the down launch was slower at every batch size (its units
+  // complete together at the launch's end).
+  const bool fused = p.decode && a->wgu_packed && !one_expert && !bf16w &&
+                     T <= DEC_FUSE_MAX_T && (p.ks_up > 1 || p.ks_up_sh > 1);
+  int* fcnt = fused ? (int*)(ws + p.fcnt) : nullptr;
+  const long nfcnt = fused ? dec_fuse_counters(p.N, T, I, sh ? Is : 0) : 0;
+  SLLM_REQUIRE(nfcnt < (1L << 31), "sllm_moe_qwen_forward: too many counters");
   const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool small_route = p.decode && route_permute_small_fits(T, E, k);
   bool gate_done = false;
@@ -318,7 +333,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
                                      ntiles, p.max_tiles, st, p.ks_r,
-                                     gate_fin));
+                                     gate_fin, fcnt, (int)nfcnt));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
@@ -327,7 +342,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st,
-                         route_hist));
+                         route_hist, fcnt, (int)nfcnt));
   }
 
   if (p.decode) {
@@ -363,12 +378,13 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
       s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
       s1.pstride = (long)T * Is;
+      const DecFuse f_up{fcnt, (long)p.N * (I / 128)};
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k, 0.f,
                               (long)p.max_tiles * (I / 128) * p.ks_up +
                                   sh_rt * (Is / 128) * p.ks_up_sh,
-                              st, p.bm) ||
-                (p.ks_up > 1 &&
+                              st, p.bm, fused ? &f_up : nullptr) ||
+                (!fused && p.ks_up > 1 &&
                  launch_split_finish(r1, sh ? &s1 : nullptr, 0.f, st)));
       SegDesc r2{}, s2{};
       r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
@@ -542,6 +558,72 @@ int sllm_moe_qwen_forward(const sllm_moe_qwen_args* a) {
   if (check_common(a, "sllm_moe_qwen_forward")) return -1;
   SLLM_REQUIRE(a->workspace, "sllm_moe_qwen_forward: null workspace");
   return qwen_forward_ws(a, (char*)a->workspace, a->workspace_bytes);
+}
+
+// ---- graphs of one layer call (decode loops: fixed buffers, many calls) ----
+struct LayerGraph {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+void* sllm_moe_qwen_graph_new(const sllm_moe_qwen_args* a) {
+  if (check_common(a, "sllm_moe_qwen_graph_new")) return nullptr;
+  if (a->stage_events) {
+    set_error("sllm_moe_qwen_graph_new: stage events cannot be captured");
+    return nullptr;
+  }
+  hipStream_t cs = nullptr;
+  if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
+    set_error("sllm_moe_qwen_graph_new: hipStreamCreateWithFlags failed");
+    return nullptr;
+  }
+  sllm_moe_qwen_args c = *a;
+  c.stream = cs;
+  LayerGraph* g = new LayerGraph{nullptr, nullptr};
+  int rc = 0;
+  hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed);
+  if (e == hipSuccess) {
+    rc = sllm_moe_qwen_forward(&c);
+    hipError_t e2 = hipStreamEndCapture(cs, &g->graph);  // ends it on error too
+    if (rc == 0 && e2 != hipSuccess) {
+      set_error("sllm_moe_qwen_graph_new: hipStreamEndCapture: %s",
+                hipGetErrorString(e2));
+      rc = -1;
+    }
+    if (rc == 0 && hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0) !=
+                       hipSuccess) {
+      set_error("sllm_moe_qwen_graph_new: hipGraphInstantiate failed");
+      rc = -1;
+    }
+  } else {
+    set_error("sllm_moe_qwen_graph_new: hipStreamBeginCapture: %s",
+              hipGetErrorString(e));
+    rc = -1;
+  }
+  (void)hipStreamDestroy(cs);
+  if (rc) {
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+    return nullptr;
+  }
+  return g;
+}
+
+int sllm_moe_graph_launch(void* graph, void* stream) {
+  SLLM_REQUIRE(graph, "sllm_moe_graph_launch: null graph");
+  SLLM_HIP(hipGraphLaunch(((LayerGraph*)graph)->exec, (hipStream_t)stream));
+  return 0;
+}
+
+int sllm_moe_graph_free(void* graph) {
+  if (!graph) return 0;
+  LayerGraph* g = (LayerGraph*)graph;
+  const hipError_t e1 = hipGraphExecDestroy(g->exec);
+  const hipError_t e2 = hipGraphDestroy(g->graph);
+  delete g;
+  SLLM_REQUIRE(e1 == hipSuccess && e2 == hipSuccess, "sllm_moe_graph_free failed");
+  return 0;
 }
 
 long sllm_moe_qwen_forward_noalloc_max_bytes(void) { return SCRATCH_BYTES; }

@@ -272,11 +272,13 @@ __global__ __launch_bounds__(1024) void permute_fused_kernel(
     const int* __restrict__ ids, int N, int E, int nbits, int bm,
     int* __restrict__ counts, int* __restrict__ offsets,
     int* __restrict__ sorted_idx, int* __restrict__ inv_pos,
-    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles) {
+    int* __restrict__ tile_info, int* __restrict__ num_tiles, int max_tiles,
+    int* __restrict__ zero, int nzero) {
   __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
   __shared__ int sh[1024];
   permute_fused_body(ids, N, E, nbits, bm, counts, offsets, sorted_idx,
-                     inv_pos, tile_info, num_tiles, max_tiles, hist, sh);
+                     inv_pos, tile_info, num_tiles, max_tiles, hist, sh, zero,
+                     nzero);
 }
 
 bool permute_uses_chunk_hist(int N, int E) {
@@ -293,10 +295,13 @@ size_t permute_scratch_bytes(int N, int E) {
 int launch_permute(const int* ids, int N, int E, int bm, int* counts,
                    int* offsets, int* sorted_idx, int* inv_pos,
                    int* tile_info, int* num_tiles, int max_tiles,
-                   void* scratch, hipStream_t st, bool hist_ready) {
+                   void* scratch, hipStream_t st, bool hist_ready,
+                   int* zero, int nzero) {
   SLLM_REQUIRE(ids && counts && offsets && sorted_idx && inv_pos &&
                    tile_info && num_tiles && scratch,
                "permute: null pointer");
+  SLLM_REQUIRE(nzero == 0 || (zero && nzero > 0 && !permute_uses_chunk_hist(N, E)),
+               "permute: zeroing needs the one-workgroup permutation");
   SLLM_REQUIRE(N > 0 && E > 0 && E <= 4096 && bm > 0,
                "permute: bad sizes (N=%d E=%d bm=%d)", N, E, bm);
   const int nchunks = (N + PERM_CHUNK - 1) / PERM_CHUNK;
@@ -305,7 +310,8 @@ int launch_permute(const int* ids, int N, int E, int bm, int* counts,
   if (!permute_uses_chunk_hist(N, E)) {
     permute_fused_kernel<<<1, 1024, 0, st>>>(ids, N, E, nbits, bm, counts,
                                              offsets, sorted_idx, inv_pos,
-                                             tile_info, num_tiles, max_tiles);
+                                             tile_info, num_tiles, max_tiles,
+                                             zero, nzero);
     SLLM_LAUNCHED();
     return 0;
   }

@@ -65,8 +65,10 @@ __device__ __forceinline__ void permute_fused_body(
     int* __restrict__ offsets, int* __restrict__ sorted_idx,
     int* __restrict__ inv_pos, int* __restrict__ tile_info,
     int* __restrict__ num_tiles, int max_tiles,
-    int (*hist)[PERM_FUSED_MAX_E], int* sh) {
+    int (*hist)[PERM_FUSED_MAX_E], int* sh, int* __restrict__ zero = nullptr,
+    int nzero = 0) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < nzero; i += 1024) zero[i] = 0;
   const int R = ((N + PERM_FUSED_WAVES - 1) / PERM_FUSED_WAVES + 63) & ~63;
   const int a0 = min(N, wave * R), a1 = min(N, a0 + R);
   int idv[PERM_FUSED_G];

@@ -452,7 +452,7 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
     int* __restrict__ offsets, int* __restrict__ sorted_idx,
     int* __restrict__ inv_pos, int* __restrict__ tile_info,
     int* __restrict__ num_tiles, int max_tiles, int ks,
-    float* __restrict__ gate) {
+    float* __restrict__ gate, int* __restrict__ zero, int nzero) {
   __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
   __shared__ int sh[1024];
   __shared__ int ids_lds[PERM_FUSED_MAX_N];
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
   __syncthreads();
   permute_fused_body(ids_lds, T * topk, E, nbits, bm, counts, offsets,
                      sorted_idx, inv_pos, tile_info, num_tiles, max_tiles,
-                     hist, sh);
+                     hist, sh, zero, nzero);
 }
 
 // --------------------------------------------------------------------------
@@ -725,9 +725,10 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
                                int max_tiles, hipStream_t st, int ks,
-                               float* gate) {
+                               float* gate, int* zero, int nzero) {
   SLLM_REQUIRE(ks >= 1 && (!gate || ks > 1),
                "route_permute_small: bad logit slices %d", ks);
+  SLLM_REQUIRE(nzero == 0 || (zero && nzero > 0), "route_permute_small: bad zero range");
   SLLM_REQUIRE(logits && w && ids && route_permute_small_fits(T, E, topk) &&
                    topk > 0 && topk <= E && topk <= 64 && T > 0,
                "route_permute_small: bad sizes (T=%d E=%d k=%d)", T, E, topk);
@@ -738,7 +739,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
   case n:                                                                     \
     route_permute_small_kernel<n><<<1, 1024, 0, st>>>(                        \
         (float*)logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,  \
-        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks, gate);      \
+        sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks, gate,      \
+        zero, nzero);                                                         \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16)
 #undef CASE

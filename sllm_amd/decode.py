@@ -18,8 +18,10 @@ launches (gate/up, down, slice sum) over the rows in token order.
 
 Both keep their staging buffers, workspace and argument blocks between
 calls, so a decode step allocates nothing after its first call at a given
-batch size. `moe_dev` / `forward_dev` take device buffers for callers that
-keep the hidden state on the device.
+batch size; the host-array calls also capture each (layer, batch size)
+layer call as a HIP graph on first use and replay it afterwards (one launch
+instead of the layer's kernel launches). `moe_dev` / `forward_dev` take
+device buffers for callers that keep the hidden state on the device.
 
 Weights come from the reference's float weight dict (the names of
 Q4DeviceWeightTable, q4_device_decode.py:112-122, and of the hybrid table's
@@ -35,7 +37,7 @@ from ctypes import c_float, c_void_p
 import numpy as np
 
 from . import _lib
-from .moe import QwenMoE, _qwen_args, qwen_workspace_bytes
+from .moe import QwenMoE, _graph_free, _qwen_args, qwen_workspace_bytes
 from .runtime import DeviceBuffer, memset, ptr, stream_handle, sync
 
 TEXT_PREFIX = "model.language_model"
@@ -59,17 +61,38 @@ class _Pinned:
             pass
 
 
+class _Graph:
+    """Owner of one captured layer call (sllm_moe_qwen_graph_new)."""
+
+    def __init__(self, a):
+        h = _lib.lib().sllm_moe_qwen_graph_new(a)
+        if not h:
+            raise RuntimeError("sllm_moe_qwen_graph_new: " + _lib.last_error())
+        self.h = h
+
+    def launch(self):
+        _lib.check(_lib.lib().sllm_moe_graph_launch(c_void_p(self.h), None),
+                   "sllm_moe_graph_launch")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _graph_free(self.h)
+            self.h = None
+
+
 class _Runner:
     """Calls the fused layer for a QwenMoE at decode sizes, reusing the
     device input staging, the output buffer, the workspace, the argument
     block of each (layer, n) and page-locked host staging: a host call is
-    one host bf16 rounding, an upload, the layer and a download, ordered on
-    one stream with one wait."""
+    one host bf16 rounding, an upload, the layer (a graph replay when
+    `graphs`) and a download, ordered on one stream with one wait."""
 
-    def __init__(self):
+    def __init__(self, graphs: bool = True):
         self._x = self._out = self._ws = self._zl = None
         self._hx = self._hy = None
         self._args = {}
+        self._graphs = {}
+        self.graphs = graphs
 
     def _pin(self, name, nbytes):
         b = getattr(self, name)
@@ -81,9 +104,10 @@ class _Runner:
     def _grow(self, name, nbytes):
         b = getattr(self, name)
         if b is None or b.nbytes < nbytes:
+            self._graphs.clear()  # graphs and argument blocks hold old pointers
+            self._args.clear()
             b = DeviceBuffer(max(int(nbytes), 4))
             setattr(self, name, b)
-            self._args.clear()  # cached argument blocks hold old pointers
         return b
 
     def args(self, layer: QwenMoE, n: int, zero_logits: bool, x=None, out=None,
@@ -130,7 +154,14 @@ class _Runner:
                                            cnt), "sllm_host_f32_to_bf16")
         _lib.check(L.sllm_copy_async(c_void_p(self._x.ptr), c_void_p(hx.ptr),
                                      cnt * 2, None), "sllm_copy_async")
-        _lib.check(L.sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
+        if self.graphs:
+            key = (id(layer), n, zero_logits)
+            g = self._graphs.get(key)
+            if g is None:
+                g = self._graphs[key] = _Graph(a)
+            g.launch()
+        else:
+            _lib.check(L.sllm_moe_qwen_forward(a), "sllm_moe_qwen_forward")
         _lib.check(L.sllm_copy_async(c_void_p(hy.ptr), c_void_p(self._out.ptr),
                                      cnt * 4, None), "sllm_copy_async")
         _lib.check(L.sllm_stream_sync(None), "sllm_stream_sync")
@@ -152,9 +183,9 @@ class DeviceMoEStack:
     """One fused device MoE layer per decoder layer, indexed like the
     reference's `_moe(x, i)`."""
 
-    def __init__(self, layers):
+    def __init__(self, layers, graphs: bool = True):
         self.layers = list(layers)
-        self._run = _Runner()
+        self._run = _Runner(graphs)
 
     @classmethod
     def from_weights(cls, weights: dict, n_layers: int, top_k: int,
@@ -209,13 +240,13 @@ class DenseSwiGLU:
     """A dense SwiGLU MLP, down(silu(gate x) * up x), on the fused layer
     (one expert, top-1 on zero logits, no shared expert)."""
 
-    def __init__(self, layer: QwenMoE):
+    def __init__(self, layer: QwenMoE, graphs: bool = True):
         if layer.E != 1 or layer.top_k != 1 or layer.Is:
             raise ValueError("DenseSwiGLU needs a one-expert, top-1 layer "
                              "without a shared expert")
         self.layer = layer
         self.H, self.I = layer.H, layer.I
-        self._run = _Runner()
+        self._run = _Runner(graphs)
 
     @classmethod
     def from_arrays(cls, gate_w, up_w, down_w):

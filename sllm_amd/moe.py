@@ -17,6 +17,8 @@ Two levels:
 
 from __future__ import annotations
 
+import weakref
+from ctypes import c_void_p
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -135,6 +137,50 @@ def qwen_forward_noalloc(x, out, weights: dict, *, T, H, E, I, topk, Is=0,
 def noalloc_max_bytes() -> int:
     """Size of the per-device scratch of qwen_forward_noalloc."""
     return int(_lib.lib().sllm_moe_qwen_forward_noalloc_max_bytes())
+
+
+def _graph_free(h):
+    try:
+        _lib.lib().sllm_moe_graph_free(c_void_p(h))
+    except Exception:
+        pass
+
+
+class LayerGraph:
+    """One qwen_forward_dev call captured as a HIP graph
+    (sllm_moe_qwen_graph_new). `launch()` replays it on the current contents
+    of the buffers it was captured with; the graph keeps references to them.
+    For decode batches a replay costs one launch instead of the layer's
+    kernel launches and their gaps."""
+
+    def __init__(self, x, out, weights: dict, *, T, H, E, I, topk, Is=0,
+                 mode="auto", out_f32=False, wdtype=0, eps=1e-20, logits=None,
+                 workspace=None, workspace_bytes=None, debug=None):
+        if workspace_bytes is None:
+            workspace_bytes = getattr(workspace, "nbytes", None)
+            if workspace_bytes is None and hasattr(workspace, "numel"):
+                workspace_bytes = workspace.numel() * workspace.element_size()
+        a = _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x,
+                       logits, weights, out, debug, workspace, workspace_bytes,
+                       None)
+        h = _lib.lib().sllm_moe_qwen_graph_new(a)
+        if not h:
+            raise RuntimeError("sllm_moe_qwen_graph_new: " + _lib.last_error())
+        self._keep = (x, out, weights, logits, workspace, debug)
+        self._h = h
+        self._fin = weakref.finalize(self, _graph_free, h)
+
+    def launch(self, stream=None) -> None:
+        if not self._fin.alive:
+            raise RuntimeError("LayerGraph: launch after free")
+        _lib.check(_lib.lib().sllm_moe_graph_launch(c_void_p(self._h),
+                                                    stream_handle(stream)),
+                   "sllm_moe_graph_launch")
+
+    def free(self) -> None:
+        """Destroys the graph (work already launched is unaffected)."""
+        self._fin()
+        self._keep = None
 
 
 # ---------------------------------------------------------------------------

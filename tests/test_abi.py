@@ -70,6 +70,16 @@ def test_error_contract_without_gpu():
     with pytest.raises(RuntimeError, match="rc=-1"):
         _lib.check(rc, "q4 kernel")
     assert q4.available()
+    # graph entry points: argument errors before any device call
+    assert lib.sllm_moe_qwen_graph_new(None) is None
+    assert "null args" in _lib.last_error()
+    a = _lib.QwenArgs()
+    a.T, a.H, a.E, a.I, a.topk = 4, 100, 8, 128, 2
+    assert lib.sllm_moe_qwen_graph_new(a) is None
+    assert "H % 256" in _lib.last_error()
+    assert lib.sllm_moe_graph_launch(None, None) == -1
+    assert "null graph" in _lib.last_error()
+    assert lib.sllm_moe_graph_free(None) == 0
 
 
 def test_host_bf16_rounding_matches_python():

@@ -160,3 +160,59 @@ def test_dense_swiglu_fp8_checkpoint(tmp_path):
         rel = rel_l2(mlp(x), qm.swiglu_mlp(x, deq["gate"], deq["up"], deq["down"]))
         print(f"dense fp8 n {n}: rel-L2 {rel:.2e}")
         assert rel < 1e-4
+
+
+@pytest.mark.parametrize("T,mode", [(1, "decode"), (8, "decode"), (32, "decode"),
+                                    (96, "prefill")])
+def test_layer_graph_replays_match_eager(T, mode):
+    """A captured layer call (sllm_moe_qwen_graph_new) replayed five times,
+    with new inputs written into the captured x buffer and eager layer calls
+    and synchronizations between the replays: every replay equals the eager
+    call on the same input bit for bit (same kernels, same order)."""
+    from sllm_amd.moe import LayerGraph, qwen_forward_dev, qwen_workspace_bytes
+    from sllm_amd.runtime import DeviceBuffer, sync, to_bf16
+    x0, W = qwen_fp8(seed=80 + T, T=T, H=512, E=16, I=256, Is=256)
+    k = 4
+    layer = qwen_layer(W, k)
+    H, E, I, Is = layer.H, layer.E, layer.I, layer.Is
+    kw = dict(T=T, H=H, E=E, I=I, Is=Is, topk=k, mode=mode, out_f32=True,
+              wdtype=layer.wdtype, eps=layer.eps)
+    xg = DeviceBuffer(T * H * 2)
+    og = DeviceBuffer(T * H * 4)
+    wsg = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, mode))
+    g = LayerGraph(xg, og, layer._w, workspace=wsg, **kw)
+    xe = DeviceBuffer(T * H * 2)
+    oe = DeviceBuffer(T * H * 4)
+    wse = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, mode))
+    rng = np.random.default_rng(T)
+    for r in range(5):
+        x = bf(rng.standard_normal((T, H)).astype(np.float32))
+        xg.upload_raw(to_bf16(x))
+        xe.upload_raw(to_bf16(x))
+        sync()
+        g.launch()
+        qwen_forward_dev(xe, oe, layer._w, workspace=wse, **kw)
+        sync()
+        got, want = og.copy_host().reshape(T, H), oe.copy_host().reshape(T, H)
+        np.testing.assert_array_equal(got, want, err_msg=f"replay {r}")
+        # eager work on the graph's own buffers between replays
+        qwen_forward_dev(xg, og, layer._w, workspace=wsg, **kw)
+        sync()
+    g.free()
+    with pytest.raises(RuntimeError):
+        g.launch()
+
+
+def test_moe_stack_graphs_match_eager():
+    """DeviceMoEStack with graph replay (the default) equals it without, at
+    changing batch sizes (1 -> 8 -> 1 -> 3) over two layers."""
+    from sllm_amd.decode import DeviceMoEStack
+    rng = np.random.default_rng(42)
+    E, H, I, Is, k = 16, 512, 256, 256, 4
+    w = _weight_dict(rng, 2, E, H, I, Is)
+    sg = DeviceMoEStack.from_weights(w, 2, k)
+    se = DeviceMoEStack(sg.layers, graphs=False)
+    for n in (1, 8, 1, 3):
+        x = bf(rng.standard_normal((n, H)).astype(np.float32))
+        for i in (0, 1):
+            np.testing.assert_array_equal(sg.moe(x, i), se.moe(x, i))
