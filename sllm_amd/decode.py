@@ -18,10 +18,12 @@ launches (gate/up, down, slice sum) over the rows in token order.
 
 Both keep their staging buffers, workspace and argument blocks between
 calls, so a decode step allocates nothing after its first call at a given
-batch size; the host-array calls also capture each (layer, batch size)
-layer call as a HIP graph on first use and replay it afterwards (one launch
-instead of the layer's kernel launches). `moe_dev` / `forward_dev` take
-device buffers for callers that keep the hidden state on the device.
+batch size. With graphs=True the host-array calls capture each (layer,
+batch size) layer call as a HIP graph on first use and replay it after
+that; on ROCm 7.2 a replay of the layer's 5-6 launches measured slower than
+issuing them (B=1 hook call 67 vs 59 us), so launches are the default.
+`moe_dev` / `forward_dev` take device buffers for callers that keep the
+hidden state on the device.
 
 Weights come from the reference's float weight dict (the names of
 Q4DeviceWeightTable, q4_device_decode.py:112-122, and of the hybrid table's
@@ -87,7 +89,7 @@ class _Runner:
     one host bf16 rounding, an upload, the layer (a graph replay when
     `graphs`) and a download, ordered on one stream with one wait."""
 
-    def __init__(self, graphs: bool = True):
+    def __init__(self, graphs: bool = False):
         self._x = self._out = self._ws = self._zl = None
         self._hx = self._hy = None
         self._args = {}
@@ -183,7 +185,7 @@ class DeviceMoEStack:
     """One fused device MoE layer per decoder layer, indexed like the
     reference's `_moe(x, i)`."""
 
-    def __init__(self, layers, graphs: bool = True):
+    def __init__(self, layers, graphs: bool = False):
         self.layers = list(layers)
         self._run = _Runner(graphs)
 
@@ -240,7 +242,7 @@ class DenseSwiGLU:
     """A dense SwiGLU MLP, down(silu(gate x) * up x), on the fused layer
     (one expert, top-1 on zero logits, no shared expert)."""
 
-    def __init__(self, layer: QwenMoE, graphs: bool = True):
+    def __init__(self, layer: QwenMoE, graphs: bool = False):
         if layer.E != 1 or layer.top_k != 1 or layer.Is:
             raise ValueError("DenseSwiGLU needs a one-expert, top-1 layer "
                              "without a shared expert")

@@ -204,14 +204,14 @@ def test_layer_graph_replays_match_eager(T, mode):
 
 
 def test_moe_stack_graphs_match_eager():
-    """DeviceMoEStack with graph replay (the default) equals it without, at
+    """DeviceMoEStack with graph replay equals it without (the default), at
     changing batch sizes (1 -> 8 -> 1 -> 3) over two layers."""
     from sllm_amd.decode import DeviceMoEStack
     rng = np.random.default_rng(42)
     E, H, I, Is, k = 16, 512, 256, 256, 4
     w = _weight_dict(rng, 2, E, H, I, Is)
-    sg = DeviceMoEStack.from_weights(w, 2, k)
-    se = DeviceMoEStack(sg.layers, graphs=False)
+    se = DeviceMoEStack.from_weights(w, 2, k)
+    sg = DeviceMoEStack(se.layers, graphs=True)
     for n in (1, 8, 1, 3):
         x = bf(rng.standard_normal((n, H)).astype(np.float32))
         for i in (0, 1):
