@@ -1,0 +1,421 @@
+// Compute-dense grouped expert GEMM over packed MXFP4 weights, for prefill
+// launches whose experts average more than one 128-row tile (a
+// DeepSeek-style layer at thousands of tokens, where the matrix cores, the
+// LDS and the weight stream all bound the projection).
+//
+// Same items' arithmetic and outputs as moe_stream_kernel (gemm_stream.hip)
+// with the fp4 weight format, over the same packed weights (the outputs
+// agree bit for bit); what changes is how operands reach the matrix cores:
+// * Wider wave tiles. An item is a 128-row tile x two packed slabs (256 h
+//   columns of gate/up, 512 output columns of down); wave w reads packed
+//   waves 2 (w % 4) and 2 (w % 4) + 1 of slab 2 np + w / 4 (a contiguous
+//   4 KB per K step) and owns 32 h columns (subtiles g, u, g, u) or 64
+//   output columns, so each activation fragment read from LDS feeds four
+//   MFMAs instead of two.
+// * Operands staged in LDS by the gfx950 direct-to-LDS loads
+//   (global_load_lds_dwordx4): a K step's weights and its 128 gathered
+//   activation rows go to LDS without passing through VGPRs, which leaves
+//   the registers to the 128 accumulators of the wider tile. Three LDS
+//   stages, loads two steps ahead. The activation rows are XOR-swizzled by
+//   row, which keeps the fragment reads free of bank conflicts (the
+//   streaming kernel's LDS was in conflict stalls 30% of its cycles at C4).
+// * All eight 16-row groups of a step run branch-free, group mi + 1's LDS
+//   reads issued before group mi's MFMAs (padding rows included: a
+//   per-group branch keeps the compiler from issuing reads ahead, and a
+//   second code path for partial tiles does not fit the registers).
+//
+// Synchronization: a step waits for its own stage's loads (vmcnt, counted
+// per wave: eight loads per stage) and then meets the other waves at a
+// barrier without a memory fence -- a fence would wait for every load in
+// flight, the prefetched stages included. The barrier also orders the
+// previous step's LDS reads before the loads that overwrite that stage.
+//
+// Measured at C4 (cycle counters around each phase of a step, one run):
+// waves spend ~40% of their time in the MFMA phase, ~30% issuing the
+// stage's 64 direct-to-LDS loads right after the barrier (the address unit
+// takes them one after another) and ~20% at the barrier; issuing the loads
+// between the groups' MFMAs instead made the step slower.
+#include <type_traits>
+
+#include "launch.h"
+
+namespace sllm {
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void;
+
+constexpr int DN_BM = 128;  // rows per tile (the permutation's prefill tiles)
+constexpr int DN_WAVES = 8;
+constexpr int DN_THREADS = 64 * DN_WAVES;
+constexpr int DN_STAGES = 3;
+constexpr int DN_ITEMS = 4;                  // items per chunk (LDS row tables)
+constexpr int DN_A = DN_BM * 128;            // activations: rows x 128 e4m3
+constexpr int DN_B = DN_WAVES * 4 * 1024;    // weights: 4 fp4 subtiles per wave
+constexpr int DN_SW = DN_WAVES * 256;        // e8m0 weight scales per wave
+constexpr int DN_SX = DN_BM * 4;             // activation scales (fp32)
+constexpr int DN_STAGE = DN_A + DN_B + DN_SW + DN_SX;
+constexpr int DN_BLK = 16384;                // packed fp4 block (slab, K step)
+constexpr int DN_LOADS = 8;                  // direct-to-LDS loads per wave per stage
+
+// LDS offset of 16-byte chunk c (K bytes [16 c, +16)) of tile row r: the
+// chunk index is XOR-swizzled with the row, so that the 16 rows an MFMA
+// fragment read touches spread over the banks.
+__device__ __forceinline__ int a_off(int r, int c) {
+  return r * 128 + ((c ^ (r & 7)) << 4);
+}
+
+__device__ __forceinline__ uint32_t e8m0_of(float pow2) {
+  return (__float_as_uint(pow2) >> 23) & 0xFF;
+}
+
+// s_waitcnt for the vector-memory counter alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that orders memory operations in the compiler but
+// waits for nothing in the hardware; `lds` also waits for this wave's LDS
+// operations first (for data exchanged through LDS).
+__device__ __forceinline__ void bar_only() { asm volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void bar_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Direct-to-LDS load of 16 (or 4) bytes per lane: lane i's bytes land at
+// l + 16 i (4 i); l is wave-uniform. Written as inline assembly so that the
+// compiler, which does not see the LDS write, adds no wait of its own
+// before the step's LDS reads (it would wait for every load in flight,
+// the prefetched stages included); the steps wait for their own stage
+// with explicit vmcnt waits instead.
+__device__ __forceinline__ void to_lds(const void* g, uint8_t* l, int bytes) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void)l);
+  if (bytes == 16)
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(m0) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(m0) : "memory", "m0");
+}
+
+template <int MODE>
+__global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
+    SegDesc S, int topk, float limit, int pow2) {
+  // three stages as three arrays: the compiler then sees that a step's LDS
+  // reads (one stage) do not alias the loads in flight (the other two) and
+  // adds no wait of its own for them
+  __shared__ __attribute__((aligned(16))) uint8_t stg0[DN_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stg1[DN_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stg2[DN_STAGE];
+  __shared__ int4 desc[DN_ITEMS];
+  __shared__ int rsrc[DN_ITEMS][DN_BM];
+  __shared__ float rwl[DN_ITEMS][DN_BM];  // row weights (1 without row_w)
+  __shared__ float red[DN_BM][DN_WAVES];  // gate/up epilogue: row amax per wave
+
+  constexpr int NTW = MODE == 0 ? 256 : 512;  // columns per item
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lg = lane >> 4, lc = lane & 15;
+  const int K = S.K, KB = K / 128, N = S.N;
+  const int ntn = N / NTW;          // items per row tile
+  const int nto = N / (NTW / 2);    // packed slabs across N
+  const int ow0 = 2 * (wave & 3);   // first packed wave of this wave's pair
+
+  const int total = *S.num_tiles * ntn;
+  const int nx = gridDim.x / 8;
+  const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
+  const int xbeg = (int)((long)total * xcd / 8);
+  const int xend = (int)((long)total * (xcd + 1) / 8);
+  const int nall = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
+
+  for (int cbase = 0; cbase < nall; cbase += DN_ITEMS) {
+    const int nitems = min(DN_ITEMS, nall - cbase);
+    if (tid < nitems) {
+      const int it = xbeg + jx + (cbase + tid) * nx;
+      const int rt = it / ntn, np = it % ntn;
+      const int4 d = *(const int4*)(S.tile_info + 4 * rt);
+      desc[tid] = make_int4(np, d.x, d.y, min(DN_BM, d.z));
+    }
+    __syncthreads();
+    for (int q = tid; q < nitems * DN_BM; q += DN_THREADS) {
+      const int i = q / DN_BM, r = q % DN_BM;
+      const int4 d = desc[i];
+      const int p = d.z + (r < d.w ? r : 0);  // rows past the tile read row 0
+      rsrc[i][r] = S.gather ? S.sorted_idx[p] / topk : p;
+      rwl[i][r] = S.row_w ? S.row_w[S.row_w_by_idx ? S.sorted_idx[p] : p] : 1.f;
+    }
+    __syncthreads();
+    const int total_steps = nitems * KB;
+
+    // ---- prefetch cursor: per-lane sources of the direct-to-LDS loads ----
+    // A: slots wave * 128 + q * 64 + lane (q = 0, 1) of the stage's 1024
+    // 16-byte chunks; slot g holds chunk (g % 8) ^ (row % 8) of row g / 8.
+    const int g0 = wave * 128 + lane, g1 = g0 + 64;
+    const int ar0 = g0 >> 3, ar1 = g1 >> 3;
+    const int ac0 = (g0 & 7) ^ (ar0 & 7), ac1 = (g1 & 7) ^ (ar1 & 7);
+    int pi = 0, pkb = 0;
+    const uint8_t *pa0 = nullptr, *pa1 = nullptr, *pb = nullptr, *psw = nullptr;
+    const float* psx = nullptr;
+    auto p_enter = [&](int i) __attribute__((always_inline)) {
+      const int4 d = desc[i];
+      pa0 = S.a + (size_t)rsrc[i][ar0] * K + ac0 * 16;
+      pa1 = S.a + (size_t)rsrc[i][ar1] * K + ac1 * 16;
+      psx = S.sa + (size_t)rsrc[i][wave * 16 + lc] * KB;
+      const size_t blk = ((size_t)d.y * nto + 2 * d.x + (wave >> 2)) * KB;
+      pb = S.wp + blk * DN_BLK + ow0 * 2048 + lane * 16;
+      psw = (const uint8_t*)S.s0 + blk * 1024 + ow0 * 128 + lane * 4;
+    };
+    auto issue = [&](uint8_t* base) __attribute__((always_inline)) {
+      to_lds(pa0 + pkb * 128, base + wave * 2048, 16);
+      to_lds(pa1 + pkb * 128, base + wave * 2048 + 1024, 16);
+      const uint8_t* b = pb + (size_t)pkb * DN_BLK;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        to_lds(b + j * 1024, base + DN_A + wave * 4096 + j * 1024, 16);
+      to_lds(psw + (size_t)pkb * 1024, base + DN_A + DN_B + wave * 256, 4);
+      if (lane < 16)
+        to_lds(psx + pkb, base + DN_A + DN_B + DN_SW + wave * 64, 4);
+      if (++pkb == KB && pi + 1 < nitems) {
+        pkb = 0;
+        p_enter(++pi);
+      }
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[mi][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // ---- epilogues --------------------------------------------------------
+    // acc[mi][j][v]: token mi * 16 + lc of the tile, output column 4 lg + v
+    // of subtile j (gate/up: j = 0, 2 gate and 1, 3 up of packed waves ow0,
+    // ow0 + 1; down: columns 16 j + 4 lg + v of the wave's 64).
+    auto epilogue = [&](int i) __attribute__((always_inline)) {
+      const int4 d = desc[i];
+      const int np = d.x, rb = d.z, rows = d.w;
+      const int ngrp = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+      const int slab = 2 * np + (wave >> 2);  // packed slab of this wave
+      if constexpr (MODE == 0) {
+        // h = silu(g) * u * route weight; per-row amax over the four waves
+        // of the packed slab (one 128-column quantization block); e4m3
+        // with the row's scale
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          if (mi < ngrp) {
+            const int t = mi * 16 + lc;
+            const float rw = rwl[i][t];
+            float amax = 0.f;
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                float g = acc[mi][2 * pr][v], u = acc[mi][2 * pr + 1][v];
+                if (limit > 0.f) {
+                  u = fminf(fmaxf(u, -limit), limit);
+                  g = fminf(g, limit);
+                }
+                const float h = silu_fast(g) * u * rw;
+                acc[mi][2 * pr][v] = h;
+                amax = fmaxf(amax, fabsf(h));
+              }
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            if (lg == 0) red[t][wave] = amax;
+          }
+        }
+        bar_lds();
+        const int w0 = wave & 4;  // first wave of this packed slab
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          if (mi < ngrp) {
+            const int t = mi * 16 + lc;
+            const float amax = fmaxf(fmaxf(red[t][w0], red[t][w0 + 1]),
+                                     fmaxf(red[t][w0 + 2], red[t][w0 + 3]));
+            float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+            float inv;
+            if (pow2) {
+              const uint32_t bits = __float_as_uint(sc);
+              const int ex = (int)((bits >> 23) & 0xFF) - 127 + ((bits & 0x7FFFFF) ? 1 : 0);
+              sc = __uint_as_float((uint32_t)(ex + 127) << 23);
+              inv = __uint_as_float((uint32_t)(127 - ex) << 23);
+            } else {
+              inv = __builtin_amdgcn_rcpf(sc);
+            }
+            if (t < rows) {
+              uint8_t* hrow = S.hq + (size_t)(rb + t) * N + slab * 128;
+#pragma unroll
+              for (int pr = 0; pr < 2; ++pr) {
+                float y[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                  y[v] = fminf(fmaxf(acc[mi][2 * pr][v] * inv, -448.f), 448.f);
+                *(uint32_t*)(hrow + (ow0 + pr) * 16 + lg * 4) =
+                    f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
+              }
+              if ((wave & 3) == 0 && lg == 0)
+                S.hs[(size_t)(rb + t) * (N / 128) + slab] = sc;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          if (mi < ngrp) {
+            const int t = mi * 16 + lc;
+            if (t < rows) {
+              const float rw = rwl[i][t];
+              uint16_t* yrow = S.y + (size_t)(rb + t) * N + slab * 256 + ow0 * 32;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][j][0] * rw) |
+                                    ((uint32_t)f32_to_bf16(acc[mi][j][1] * rw) << 16);
+                const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][j][2] * rw) |
+                                    ((uint32_t)f32_to_bf16(acc[mi][j][3] * rw) << 16);
+                *(uint2*)(yrow + j * 16 + lg * 4) = make_uint2(lo, hi);
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mi][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+
+    // ---- pipeline -----------------------------------------------------------
+    // step s on stage J = s % 3 (J a compile-time constant), K step ckb of
+    // item ci; issues stage s + 2 into (J + 2) % 3. The cursors are passed
+    // by value: kept in memory by reference, the barrier's memory clobber
+    // would make every step reload them and wait for all loads in flight.
+    auto step = [&](auto J, int s, int ci, int ckb) __attribute__((always_inline)) {
+      constexpr int j = decltype(J)::value;
+      uint8_t* const cur = j == 0 ? stg0 : (j == 1 ? stg1 : stg2);
+      uint8_t* const nxt = j == 0 ? stg2 : (j == 1 ? stg0 : stg1);
+      // stage s's loads: stage s + 1's (issued after them, if any) may
+      // remain in flight; epilogue stores issued before those are waited
+      // for as well
+      if (s + 1 < total_steps) wait_vm<DN_LOADS>();
+      else wait_vm<0>();
+      bar_only();
+      const bool last = ckb + 1 == KB;
+      if (!last && s + 2 < total_steps) issue(nxt);
+      const uint8_t* A = cur;
+      const uint8_t* B = cur + DN_A + wave * 4096;
+      const uint8_t* SW = cur + DN_A + DN_B + wave * 256;
+      const float* SX = (const float*)(cur + DN_A + DN_B + DN_SW);
+      u32x4 wf[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wf[q] = *(const u32x4*)(B + q * 1024 + lane * 16);
+      const uint32_t sw = (uint32_t)*(const uint16_t*)(SW + lane * 2) |
+                          ((uint32_t)*(const uint16_t*)(SW + 128 + lane * 2) << 16);
+      // group mi of the step: its activation fragment (with an fp4 A
+      // operand the fp8 B operand's two 16-byte halves are K bytes
+      // [16 lg, +16) and [64 + 16 lg, +16) of the step, the streaming
+      // kernel's fragment for this format) against the four weight subtiles
+      struct Frag {
+        v8i x;
+        int sx;
+      };
+      auto load_frag = [&](int mi) __attribute__((always_inline)) {
+        const int r = mi * 16 + lc;
+        const u32x4 x0 = *(const u32x4*)(A + a_off(r, lg));
+        const u32x4 x1 = *(const u32x4*)(A + a_off(r, 4 + lg));
+        Frag f;
+        f.x = (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                    (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        f.sx = (int)e8m0_of(SX[r]);
+        return f;
+      };
+      auto mfmas = [&](int mi, const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const v8i wv = {(int)wf[q].x, (int)wf[q].y, (int)wf[q].z, (int)wf[q].w,
+                          0, 0, 0, 0};
+          acc[mi][q] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wv, f.x, acc[mi][q], 4, 0, 0, (int)((sw >> (8 * q)) & 0xFF), 0, f.sx);
+        }
+      };
+      // all eight groups, branch-free (the MFMAs of padding rows included:
+      // a per-group branch keeps the compiler from issuing group mi + 1's
+      // LDS reads ahead of group mi's MFMAs, and two code paths do not fit
+      // the registers); the scheduling barriers keep the compiler from
+      // hoisting every group's reads at once
+      {
+        Frag cur_f = load_frag(0);
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          Frag nx = cur_f;
+          if (mi < 7) nx = load_frag(mi + 1);
+          mfmas(mi, cur_f);
+          __builtin_amdgcn_sched_barrier(0);
+          cur_f = nx;
+        }
+      }
+      if (last) {
+        epilogue(ci);
+        if (s + 2 < total_steps) issue(nxt);
+      }
+    };
+    p_enter(0);
+    issue(stg0);
+    if (total_steps > 1) issue(stg1);
+    int ci = 0, ckb = 0;
+    auto adv = [&]() __attribute__((always_inline)) {
+      if (++ckb == KB) {
+        ckb = 0;
+        ++ci;
+      }
+    };
+    for (int s = 0; s < total_steps; s += DN_STAGES) {
+      step(std::integral_constant<int, 0>(), s, ci, ckb);
+      adv();
+      if (s + 1 < total_steps) {
+        step(std::integral_constant<int, 1>(), s + 1, ci, ckb);
+        adv();
+      }
+      if (s + 2 < total_steps) {
+        step(std::integral_constant<int, 2>(), s + 2, ci, ckb);
+        adv();
+      }
+    }
+    __syncthreads();  // the next chunk rewrites desc / rsrc
+  }
+}
+
+template <int MODE>
+int go_dense(const SegDesc& s, int topk, float limit, int pow2, hipStream_t st,
+             int num_cus) {
+  const long grid = 8L * ((num_cus + 7) / 8);
+  moe_dense_kernel<MODE><<<(unsigned)grid, DN_THREADS, 0, st>>>(s, topk, limit, pow2);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+}  // namespace
+
+bool dense_fits(int bf, int mode, const SegDesc& s0, const SegDesc* s1) {
+  return bf == 2 && !s1 && s0.wreuse && s0.tile_info && s0.num_tiles &&
+         s0.N % (mode == 0 ? 256 : 512) == 0 && s0.K % 128 == 0 &&
+         (mode == 0 ? (s0.hq && s0.hs) : s0.y != nullptr);
+}
+
+int launch_dense(int mode, const SegDesc& s0, int topk, float limit, int pow2,
+                 hipStream_t st, int num_cus) {
+  SLLM_REQUIRE(dense_fits(2, mode, s0, nullptr) && s0.a && s0.sa && s0.wp && s0.s0,
+               "dense gemm: unsupported segment (N=%d K=%d)", s0.N, s0.K);
+  SLLM_REQUIRE((long)s0.max_tiles * s0.N < (1L << 31) && s0.K <= 65536,
+               "dense gemm: too large");
+  return mode == 0 ? go_dense<0>(s0, topk, limit, pow2, st, num_cus)
+                   : go_dense<1>(s0, topk, limit, pow2, st, num_cus);
+}
+
+}  // namespace sllm

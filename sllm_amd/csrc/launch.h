@@ -149,6 +149,12 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
                   hipStream_t st);
+// Compute-dense variant (gemm_dense.hip) for MXFP4 layers whose experts
+// average more than one 128-row tile (wreuse): one routed segment with a
+// tile table, N a multiple of 256 (gate/up) or 512 (down).
+bool dense_fits(int bf, int mode, const SegDesc& s0, const SegDesc* s1);
+int launch_dense(int mode, const SegDesc& s0, int topk, float limit, int pow2,
+                 hipStream_t st, int num_cus);
 // Decode variant over the same packed weights: bm-row tiles (16 or 32; the
 // tile_info rows must fit), weights converted to bf16 in registers and
 // multiplied by unquantized activations with bf16 MFMAs. mode 0 reads bf16 rows (a, row stride K elements) and

@@ -15,6 +15,7 @@
 //  decode:  fp32 activations against dequantized weights in a
 //           bandwidth-bound GEMV over the touched experts only.
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 #include "../../include/sllm_moe.h"
@@ -656,6 +657,38 @@ long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
       .total;
 }
 
+}  // extern "C"
+
+namespace sllm {
+
+static int device_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+// The DeepSeek layer's routed projections run on the compute-dense kernel
+// in prefill over packed MXFP4 weights when the experts average more than
+// one 128-row tile. SLLM_MOE_DENSE=0 in the environment keeps the
+// streaming kernel (same arithmetic, for comparisons).
+static bool dense_layer(const sllm_moe_ds_args* a) {
+  const char* env = getenv("SLLM_MOE_DENSE");
+  if (env && env[0] == '0') return false;
+  return a->w13_packed && !pick_decode(a->mode, a->T) &&
+         (long)a->T * a->topk > (long)PREFILL_BM * a->E && a->I % 256 == 0 &&
+         a->H % 512 == 0;
+}
+
+}  // namespace sllm
+
+extern "C" {
+
 int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   if (check_common(a, "sllm_moe_ds_forward")) return -1;
   SLLM_REQUIRE(a->workspace, "sllm_moe_ds_forward: null workspace");
@@ -672,6 +705,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   const int T = a->T, H = a->H, E = a->E, I = a->I, k = a->topk;
   const int Is = sh ? a->Is : 0;
   const float L = a->swiglu_limit;
+  const bool dense = dense_layer(a);
   const Plan p = make_plan(T, H, E, I, Is, k, a->mode, sh, !a->logits_given,
                            false, true);
   SLLM_REQUIRE(a->workspace_bytes >= (long)p.total,
@@ -825,8 +859,9 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       r1.N = I; r1.K = H; r1.row_w = w; r1.row_w_by_idx = 1;
       r1.hq = hq; r1.hs = hs;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-            launch_stream(2, 0, r1, nullptr, k, L, 1,
-                          (long)p.max_tiles * (I / 128), st));
+            dense ? launch_dense(0, r1, k, L, 1, st, device_cus())
+                  : launch_stream(2, 0, r1, nullptr, k, L, 1,
+                                  (long)p.max_tiles * (I / 128), st));
       SegDesc r2{};
       r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
@@ -834,8 +869,9 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
       r2.N = H; r2.K = I; r2.y = y;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-            launch_stream(2, 1, r2, nullptr, k, 0.f, 1,
-                          (long)p.max_tiles * (H / 256), st));
+            dense ? launch_dense(1, r2, k, 0.f, 1, st, device_cus())
+                  : launch_stream(2, 1, r2, nullptr, k, 0.f, 1,
+                                  (long)p.max_tiles * (H / 256), st));
       if (sh) {
         SegDesc s1{};
         s1.wreuse = weights_reused(T, 1, PREFILL_BM);

@@ -166,6 +166,29 @@ def test_deepseek_prefill_small(T, G, kg, L, packed):
     assert rel < 3e-3 and mabs < 0.05 * scale
 
 
+@pytest.mark.parametrize("T,L", [(1024, 10.0), (777, 0.0)])
+def test_deepseek_dense_kernel_matches_stream(T, L, monkeypatch):
+    """Prefill whose experts average more than one 128-row tile runs the
+    routed MXFP4 projections on the compute-dense kernel (gemm_dense.hip);
+    SLLM_MOE_DENSE=0 runs the same items on the streaming kernel. Same
+    MFMAs over the K steps in the same order and the same epilogues: the
+    outputs agree bit for bit, and match the oracle. T=777 leaves tiles of
+    4 rows (skipped 16-row groups)."""
+    x, W = deepseek_mxfp4(seed=T, T=T, H=512, E=16, I=256, Is=256)
+    route = dict(n_group=4, topk_group=2, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=L)
+    layer = deepseek_layer(W, 8, **route)
+    y_dense, r = layer.forward(x, mode="prefill", return_routing=True)
+    for _ in range(3):  # the same bits on every call
+        np.testing.assert_array_equal(layer.forward(x, mode="prefill"), y_dense)
+    monkeypatch.setenv("SLLM_MOE_DENSE", "0")
+    y_stream = layer.forward(x, mode="prefill")
+    np.testing.assert_array_equal(y_dense, y_stream)
+    want = dm.moe_layer_mxfp4(x, r["logits"], W, 8, L, "sigmoid", 2.5, 4, 2)
+    rel, mabs, scale = _report("deepseek dense prefill", y_dense, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+
+
 @pytest.mark.parametrize("T,mode", [(200, "prefill"), (8, "decode")])
 def test_deepseek_hash_layer(T, mode):
     """A hash layer (first n_hash_layers of DeepSeek-V4): experts from the
