@@ -724,6 +724,77 @@ def cpu_c1_literal_loop():
 
 
 # --------------------------------------------------------------------------
+def decode_leg(layer, batches, iters, flush):
+    """C3: the C2 layer in decode mode at each batch size B, per call
+    between HIP events with a 512 MiB fill before each timed call (L2 and
+    MALL flushed); `us` issues the layer's launches, `us_graph` replays the
+    same call captured as a HIP graph; B=32 adds a per-stage breakdown."""
+    import numpy as np
+    from sllm_amd.moe import STAGES, LayerGraph, qwen_workspace_bytes
+    from sllm_amd.runtime import DeviceBuffer, Event, memset, sync, to_bf16, to_device_raw
+    c = layer.cfg
+    H, E, I, Is, k = c["H"], c["E"], c["I"], c["Is"], c["k"]
+    decode = {}
+    for B in batches:
+        xb_host = to_bf16_values(layer.rng.standard_normal((B, H)).astype(np.float32))
+        xb = to_device_raw(to_bf16(xb_host))
+        ob = DeviceBuffer(B * H * 2)
+        wsb = DeviceBuffer(qwen_workspace_bytes(B, H, E, I, Is, k, "decode"))
+        cb = DeviceBuffer(E * 4)
+        layer_call(layer, xb, ob, wsb, B, "decode", debug={"counts_out": cb})
+        sync()
+        tb = int((cb.copy_host_raw(np.int32, (E,)) > 0).sum())
+        a0, a1 = Event(), Event()
+
+        def timed(run):
+            t = []
+            for it in range(iters + 3):
+                memset(flush, it & 0xFF, flush.nbytes)
+                a0.record()
+                run()
+                a1.record()
+                a1.synchronize()
+                if it >= 3:
+                    t.append(a0.elapsed_ms(a1) * 1e3)
+            return statistics.median(t)
+        us = timed(lambda: layer_call(layer, xb, ob, wsb, B, "decode"))
+        g = LayerGraph(xb, ob, layer.w, T=B, H=H, E=E, I=I, Is=Is, topk=k,
+                       mode="decode", out_f32=False, workspace=wsb)
+        us_graph = timed(g.launch)
+        g.free()
+        nb = decode_bytes(c, B, tb)
+        decode[str(B)] = {"us": round(us, 2), "us_graph": round(us_graph, 2),
+                          "touched_experts": tb,
+                          "bytes": nb, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                          "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        if B == 32:  # per-stage breakdown (flushed like the timed calls)
+            evs = [Event() for _ in range(2 * len(STAGES))]
+            per = {s_: [] for s_ in STAGES}
+            for it in range(10):
+                memset(flush, it & 0xFF, flush.nbytes)
+                layer_call(layer, xb, ob, wsb, B, "decode", stage_events=evs)
+                evs[-1].synchronize()
+                for i, s_ in enumerate(STAGES):
+                    per[s_].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3)
+            decode[str(B)]["stage_us"] = {s_: round(statistics.median(v), 2)
+                                          for s_, v in per.items()}
+        log(f"decode B={B}: {us:.1f} us ({us_graph:.1f} as a graph replay), "
+            f"touched {tb}, {decode[str(B)]['GBps']} GB/s")
+    return decode
+
+
+def run_decode_batch(args):
+    """One C3 decode batch alone (the C2 layer at B = --decode-batch
+    tokens), one JSON line: for profiling the decode kernels."""
+    from sllm_amd.runtime import DeviceBuffer
+    layer = DeviceLayer(dict(C2), seed=args.seed)
+    flush = DeviceBuffer(512 << 20)
+    d = decode_leg(layer, (args.decode_batch,), args.decode_iters, flush)
+    print(json.dumps({"metric": "C3 decode layer us", "batch": args.decode_batch,
+                      **d[str(args.decode_batch)]}), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -742,6 +813,8 @@ def main(argv=None) -> int:
                     help="only time loading a synthetic C2-shaped FP8 "
                          "checkpoint (safetensors, reference naming) to the "
                          "device and exit")
+    ap.add_argument("--decode-batch", type=int, default=0, metavar="B",
+                    help="only time the C3 decode layer at B tokens and exit")
     ap.add_argument("--device-decode", action="store_true",
                     help="only time the device-decode drop-ins (MoE hook and "
                          "dense SwiGLU MLP) at decode batch sizes and exit")
@@ -760,7 +833,7 @@ def main(argv=None) -> int:
     import numpy as np
 
     from sllm_amd import _lib
-    from sllm_amd.moe import STAGES, LayerGraph, qwen_workspace_bytes
+    from sllm_amd.moe import STAGES, qwen_workspace_bytes
     from sllm_amd.runtime import (DeviceBuffer, Event, memset, sync, to_bf16,
                                   to_device_raw)
     if not _lib.available():
@@ -780,6 +853,8 @@ def main(argv=None) -> int:
         return run_loader(args)
     if args.device_decode:
         return run_device_decode(args)
+    if args.decode_batch:
+        return run_decode_batch(args)
     if args.config == "c4":
         return run_c4(args)
     if args.config == "c5":
@@ -864,60 +939,8 @@ def main(argv=None) -> int:
     log(f"prefill with caches flushed: {layer_info['ms_flushed']} ms")
 
     # ---- decode batches (C3) -------------------------------------------
-    decode = {}
-    if not args.no_decode:
-        for B in (1, 8, 32, 64):
-            xb_host = to_bf16_values(layer.rng.standard_normal((B, H)).astype(np.float32))
-            xb = to_device_raw(to_bf16(xb_host))
-            ob = DeviceBuffer(B * H * 2)
-            wsb = DeviceBuffer(qwen_workspace_bytes(B, H, E, I, Is, k, "decode"))
-            cb = DeviceBuffer(E * 4)
-            layer_call(layer, xb, ob, wsb, B, "decode", debug={"counts_out": cb})
-            sync()
-            tb = int((cb.copy_host_raw(np.int32, (E,)) > 0).sum())
-            times = []
-            a0, a1 = Event(), Event()
-            for it in range(args.decode_iters + 3):
-                memset(flush, it & 0xFF, flush.nbytes)
-                a0.record()
-                layer_call(layer, xb, ob, wsb, B, "decode")
-                a1.record()
-                a1.synchronize()
-                if it >= 3:
-                    times.append(a0.elapsed_ms(a1) * 1e3)
-            us_eager = statistics.median(times)
-            # the same call captured once as a HIP graph, replayed
-            g = LayerGraph(xb, ob, layer.w, T=B, H=H, E=E, I=I, Is=Is, topk=k,
-                           mode="decode", out_f32=False, workspace=wsb)
-            gt = []
-            for it in range(args.decode_iters + 3):
-                memset(flush, it & 0xFF, flush.nbytes)
-                a0.record()
-                g.launch()
-                a1.record()
-                a1.synchronize()
-                if it >= 3:
-                    gt.append(a0.elapsed_ms(a1) * 1e3)
-            g.free()
-            us, us_graph = us_eager, statistics.median(gt)
-            nb = decode_bytes(c, B, tb)
-            decode[str(B)] = {"us": round(us, 2), "us_graph": round(us_graph, 2),
-                              "touched_experts": tb,
-                              "bytes": nb, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
-                              "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
-            if B == 32:  # per-stage breakdown (flushed like the timed calls)
-                evs = [Event() for _ in range(2 * len(STAGES))]
-                per = {s_: [] for s_ in STAGES}
-                for it in range(10):
-                    memset(flush, it & 0xFF, flush.nbytes)
-                    layer_call(layer, xb, ob, wsb, B, "decode", stage_events=evs)
-                    evs[-1].synchronize()
-                    for i, s_ in enumerate(STAGES):
-                        per[s_].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3)
-                decode[str(B)]["stage_us"] = {s_: round(statistics.median(v), 2)
-                                              for s_, v in per.items()}
-            log(f"decode B={B}: {us:.1f} us ({us_graph:.1f} as a graph replay), touched {tb}, "
-                f"{decode[str(B)]['GBps']} GB/s")
+    decode = {} if args.no_decode else decode_leg(layer, (1, 8, 32, 64),
+                                                  args.decode_iters, flush)
 
     # ---- CPU baseline -----------------------------------------------------
     cpu = c1_loop = None
