@@ -25,16 +25,18 @@
 //   second code path for partial tiles does not fit the registers).
 //
 // Synchronization: a step waits for its own stage's loads (vmcnt, counted
-// per wave: eight loads per stage) and then meets the other waves at a
+// per wave: fifteen loads per loader wave per stage) and then meets the other waves at a
 // barrier without a memory fence -- a fence would wait for every load in
 // flight, the prefetched stages included. The barrier also orders the
 // previous step's LDS reads before the loads that overwrite that stage.
 //
-// Measured at C4 (cycle counters around each phase of a step, one run):
-// waves spend ~40% of their time in the MFMA phase, ~30% issuing the
-// stage's 64 direct-to-LDS loads right after the barrier (the address unit
-// takes them one after another) and ~20% at the barrier; issuing the loads
-// between the groups' MFMAs instead made the step slower.
+// Measured at C4 (cycle counters around each phase of a step, one run,
+// all eight waves loading): waves spent ~40% of their time in the MFMA
+// phase, ~30% issuing the stage's 64 direct-to-LDS loads right after the
+// barrier (the address unit takes them one after another) and ~20% at the
+// barrier; issuing the loads between the groups' MFMAs made the step
+// slower. Loading by waves 0-3 only (the other wave on each SIMD computes
+// meanwhile) took the C4 gate/up launch from 2.16 to 2.07 ms.
 #include <type_traits>
 
 #include "launch.h"
@@ -59,7 +61,7 @@ constexpr int DN_SW = DN_WAVES * 256;        // e8m0 weight scales per wave
 constexpr int DN_SX = DN_BM * 4;             // activation scales (fp32)
 constexpr int DN_STAGE = DN_A + DN_B + DN_SW + DN_SX;
 constexpr int DN_BLK = 16384;                // packed fp4 block (slab, K step)
-constexpr int DN_LOADS = 8;                  // direct-to-LDS loads per wave per stage
+constexpr int DN_LOADS = 15;                 // direct-to-LDS loads per loader wave per stage
 
 // LDS offset of 16-byte chunk c (K bytes [16 c, +16)) of tile row r: the
 // chunk index is XOR-swizzled with the row, so that the 16 rows an MFMA
@@ -154,33 +156,54 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
     const int total_steps = nitems * KB;
 
     // ---- prefetch cursor: per-lane sources of the direct-to-LDS loads ----
-    // A: slots wave * 128 + q * 64 + lane (q = 0, 1) of the stage's 1024
-    // 16-byte chunks; slot g holds chunk (g % 8) ^ (row % 8) of row g / 8.
-    const int g0 = wave * 128 + lane, g1 = g0 + 64;
-    const int ar0 = g0 >> 3, ar1 = g1 >> 3;
-    const int ac0 = (g0 & 7) ^ (ar0 & 7), ac1 = (g1 & 7) ^ (ar1 & 7);
+    // Waves 0-3 load every stage (waves 4-7 only compute, so that on each
+    // SIMD one wave's MFMAs run while the other issues loads; issued by all
+    // eight right after the barrier, the loads held every wave at the
+    // address unit). Loader L: activation slots 256 L + 64 q + lane (q < 4)
+    // of the stage's 1024 16-byte chunks (slot g holds chunk
+    // (g % 8) ^ (row % 8) of row g / 8); the weights and weight scales of
+    // compute waves 2 L and 2 L + 1; the activation scales of rows 32 L +
+    // lane (lane < 32).
+    const bool loader = wave < 4;
     int pi = 0, pkb = 0;
-    const uint8_t *pa0 = nullptr, *pa1 = nullptr, *pb = nullptr, *psw = nullptr;
-    const float* psx = nullptr;
+    uint32_t poff[4], psx = 0;  // byte offsets from S.a / S.sa
+    const uint8_t* pbw[2] = {nullptr, nullptr};   // weight block of wave 2 L + c
+    const uint8_t* psw[2] = {nullptr, nullptr};   // its scale block
     auto p_enter = [&](int i) __attribute__((always_inline)) {
       const int4 d = desc[i];
-      pa0 = S.a + (size_t)rsrc[i][ar0] * K + ac0 * 16;
-      pa1 = S.a + (size_t)rsrc[i][ar1] * K + ac1 * 16;
-      psx = S.sa + (size_t)rsrc[i][wave * 16 + lc] * KB;
-      const size_t blk = ((size_t)d.y * nto + 2 * d.x + (wave >> 2)) * KB;
-      pb = S.wp + blk * DN_BLK + ow0 * 2048 + lane * 16;
-      psw = (const uint8_t*)S.s0 + blk * 1024 + ow0 * 128 + lane * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int g = 256 * wave + 64 * q + lane, row = g >> 3;
+        poff[q] = (uint32_t)rsrc[i][row] * K + (((g & 7) ^ (row & 7)) << 4);
+      }
+      psx = (uint32_t)rsrc[i][32 * wave + (lane & 31)] * KB * 4;
+      const int e = __builtin_amdgcn_readfirstlane(d.y);
+      const int np = __builtin_amdgcn_readfirstlane(d.x);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int cw = 2 * wave + c;  // the compute wave served
+        const size_t blk = ((size_t)e * nto + 2 * np + (cw >> 2)) * KB;
+        pbw[c] = S.wp + blk * DN_BLK + 2 * (cw & 3) * 2048;
+        psw[c] = (const uint8_t*)S.s0 + blk * 1024 + 2 * (cw & 3) * 128;
+      }
     };
     auto issue = [&](uint8_t* base) __attribute__((always_inline)) {
-      to_lds(pa0 + pkb * 128, base + wave * 2048, 16);
-      to_lds(pa1 + pkb * 128, base + wave * 2048 + 1024, 16);
-      const uint8_t* b = pb + (size_t)pkb * DN_BLK;
+      if (!loader) return;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        to_lds(b + j * 1024, base + DN_A + wave * 4096 + j * 1024, 16);
-      to_lds(psw + (size_t)pkb * 1024, base + DN_A + DN_B + wave * 256, 4);
-      if (lane < 16)
-        to_lds(psx + pkb, base + DN_A + DN_B + DN_SW + wave * 64, 4);
+      for (int q = 0; q < 4; ++q)
+        to_lds(S.a + poff[q] + pkb * 128, base + wave * 4096 + q * 1024, 16);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int cw = 2 * wave + c;
+        const uint8_t* b = pbw[c] + (size_t)pkb * DN_BLK + lane * 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          to_lds(b + j * 1024, base + DN_A + cw * 4096 + j * 1024, 16);
+        to_lds(psw[c] + (size_t)pkb * 1024 + lane * 4, base + DN_A + DN_B + cw * 256, 4);
+      }
+      if (lane < 32)
+        to_lds((const uint8_t*)S.sa + psx + pkb * 4,
+               base + DN_A + DN_B + DN_SW + wave * 128, 4);
       if (++pkb == KB && pi + 1 < nitems) {
         pkb = 0;
         p_enter(++pi);
@@ -365,7 +388,7 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
         if (s + 2 < total_steps) issue(nxt);
       }
     };
-    p_enter(0);
+    if (loader) p_enter(0);
     issue(stg0);
     if (total_steps > 1) issue(stg1);
     int ci = 0, ckb = 0;
