@@ -24,11 +24,13 @@
 //   per-group branch keeps the compiler from issuing reads ahead, and a
 //   second code path for partial tiles does not fit the registers).
 //
-// Synchronization: a step waits for its own stage's loads (vmcnt, counted
-// per wave: fifteen loads per loader wave per stage) and then meets the other waves at a
-// barrier without a memory fence -- a fence would wait for every load in
-// flight, the prefetched stages included. The barrier also orders the
-// previous step's LDS reads before the loads that overwrite that stage.
+// Synchronization: a stage is ready when each loader wave has waited for
+// its own loads of it (vmcnt, counted per wave: fourteen loads per stage)
+// and the waves meet at a barrier without a memory fence -- a fence would
+// wait for every load in flight, the prefetched stages included. The
+// barrier also orders every wave's reads of the stage before the loads
+// that overwrite it. A step makes the next stage ready before its last
+// group's MFMAs, so that their issue covers the barrier.
 //
 // Measured at C4 (cycle counters around each phase of a step, one run,
 // all eight waves loading): waves spent ~40% of their time in the MFMA
@@ -61,7 +63,7 @@ constexpr int DN_SW = DN_WAVES * 256;        // e8m0 weight scales per wave
 constexpr int DN_SX = DN_BM * 4;             // activation scales (fp32)
 constexpr int DN_STAGE = DN_A + DN_B + DN_SW + DN_SX;
 constexpr int DN_BLK = 16384;                // packed fp4 block (slab, K step)
-constexpr int DN_LOADS = 15;                 // direct-to-LDS loads per loader wave per stage
+constexpr int DN_LOADS = 14;                 // direct-to-LDS loads per loader wave per stage
 
 // LDS offset of 16-byte chunk c (K bytes [16 c, +16)) of tile row r: the
 // chunk index is XOR-swizzled with the row, so that the 16 rows an MFMA
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
     int pi = 0, pkb = 0;
     uint32_t poff[4], psx = 0;  // byte offsets from S.a / S.sa
     const uint8_t* pbw[2] = {nullptr, nullptr};   // weight block of wave 2 L + c
-    const uint8_t* psw[2] = {nullptr, nullptr};   // its scale block
+    const uint8_t* psw = nullptr;  // scales of both (512 contiguous bytes)
     auto p_enter = [&](int i) __attribute__((always_inline)) {
       const int4 d = desc[i];
 #pragma unroll
@@ -184,30 +186,40 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
         const int cw = 2 * wave + c;  // the compute wave served
         const size_t blk = ((size_t)e * nto + 2 * np + (cw >> 2)) * KB;
         pbw[c] = S.wp + blk * DN_BLK + 2 * (cw & 3) * 2048;
-        psw[c] = (const uint8_t*)S.s0 + blk * 1024 + 2 * (cw & 3) * 128;
+        if (c == 0) psw = (const uint8_t*)S.s0 + blk * 1024 + 2 * (cw & 3) * 128;
+      }
+    };
+    // load j (0 <= j < DN_LOADS, a compile-time constant once unrolled) of
+    // the loader's stage: 0-3 activation chunks, 4-7 and 8-11 the four
+    // weight subtiles of compute waves 2 L and 2 L + 1, 12 their weight
+    // scales (512 contiguous bytes, 16 per lane), 13 the activation scales
+    auto dma = [&](int j, uint8_t* base) __attribute__((always_inline)) {
+      if (j < 4) {
+        to_lds(S.a + poff[j] + pkb * 128, base + wave * 4096 + j * 1024, 16);
+      } else if (j < 12) {
+        const int c = (j - 4) / 4, q = (j - 4) % 4, cw = 2 * wave + c;
+        to_lds(pbw[c] + (size_t)pkb * DN_BLK + lane * 16 + q * 1024,
+               base + DN_A + cw * 4096 + q * 1024, 16);
+      } else if (lane < 32) {
+        if (j == 12)
+          to_lds(psw + (size_t)pkb * 1024 + lane * 16,
+                 base + DN_A + DN_B + 2 * wave * 256, 16);
+        else
+          to_lds((const uint8_t*)S.sa + psx + pkb * 4,
+                 base + DN_A + DN_B + DN_SW + wave * 128, 4);
+      }
+    };
+    auto advance = [&]() __attribute__((always_inline)) {
+      if (++pkb == KB && pi + 1 < nitems) {
+        pkb = 0;
+        p_enter(++pi);
       }
     };
     auto issue = [&](uint8_t* base) __attribute__((always_inline)) {
       if (!loader) return;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        to_lds(S.a + poff[q] + pkb * 128, base + wave * 4096 + q * 1024, 16);
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int cw = 2 * wave + c;
-        const uint8_t* b = pbw[c] + (size_t)pkb * DN_BLK + lane * 16;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          to_lds(b + j * 1024, base + DN_A + cw * 4096 + j * 1024, 16);
-        to_lds(psw[c] + (size_t)pkb * 1024 + lane * 4, base + DN_A + DN_B + cw * 256, 4);
-      }
-      if (lane < 32)
-        to_lds((const uint8_t*)S.sa + psx + pkb * 4,
-               base + DN_A + DN_B + DN_SW + wave * 128, 4);
-      if (++pkb == KB && pi + 1 < nitems) {
-        pkb = 0;
-        p_enter(++pi);
-      }
+      for (int j = 0; j < DN_LOADS; ++j) dma(j, base);
+      advance();
     };
 
     f32x4 acc[8][4];
@@ -315,82 +327,126 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
     };
 
     // ---- pipeline -----------------------------------------------------------
+    // group mi of a step: its activation fragment (with an fp4 A operand
+    // the fp8 B operand's two 16-byte halves are K bytes [16 lg, +16) and
+    // [64 + 16 lg, +16) of the step, the streaming kernel's fragment for
+    // this format) and the row's activation scale
+    struct Frag {
+      v8i x;
+      int sx;
+    };
+    // a step's weight fragments (the wave's four subtiles) and scales
+    // (four named vectors: held in an array, the fragments passed between
+    // steps went through the stack)
+    struct WFrag {
+      u32x4 w0, w1, w2, w3;
+      uint32_t sw;
+    };
+    auto wfrag_at = [&](const uint8_t* stage) __attribute__((always_inline)) {
+      const uint8_t* B = stage + DN_A + wave * 4096 + lane * 16;
+      const uint8_t* SW = stage + DN_A + DN_B + wave * 256;
+      WFrag g;
+      g.w0 = *(const u32x4*)(B);
+      g.w1 = *(const u32x4*)(B + 1024);
+      g.w2 = *(const u32x4*)(B + 2048);
+      g.w3 = *(const u32x4*)(B + 3072);
+      g.sw = (uint32_t)*(const uint16_t*)(SW + lane * 2) |
+             ((uint32_t)*(const uint16_t*)(SW + 128 + lane * 2) << 16);
+      return g;
+    };
+    auto frag_at = [&](const uint8_t* stage, int mi) __attribute__((always_inline)) {
+      const int r = mi * 16 + lc;
+      const u32x4 x0 = *(const u32x4*)(stage + a_off(r, lg));
+      const u32x4 x1 = *(const u32x4*)(stage + a_off(r, 4 + lg));
+      const float* SX = (const float*)(stage + DN_A + DN_B + DN_SW);
+      Frag f;
+      f.x = (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                  (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+      f.sx = (int)e8m0_of(SX[r]);
+      return f;
+    };
+    // A stage is ready once every loader has waited for its own loads of
+    // the stage (vmcnt; the loads of the stage after it may stay in flight:
+    // `newer`) and the waves meet at a barrier; each wave's LDS reads are
+    // complete by then, so the barrier also ends the reads of the stage
+    // that the loads issued after it overwrite.
+    auto stage_ready = [&](bool newer) __attribute__((always_inline)) {
+      if (newer) wait_vm<DN_LOADS>();
+      else wait_vm<0>();
+      bar_lds();
+    };
+
     // step s on stage J = s % 3 (J a compile-time constant), K step ckb of
-    // item ci; issues stage s + 2 into (J + 2) % 3. The cursors are passed
-    // by value: kept in memory by reference, the barrier's memory clobber
-    // would make every step reload them and wait for all loads in flight.
+    // item ci, entered with group 0's fragment of the stage; the loaders
+    // spread stage s + 2's loads over groups 0-6 (in one burst after the
+    // barrier, they held the loader waves at the address unit while the
+    // others waited at the next barrier). Stage s + 1 is made ready before
+    // group 7's MFMAs, whose issue then covers the barrier and the next
+    // step's first fragment reads; returns that fragment. The cursors are
+    // passed by value: kept in memory, the barrier's memory clobber would
+    // make every step reload them.
+    Frag nf;    // the next step's first activation fragment
+    WFrag ng;   // and its weight fragments
     auto step = [&](auto J, int s, int ci, int ckb) __attribute__((always_inline)) {
       constexpr int j = decltype(J)::value;
       uint8_t* const cur = j == 0 ? stg0 : (j == 1 ? stg1 : stg2);
+      uint8_t* const nst = j == 0 ? stg1 : (j == 1 ? stg2 : stg0);
       uint8_t* const nxt = j == 0 ? stg2 : (j == 1 ? stg0 : stg1);
-      // stage s's loads: stage s + 1's (issued after them, if any) may
-      // remain in flight; epilogue stores issued before those are waited
-      // for as well
-      if (s + 1 < total_steps) wait_vm<DN_LOADS>();
-      else wait_vm<0>();
-      bar_only();
       const bool last = ckb + 1 == KB;
-      if (!last && s + 2 < total_steps) issue(nxt);
-      const uint8_t* A = cur;
-      const uint8_t* B = cur + DN_A + wave * 4096;
-      const uint8_t* SW = cur + DN_A + DN_B + wave * 256;
-      const float* SX = (const float*)(cur + DN_A + DN_B + DN_SW);
-      u32x4 wf[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) wf[q] = *(const u32x4*)(B + q * 1024 + lane * 16);
-      const uint32_t sw = (uint32_t)*(const uint16_t*)(SW + lane * 2) |
-                          ((uint32_t)*(const uint16_t*)(SW + 128 + lane * 2) << 16);
-      // group mi of the step: its activation fragment (with an fp4 A
-      // operand the fp8 B operand's two 16-byte halves are K bytes
-      // [16 lg, +16) and [64 + 16 lg, +16) of the step, the streaming
-      // kernel's fragment for this format) against the four weight subtiles
-      struct Frag {
-        v8i x;
-        int sx;
-      };
-      auto load_frag = [&](int mi) __attribute__((always_inline)) {
-        const int r = mi * 16 + lc;
-        const u32x4 x0 = *(const u32x4*)(A + a_off(r, lg));
-        const u32x4 x1 = *(const u32x4*)(A + a_off(r, 4 + lg));
-        Frag f;
-        f.x = (v8i){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
-                    (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-        f.sx = (int)e8m0_of(SX[r]);
-        return f;
-      };
+      const bool spread = loader && !last && s + 2 < total_steps;
+      Frag cur_f = nf;
+      const WFrag g = ng;
       auto mfmas = [&](int mi, const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const v8i wv = {(int)wf[q].x, (int)wf[q].y, (int)wf[q].z, (int)wf[q].w,
-                          0, 0, 0, 0};
+          const u32x4 w = q == 0 ? g.w0 : (q == 1 ? g.w1 : (q == 2 ? g.w2 : g.w3));
+          const v8i wv = {(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
           acc[mi][q] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wv, f.x, acc[mi][q], 4, 0, 0, (int)((sw >> (8 * q)) & 0xFF), 0, f.sx);
+              wv, f.x, acc[mi][q], 4, 0, 0, (int)((g.sw >> (8 * q)) & 0xFF), 0, f.sx);
         }
       };
-      // all eight groups, branch-free (the MFMAs of padding rows included:
-      // a per-group branch keeps the compiler from issuing group mi + 1's
-      // LDS reads ahead of group mi's MFMAs, and two code paths do not fit
-      // the registers); the scheduling barriers keep the compiler from
-      // hoisting every group's reads at once
-      {
-        Frag cur_f = load_frag(0);
+      // the groups' MFMAs (padding groups skipped; the next group's LDS
+      // reads are issued first either way), the scheduling barriers keeping
+      // the compiler from hoisting every group's reads at once
+      const int ngrp = __builtin_amdgcn_readfirstlane((desc[ci].w + 15) >> 4);
 #pragma unroll
-        for (int mi = 0; mi < 8; ++mi) {
-          Frag nx = cur_f;
-          if (mi < 7) nx = load_frag(mi + 1);
-          mfmas(mi, cur_f);
-          __builtin_amdgcn_sched_barrier(0);
-          cur_f = nx;
+      for (int mi = 0; mi < 8; ++mi) {
+        Frag nx = cur_f;
+        if (mi < 7) {
+          nx = frag_at(cur, mi + 1);
+          if (spread) {
+            dma(2 * mi, nxt);
+            dma(2 * mi + 1, nxt);
+          }
+        } else if (s + 1 < total_steps) {
+          // loads newer than stage s + 1's: stage s + 2's, when this step
+          // spread them (and for the other waves, only stores)
+          stage_ready(spread || !loader);
+          nx = frag_at(nst, 0);
         }
+        if (mi < ngrp) mfmas(mi, cur_f);
+        // the next step's weight fragments, read once group 7's MFMAs (the
+        // last readers of this step's) are issued
+        if (mi == 7 && s + 1 < total_steps && !last) ng = wfrag_at(nst);
+        __builtin_amdgcn_sched_barrier(0);
+        cur_f = nx;
       }
+      nf = cur_f;
+      if (spread) advance();
       if (last) {
         epilogue(ci);
         if (s + 2 < total_steps) issue(nxt);
+        // (read after the epilogue: kept across it, the fragments would not
+        // fit the registers)
+        if (s + 1 < total_steps) ng = wfrag_at(nst);
       }
     };
     if (loader) p_enter(0);
     issue(stg0);
     if (total_steps > 1) issue(stg1);
+    stage_ready(total_steps > 1 || !loader);
+    nf = frag_at(stg0, 0);
+    ng = wfrag_at(stg0);
     int ci = 0, ckb = 0;
     auto adv = [&]() __attribute__((always_inline)) {
       if (++ckb == KB) {
