@@ -254,6 +254,15 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   const int xbeg = (int)((long)total * xcd / 8);
   const int xend = (int)((long)total * (xcd + 1) / 8);
   const int nall = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
+  // Gate/up: the upper half of each XCD's workgroups (those dealt one item
+  // fewer when the count does not divide) start ~16K cycles later, so that
+  // the workgroups stream and finish items in two phases rather than all
+  // in step: at C2 (8-9 items of 16 steps per workgroup) the launch takes
+  // 258 -> 243-247 us. Measured without effect: the same for the down
+  // projection or the dense MXFP4 kernel, three or eight phases, and the
+  // delay after the first loads.
+  if (MODE == 0 && nall >= 2 && 2 * jx >= nx)
+    for (int z = 0; z < 8; ++z) __builtin_amdgcn_s_sleep(32);
   // The items are taken ST_MAX_ITEMS at a time (the LDS holds the row
   // indices and weights of that many): one pipeline per chunk, so that the
   // grid stays at one workgroup per CU whatever the item count.
