@@ -19,10 +19,11 @@
 //   stages, loads two steps ahead. The activation rows are XOR-swizzled by
 //   row, which keeps the fragment reads free of bank conflicts (the
 //   streaming kernel's LDS was in conflict stalls 30% of its cycles at C4).
-// * All eight 16-row groups of a step run branch-free, group mi + 1's LDS
-//   reads issued before group mi's MFMAs (padding rows included: a
-//   per-group branch keeps the compiler from issuing reads ahead, and a
-//   second code path for partial tiles does not fit the registers).
+// * Group mi + 1's LDS reads are issued before group mi's MFMAs; the MFMAs
+//   of padding row groups are skipped by a uniform branch around the MFMAs
+//   alone (around the reads too, it kept the compiler from issuing them
+//   ahead; a second code path for partial tiles does not fit the
+//   registers).
 //
 // Synchronization: a stage is ready when each loader wave has waited for
 // its own loads of it (vmcnt, counted per wave: fourteen loads per stage)
@@ -38,7 +39,11 @@
 // barrier (the address unit takes them one after another) and ~20% at the
 // barrier; issuing the loads between the groups' MFMAs made the step
 // slower. Loading by waves 0-3 only (the other wave on each SIMD computes
-// meanwhile) took the C4 gate/up launch from 2.16 to 2.07 ms.
+// meanwhile) took the C4 gate/up launch from 2.16 to 2.07 ms; spreading the
+// loaders' loads over their MFMA groups, one load for the weight scales,
+// the early barrier and the next step's fragments read under the last
+// group's MFMAs, to 1.94 ms (3445 cycles per step against 2048 of MFMA
+// issue per SIMD).
 #include <type_traits>
 
 #include "launch.h"
