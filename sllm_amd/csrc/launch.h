@@ -19,10 +19,21 @@ int router_ksplit(int T, int H);
 int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
                        int T, int E, int H, hipStream_t st, int ks = 1,
                        int* zero = nullptr, long zero_n = 0);
+// Per-token activation quantization run by the softmax routing launch
+// (act_quant.h; x == nullptr: none).
+struct ActQuant {
+  const uint16_t* x;
+  int H, pow2;
+  uint8_t* q;
+  float* s;
+  const uint16_t* gate_w;
+  float* gate_out;
+};
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st,
                          int ks = 1, float* gate = nullptr,
-                         int* chunk_hist = nullptr);
+                         int* chunk_hist = nullptr,
+                         const ActQuant* aq = nullptr);
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).

@@ -296,6 +296,17 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   SLLM_REQUIRE(nfcnt < (1L << 31), "sllm_moe_qwen_forward: too many counters");
   const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool small_route = p.decode && route_permute_small_fits(T, E, k);
+  // Prefill: the softmax routing launch also quantizes each token's row
+  // (and forms the shared-expert gate), in place of the activation-quant
+  // launch (one wave per token in both; C2: 11.8 + 11.3 -> 19.8 us).
+  const bool aq_fused = !p.decode && !one_expert && !small_route;
+  ActQuant aq{};
+  if (aq_fused) {
+    aq.x = (const uint16_t*)a->x; aq.H = H; aq.pow2 = 0;
+    aq.q = (uint8_t*)(ws + p.xq); aq.s = (float*)(ws + p.sx);
+    aq.gate_w = sh ? (const uint16_t*)a->sgl : nullptr;
+    aq.gate_out = sh ? gate : nullptr;
+  }
   bool gate_done = false;
   if (one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM, 0);
@@ -339,7 +350,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
           launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
-                               gate_fin, chunk_hist));
+                               gate_fin, chunk_hist, aq_fused ? &aq : nullptr));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st,
@@ -446,8 +457,10 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
     float* hs = (float*)(ws + p.hs);
     uint16_t* y = (uint16_t*)(ws + p.y);
     STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
-          launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
-          sh ? (const uint16_t*)a->sgl : nullptr, gate, st));
+          aq_fused ? 0
+                   : launch_act_quant((const uint16_t*)a->x, T, H, 0, xq, sx,
+                                      sh ? (const uint16_t*)a->sgl : nullptr,
+                                      gate, st));
     uint16_t* y_sh = nullptr;
     uint8_t* hq_sh = nullptr;
     float* hs_sh = nullptr;

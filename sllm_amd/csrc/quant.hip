@@ -1,85 +1,24 @@
 // Activation quantization and synthetic-weight quantizers.
 //
 // act_quant restates the upstream quantization point that the reference's
-// numpy oracles leave out (ref/hf_sources/dsv4/kernel.py:40-125): per row
-// and per 128 columns, amax = max(|x|, 1e-4), s = amax * fp32(1/448) (or
-// its power-of-two ceiling, the ue8m0 format, :22-37), q = e4m3(clamp(x/s,
-// +-448)) with round-to-nearest-even. Bit-exact with oracle/quant.py: the
-// same fp32 operations in the same order (IEEE division, hardware RNE
-// conversion).
-//
-// The shared-expert gate of the Qwen layer, sigmoid(x . W_sg)
-// (ref/qwen4_exp.py:180-183), needs one dot product per token over the same
-// row, so it is fused here rather than paid as a separate pass over x.
+// numpy oracles leave out (act_quant.h: the per-row body, also run by the
+// prefill softmax routing launch). The shared-expert gate of the Qwen layer,
+// sigmoid(x . W_sg) (ref/qwen4_exp.py:180-183), needs one dot product per
+// token over the same row, so it is fused here rather than paid as a
+// separate pass over x.
+#include "act_quant.h"
 #include "launch.h"
 
 namespace sllm {
 
-__device__ __forceinline__ float pow2_ceil(float v) {
-  uint32_t b = __float_as_uint(v);
-  int e = (int)((b >> 23) & 0xFF) - 127 + ((b & 0x7FFFFF) ? 1 : 0);
-  return __uint_as_float((uint32_t)(e + 127) << 23);
-}
-
-// One wave per row, 4 rows per workgroup. Lane group g = lane/16 takes one
-// 128-column block at a time; its 16 lanes load 8 bf16 each (16 bytes).
-// q == nullptr computes only the gate (the decode path keeps x in fp32).
+// One wave per row, 4 rows per workgroup. q == nullptr computes only the
+// gate (the decode path keeps x in fp32).
 __global__ __launch_bounds__(256) void act_quant_kernel(
-    const uint16_t* __restrict__ x, int T, int H, int pow2,
-    uint8_t* __restrict__ q, float* __restrict__ s,
-    const uint16_t* __restrict__ gate_w, float* __restrict__ gate_out) {
-  const int lane = threadIdx.x & 63;
+    const uint16_t* x, int T, int H, int pow2, uint8_t* q, float* s,
+    const uint16_t* gate_w, float* gate_out) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int g = lane >> 4, li = lane & 15;
-  const int nblk = H / 128;
-  const uint16_t* row = x + (size_t)t * H;
-  float gdot = 0.f;
-  for (int b0 = 0; b0 < nblk; b0 += 4) {
-    const int blk = b0 + g;
-    const bool on = blk < nblk;
-    const int col = blk * 128 + li * 8;
-    float v[8];
-    float amax = 0.f;
-    if (on) {
-      uint4 raw = *(const uint4*)(row + col);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(w4[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      if (gate_w) {
-        uint4 gr = *(const uint4*)(gate_w + col);
-        const uint32_t g4[4] = {gr.x, gr.y, gr.z, gr.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          gdot += v[2 * i] * __uint_as_float(g4[i] << 16);
-          gdot += v[2 * i + 1] * __uint_as_float(g4[i] & 0xFFFF0000u);
-        }
-      }
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
-    if (on && q) {
-      float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
-      if (pow2) sc = pow2_ceil(sc);
-      float y[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(v[i] / sc, -448.f), 448.f);
-      uint2 packed;
-      packed.x = f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
-      packed.y = f32x4_to_e4m3(y[4], y[5], y[6], y[7]);
-      *(uint2*)(q + (size_t)t * H + col) = packed;
-      if (li == 0) s[(size_t)t * nblk + blk] = sc;
-    }
-  }
-  if (gate_w) {
-    gdot = wave_sum(gdot);
-    if (lane == 0) gate_out[t] = sigmoid_f32(gdot);
-  }
+  act_quant_row(x, t, H, pow2, q, s, gate_w, gate_out);
 }
 
 int launch_act_quant(const uint16_t* x, int T, int H, int pow2, uint8_t* q,
