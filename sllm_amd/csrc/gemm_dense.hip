@@ -47,15 +47,17 @@
 #include <type_traits>
 
 #include "launch.h"
+#include "lds_dma.h"
 
 namespace sllm {
 
 namespace {
 
+using namespace dma;
+
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_void;
 
 constexpr int DN_BM = 128;  // rows per tile (the permutation's prefill tiles)
 constexpr int DN_WAVES = 8;
@@ -69,49 +71,6 @@ constexpr int DN_SX = DN_BM * 4;             // activation scales (fp32)
 constexpr int DN_STAGE = DN_A + DN_B + DN_SW + DN_SX;
 constexpr int DN_BLK = 16384;                // packed fp4 block (slab, K step)
 constexpr int DN_LOADS = 14;                 // direct-to-LDS loads per loader wave per stage
-
-// LDS offset of 16-byte chunk c (K bytes [16 c, +16)) of tile row r: the
-// chunk index is XOR-swizzled with the row, so that the 16 rows an MFMA
-// fragment read touches spread over the banks.
-__device__ __forceinline__ int a_off(int r, int c) {
-  return r * 128 + ((c ^ (r & 7)) << 4);
-}
-
-__device__ __forceinline__ uint32_t e8m0_of(float pow2) {
-  return (__float_as_uint(pow2) >> 23) & 0xFF;
-}
-
-// s_waitcnt for the vector-memory counter alone (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier that orders memory operations in the compiler but
-// waits for nothing in the hardware; `lds` also waits for this wave's LDS
-// operations first (for data exchanged through LDS).
-__device__ __forceinline__ void bar_only() { asm volatile("s_barrier" ::: "memory"); }
-__device__ __forceinline__ void bar_lds() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Direct-to-LDS load of 16 (or 4) bytes per lane: lane i's bytes land at
-// l + 16 i (4 i); l is wave-uniform. Written as inline assembly so that the
-// compiler, which does not see the LDS write, adds no wait of its own
-// before the step's LDS reads (it would wait for every load in flight,
-// the prefetched stages included); the steps wait for their own stage
-// with explicit vmcnt waits instead.
-__device__ __forceinline__ void to_lds(const void* g, uint8_t* l, int bytes) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void)l);
-  if (bytes == 16)
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(g), "s"(m0) : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
-                 :: "v"(g), "s"(m0) : "memory", "m0");
-}
 
 template <int MODE>
 __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(

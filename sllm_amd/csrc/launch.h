@@ -164,6 +164,12 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 // average more than one 128-row tile (wreuse): one routed segment with a
 // tile table, N a multiple of 256 (gate/up) or 512 (down).
 bool dense_fits(int bf, int mode, const SegDesc& s0, const SegDesc* s1);
+// FP8 variant (gemm_dense8.hip): one segment, routed (tile table) or
+// identity rows; f32s: fp32 block scales (else powers of two, applied as
+// e8m0 MFMA scales); N a multiple of 128 (gate/up) or 256 (down), K <= 8192.
+bool dense8_fits(int mode, const SegDesc& s0);
+int launch_dense8(int mode, const SegDesc& s0, int f32s, int topk, float limit,
+                  int pow2, hipStream_t st, int num_cus);
 int launch_dense(int mode, const SegDesc& s0, int topk, float limit, int pow2,
                  hipStream_t st, int num_cus);
 // Decode variant over the same packed weights: bm-row tiles (16 or 32; the

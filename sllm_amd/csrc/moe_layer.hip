@@ -51,6 +51,9 @@ static int weights_reused(long rows, long experts, int bm) {
   return rows > (long)bm * experts ? 1 : 0;
 }
 
+static int dense8_mode();
+static int device_cus();
+
 static size_t take(size_t& cur, size_t bytes) {
   size_t at = cur;
   cur += align_up(bytes ? bytes : 1, 256);
@@ -483,8 +486,19 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s1.wp = (const uint8_t*)a->sgu_packed; s1.s0 = a->sg_s; s1.s1 = a->su_s;
       s1.N = Is; s1.K = H; s1.hq = hq_sh; s1.hs = hs_sh;
       const long up1 = (long)p.max_tiles * (I / 128) + sh_rt * (Is / 128);
+      // SLLM_MOE_DENSE8=2 with experts averaging more than one row tile:
+      // the compute-dense FP8 kernel, one launch per segment (the shared
+      // expert's too once its rows fill more than one tile).
+      const bool rdense = dense8_mode() == 2 && r1.wreuse;
+      const bool sdense = rdense && sh && T > PREFILL_BM;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-            launch_stream(0, 0, r1, sh ? &s1 : nullptr, k, 0.f, 0, up1, st));
+            rdense && dense8_fits(0, r1)
+                ? launch_dense8(0, r1, 1, k, 0.f, 0, st, device_cus()) ||
+                      (sh && (sdense && dense8_fits(0, s1)
+                                  ? launch_dense8(0, s1, 1, k, 0.f, 0, st, device_cus())
+                                  : launch_stream(0, 0, s1, nullptr, k, 0.f, 0,
+                                                  sh_rt * (Is / 128), st)))
+                : launch_stream(0, 0, r1, sh ? &s1 : nullptr, k, 0.f, 0, up1, st));
       SegDesc r2{}, s2{};
       r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
       r2.a = hq; r2.sa = hs; r2.sorted_idx = sorted; r2.gather = 0;
@@ -496,7 +510,13 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s2.K = Is; s2.row_w = gate; s2.y = y_sh;
       const long up2 = (long)p.max_tiles * (H / 256) + sh_rt * (H / 256);
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-            launch_stream(0, 1, r2, sh ? &s2 : nullptr, k, 0.f, 0, up2, st));
+            rdense && dense8_fits(1, r2)
+                ? launch_dense8(1, r2, 1, k, 0.f, 0, st, device_cus()) ||
+                      (sh && (sdense && dense8_fits(1, s2)
+                                  ? launch_dense8(1, s2, 1, k, 0.f, 0, st, device_cus())
+                                  : launch_stream(0, 1, s2, nullptr, k, 0.f, 0,
+                                                  sh_rt * (H / 256), st)))
+                : launch_stream(0, 1, r2, sh ? &s2 : nullptr, k, 0.f, 0, up2, st));
       // the shared expert ran inside the two launches above
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
@@ -690,6 +710,20 @@ static int device_cus() {
 // in prefill over packed MXFP4 weights when the experts average more than
 // one 128-row tile. SLLM_MOE_DENSE=0 in the environment keeps the
 // streaming kernel (same arithmetic, for comparisons).
+// The compute-dense FP8 kernel (gemm_dense8.hip) where it measured faster:
+// the DeepSeek shared expert's gate/up at more than one row tile (C4:
+// 327 -> 287 us). Slower where not used: that expert's down projection
+// (174 -> 178 us) and the skewed Qwen layer's routed projections (C5
+// gate/up 541 -> 593 us, down 379 -> 521 us: its 256-column items, all
+// that three LDS stages hold with fp8 weights, leave the per-step barrier
+// and load issue larger than the step's MFMAs). SLLM_MOE_DENSE8=0 keeps
+// every FP8 projection on the streaming kernel, =2 runs it wherever it
+// fits (both give the same bits).
+static int dense8_mode() {
+  const char* v = std::getenv("SLLM_MOE_DENSE8");
+  return v && v[0] == '0' ? 0 : (v && v[0] == '2' ? 2 : 1);
+}
+
 static bool dense_layer(const sllm_moe_ds_args* a) {
   const char* env = getenv("SLLM_MOE_DENSE");
   if (env && env[0] == '0') return false;
@@ -891,17 +925,25 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
         s1.a = xq; s1.sa = sx; s1.total_rows = T;
         s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
         s1.N = Is; s1.K = H; s1.hq = hq_sh; s1.hs = hs_sh;
+        // the shared expert's gate/up on the compute-dense FP8 kernel
+        // (power-of-two scales as e8m0 MFMA scales) when its rows fill more
+        // than one tile
+        const bool sdense = dense8_mode() >= 1 && T > PREFILL_BM;
         STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
-              launch_stream(1, 0, s1, nullptr, k, L, 1, sh_rt * (Is / 128),
-                            st));
+              sdense && dense8_fits(0, s1)
+                  ? launch_dense8(0, s1, 0, k, L, 1, st, device_cus())
+                  : launch_stream(1, 0, s1, nullptr, k, L, 1, sh_rt * (Is / 128),
+                                  st));
         SegDesc s2{};
         s2.wreuse = weights_reused(T, 1, PREFILL_BM);
         s2.a = hq_sh; s2.sa = hs_sh; s2.total_rows = T;
         s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
         s2.N = H; s2.K = Is; s2.y = y_sh;
         STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
-              launch_stream(1, 1, s2, nullptr, k, 0.f, 1, sh_rt * (H / 256),
-                            st));
+              dense8_mode() == 2 && T > PREFILL_BM && dense8_fits(1, s2)
+                  ? launch_dense8(1, s2, 0, k, 0.f, 1, st, device_cus())
+                  : launch_stream(1, 1, s2, nullptr, k, 0.f, 1, sh_rt * (H / 256),
+                                  st));
       }
     } else {
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,

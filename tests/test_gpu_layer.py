@@ -150,6 +150,30 @@ def test_qwen_skewed_with_empty_experts():
     assert rel < 3e-3
 
 
+@pytest.mark.parametrize("T,E,k,shared", [(1024, 8, 2, True), (777, 16, 4, True),
+                                          (2048, 64, 6, False)])
+def test_qwen_dense8_kernel_matches_stream(T, E, k, shared, monkeypatch):
+    """With SLLM_MOE_DENSE8=2, prefill whose experts average more than one
+    128-row tile (T k > 128 E) runs its FP8 projections (fp32 block scales)
+    on the compute-dense kernel (gemm_dense8.hip), the shared expert's too
+    when T > 128; SLLM_MOE_DENSE8=0 runs the same items on the streaming
+    kernel. The same MFMA per K step, the same rescale order and
+    epilogues: the outputs agree bit for bit, on every call, and match the
+    oracle. T=777 leaves partial tiles."""
+    x, W = qwen_fp8(seed=T + E, T=T, H=512, E=E, I=256, Is=256, shared=shared)
+    layer = qwen_layer(W, k)
+    monkeypatch.setenv("SLLM_MOE_DENSE8", "2")
+    y_dense, r = layer.forward(x, mode="prefill", return_routing=True)
+    for _ in range(3):  # the same bits on every call
+        np.testing.assert_array_equal(layer.forward(x, mode="prefill"), y_dense)
+    monkeypatch.setenv("SLLM_MOE_DENSE8", "0")
+    y_stream = layer.forward(x, mode="prefill")
+    np.testing.assert_array_equal(y_dense, y_stream)
+    want = qm.moe_layer_fp8(x, r["logits"], W, k)
+    rel, mabs, scale = _report("qwen dense8 prefill", y_dense, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+
+
 @pytest.mark.parametrize("packed", [True, False])
 @pytest.mark.parametrize("T,G,kg,L", [(200, 4, 2, 10.0), (256, 1, 1, 0.0)])
 def test_deepseek_prefill_small(T, G, kg, L, packed):
@@ -186,6 +210,30 @@ def test_deepseek_dense_kernel_matches_stream(T, L, monkeypatch):
     np.testing.assert_array_equal(y_dense, y_stream)
     want = dm.moe_layer_mxfp4(x, r["logits"], W, 8, L, "sigmoid", 2.5, 4, 2)
     rel, mabs, scale = _report("deepseek dense prefill", y_dense, want)
+    assert rel < 3e-3 and mabs < 0.05 * scale
+
+
+@pytest.mark.parametrize("T,force", [(1024, False), (300, False), (1024, True)])
+def test_deepseek_shared_dense8_matches_stream(T, force, monkeypatch):
+    """The DeepSeek shared expert (FP8 with power-of-two scales) runs its
+    gate/up on the compute-dense FP8 kernel once its T rows fill more than
+    one tile (its down projection too with SLLM_MOE_DENSE8=2), the scales
+    applied as e8m0 MFMA scales as in the streaming kernel: the same bits as
+    SLLM_MOE_DENSE8=0, and the oracle's result."""
+    x, W = deepseek_mxfp4(seed=T + 3, T=T, H=512, E=16, I=256, Is=256)
+    route = dict(n_group=4, topk_group=2, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=10.0)
+    layer = deepseek_layer(W, 8, **route)
+    if force:
+        monkeypatch.setenv("SLLM_MOE_DENSE8", "2")
+    y_dense, r = layer.forward(x, mode="prefill", return_routing=True)
+    for _ in range(2):
+        np.testing.assert_array_equal(layer.forward(x, mode="prefill"), y_dense)
+    monkeypatch.setenv("SLLM_MOE_DENSE8", "0")
+    y_stream = layer.forward(x, mode="prefill")
+    np.testing.assert_array_equal(y_dense, y_stream)
+    want = dm.moe_layer_mxfp4(x, r["logits"], W, 8, 10.0, "sigmoid", 2.5, 4, 2)
+    rel, mabs, scale = _report("deepseek shared dense8", y_dense, want)
     assert rel < 3e-3 and mabs < 0.05 * scale
 
 
