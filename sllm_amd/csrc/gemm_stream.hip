@@ -251,24 +251,33 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
   const int total = n0 + n1;
   const int nx = gridDim.x / 8;  // workgroups per XCD (grid is a multiple of 8)
   const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
+  // Items to XCDs. Weights through L2 (wreuse: an expert's row tiles share
+  // its weights): each XCD a contiguous range of the items, so that an
+  // expert's tiles meet in one L2. Streamed weights: XCD x takes chunks x,
+  // x + 8, ... of CB consecutive items (one routed row tile's column slabs,
+  // which share its gathered rows in L2), so that every XCD gets the same
+  // mix of items -- with contiguous ranges the last XCD got the shared
+  // expert's tiles, whose weights stay in L2, and finished early while the
+  // others streamed (C2 gate/up 244-247 -> 218-219 us; C5, where an
+  // expert's tiles then spread over the XCDs, 567 -> 580-588 us).
+  const bool ranges = S0.wreuse != 0;
+  const int CB = max(1, S0.N / NTW);
+  const int ncf = total / CB, crem = total % CB;
   const int xbeg = (int)((long)total * xcd / 8);
   const int xend = (int)((long)total * (xcd + 1) / 8);
-  const int nall = xend - xbeg > jx ? (xend - xbeg - jx + nx - 1) / nx : 0;
-  // Gate/up: the upper half of each XCD's workgroups (those dealt one item
-  // fewer when the count does not divide) start ~16K cycles later, so that
-  // the workgroups stream and finish items in two phases rather than all
-  // in step: at C2 (8-9 items of 16 steps per workgroup) the launch takes
-  // 258 -> 243-247 us. Measured without effect: the same for the down
-  // projection or the dense MXFP4 kernel, three or eight phases, and the
-  // delay after the first loads.
-  if (MODE == 0 && nall >= 2 && 2 * jx >= nx)
-    for (int z = 0; z < 8; ++z) __builtin_amdgcn_s_sleep(32);
+  const int xcount = ranges ? xend - xbeg
+                            : (ncf > xcd ? (ncf - xcd + 7) / 8 : 0) * CB +
+                                  (ncf % 8 == xcd ? crem : 0);
+  const int nall = xcount > jx ? (xcount - jx + nx - 1) / nx : 0;
   // The items are taken ST_MAX_ITEMS at a time (the LDS holds the row
   // indices and weights of that many): one pipeline per chunk, so that the
   // grid stays at one workgroup per CU whatever the item count.
   for (int cbase = 0; cbase < nall; cbase += ST_MAX_ITEMS) {
   const int nitems = min(ST_MAX_ITEMS, nall - cbase);
-  auto item_at = [&](int m) { return xbeg + jx + (cbase + m) * nx; };
+  auto item_at = [&](int m) {
+    const int q = jx + (cbase + m) * nx;  // the XCD's q-th item
+    return ranges ? xbeg + q : (xcd + 8 * (q / CB)) * CB + q % CB;
+  };
 
   // ---- phase 0: descriptors and gathered row indices -> LDS ---------------
   if (tid < nitems) {
