@@ -34,6 +34,36 @@ int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int ks = 1, float* gate = nullptr,
                          int* chunk_hist = nullptr,
                          const ActQuant* aq = nullptr);
+// Fused prefill router (softmax routing, router_topk_fits): per token t
+// and 128-expert tile y of the ny = ceil(E / 128) tiles, the tile's largest
+// logit m and sum of exp(l - m) at stat[2 (t ny + y)] (+1), and its topk
+// largest top-k keys, descending, at keys[(t ny + y) topk + j] (0 = none).
+// launch_router_topk writes them (logits: null, or also the logits for the
+// caller's copy) and zeroes zero_n ints at zero as launch_router_gemm.
+// With q it also quantizes the activations into q / s (the activation-quant
+// launch's layout and values), and with gate_w writes the shared-expert
+// gate sigmoid(x . gate_w) to gate_out. launch_route_merge routes from the
+// partials (filling chunk_hist as launch_route_softmax).
+// router_part_bytes / router_part_at: the arrays' size and places in one
+// buffer.
+struct RouterPart {
+  float* stat;
+  uint64_t* keys;
+  int topk;
+  uint8_t* q;
+  float* s;
+  const uint16_t* gate_w;
+  float* gate_out;
+};
+bool router_topk_fits(int T, int E, int topk, int H);
+size_t router_part_bytes(int T, int E, int topk);
+RouterPart router_part_at(char* base, int T, int E, int topk);
+int launch_router_topk(const uint16_t* x, const uint16_t* w, float* logits,
+                       int T, int E, int H, const RouterPart& rp,
+                       hipStream_t st, int* zero = nullptr, long zero_n = 0);
+int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
+                       float* w, int* ids, hipStream_t st,
+                       int* chunk_hist = nullptr);
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).

@@ -38,6 +38,7 @@ struct Plan {
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
   size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters
+  size_t rpart;  // Qwen prefill router partials (RouterPart), or 0
   size_t total;
 };
 
@@ -105,6 +106,8 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.pscr = take(c, permute_scratch_bytes(p.N, E));
   // shared-expert gate, then (split router) its ks_r partial slices
   p.gate = take(c, (size_t)(p.ks_r > 1 ? 1 + p.ks_r : 1) * T * 4);
+  if (!deepseek && !p.decode && need_logits && router_topk_fits(T, E, topk, H))
+    p.rpart = take(c, router_part_bytes(T, E, topk));
   if (p.decode) {
     if (!force_gemv) {  // the streamed kernels (the GEMV path does not split)
       const long rt = p.max_tiles;
@@ -332,13 +335,34 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   int* chunk_hist = route_hist ? (int*)(ws + p.pscr) : nullptr;
   const long hist_n =
       route_hist ? (long)((p.N + PERM_CHUNK - 1) / PERM_CHUNK) * E : 0;
+  // Prefill router fused with the first half of the routing: the router
+  // launch leaves each 128-expert tile's top-k and softmax partials, not
+  // the (T, E) logits (written only for the caller's copy), quantizes the
+  // activations and forms partial shared-expert gates from the x tiles it
+  // holds; the routing launch merges the partials.
+  const bool topk_router = !small_router && !one_expert && !small_route &&
+                           !a->logits_given && p.rpart != 0;
+  RouterPart rp{};
+  if (topk_router) {
+    rp = router_part_at(ws + p.rpart, T, E, k);
+    if (aq_fused) {
+      rp.q = aq.q;
+      rp.s = aq.s;
+      rp.gate_w = aq.gate_w;
+      rp.gate_out = aq.gate_out;
+    }
+  }
   if (!small_router && !one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
           a->logits_given ? 0
-                          : launch_router_gemm((const uint16_t*)a->x,
-                                               (const uint16_t*)a->router_w,
-                                               logits, T, E, H, st, 1,
-                                               chunk_hist, hist_n));
+          : topk_router
+              ? launch_router_topk((const uint16_t*)a->x,
+                                   (const uint16_t*)a->router_w,
+                                   a->logits_out ? logits : nullptr, T, E, H,
+                                   rp, st, chunk_hist, hist_n)
+              : launch_router_gemm((const uint16_t*)a->x,
+                                   (const uint16_t*)a->router_w, logits, T, E,
+                                   H, st, 1, chunk_hist, hist_n));
   }
   if (one_expert) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE, 0);
@@ -352,8 +376,11 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-          launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
-                               gate_fin, chunk_hist, aq_fused ? &aq : nullptr));
+          topk_router
+              ? launch_route_merge(rp, T, E, eps, w, ids, st, chunk_hist)
+              : launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
+                                     gate_fin, chunk_hist,
+                                     aq_fused ? &aq : nullptr));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st,

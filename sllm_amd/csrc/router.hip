@@ -20,6 +20,7 @@
 
 #include "act_quant.h"
 #include "launch.h"
+#include "lds_dma.h"
 #include "permute_fused.h"
 
 namespace sllm {
@@ -287,8 +288,9 @@ __device__ __forceinline__ void sort_desc(uint64_t (&k)[N]) {
   }
 }
 
-// Descending top-k of the wave's candidate keys (candidate e = lane + 64 i
-// in key[i]); lane j < topk returns pick j's key (0 past the candidates).
+// Descending top-k of the wave's candidate keys (key[i] of each lane, 0 =
+// none; keys are distinct, as each carries its expert id); lane j < topk
+// returns pick j's key (0 past the candidates).
 // Up to 8 keys per lane: each lane sorts its keys once, then every pick
 // is one wave maximum of the lanes' heads and a pop on the owning lane.
 // More keys per lane: every pick takes the lane maxima afresh.
@@ -314,7 +316,7 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
         best = wave_max_u64(hi == mhi ? key[0] : 0ull);
       }
       if (lane == kk) mine = best;
-      if (lane == (topk_key_id(best) & 63)) {
+      if (best != 0 && key[0] == best) {  // the one lane whose head it is
 #pragma unroll
         for (int i = 0; i + 1 < EPL; ++i) key[i] = key[i + 1];
         key[EPL - 1] = 0;
@@ -327,13 +329,340 @@ __device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
       for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
       best = wave_max_u64(best);
       if (lane == kk) mine = best;
-      const int e = topk_key_id(best);
 #pragma unroll
       for (int i = 0; i < EPL; ++i)
-        if (lane == (e & 63) && i == (e >> 6)) key[i] = 0;
+        if (best != 0 && key[i] == best) key[i] = 0;
     }
   }
   return mine;
+}
+
+// --------------------------------------------------------------------------
+// fused prefill router (softmax routing): router GEMM, each 128-expert
+// tile's top-k and softmax partials, activation quantization
+// --------------------------------------------------------------------------
+// Maximum / sum over each 16-lane row, in every lane of the row (the first
+// four DPP steps of wave_max / wave_sum: all lanes add in the same order).
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v, 0u));
+  v = max(v, dpp_u32<0x4E>(v, 0u));
+  v = max(v, dpp_u32<0x141>(v, 0u));
+  return max(v, dpp_u32<0x140>(v, 0u));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  const uint32_t ni = __float_as_uint(-INFINITY);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v), ni)));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x141>(__float_as_uint(v), ni)));
+  return fmaxf(v, __uint_as_float(dpp_u32<0x140>(__float_as_uint(v), ni)));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v), 0u));
+  return v + __uint_as_float(dpp_u32<0x140>(__float_as_uint(v), 0u));
+}
+
+// Descending top-k (topk <= 16) of two tokens' keys per 16-lane row (key[h],
+// 8 per lane, 0 = none, distinct): pick j of token h goes to kl[h][j]. The
+// two tokens' picks interleave (independent reduction chains). Every pick
+// is the maximum of the row's lane heads, found on the value halves; only
+// when some row holds its maximum value on two lanes (a ballot shows it)
+// are the low halves (the lower expert id) compared among them. The lane
+// holding the pick stores and pops it.
+__device__ __forceinline__ void row16_topk_keys2(uint64_t (&key)[2][8],
+                                                 int topk, uint64_t* kl0,
+                                                 uint64_t* kl1) {
+  sort_desc<8>(key[0]);
+  sort_desc<8>(key[1]);
+  for (int kk = 0; kk < topk; ++kk) {
+    uint32_t hi[2], mhi[2];
+    bool own[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) hi[h] = (uint32_t)(key[h][0] >> 32);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) mhi[h] = row16_max_u32(hi[h]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) own[h] = hi[h] == mhi[h];
+    if (__popcll(__ballot(own[0])) != 4 || __popcll(__ballot(own[1])) != 4) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t mlo = row16_max_u32(own[h] ? (uint32_t)key[h][0] : 0u);
+        own[h] = own[h] && (uint32_t)key[h][0] == mlo;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (own[h]) {
+        (h ? kl1 : kl0)[kk] = key[h][0];
+#pragma unroll
+        for (int i = 0; i < 7; ++i) key[h][i] = key[h][i + 1];
+        key[h][7] = 0;
+      }
+    }
+  }
+}
+
+constexpr int RT_XB = RG_TT * 256;                 // x chunk: 64 rows x 256 B
+constexpr int RT_WB = RG_TE * 256;                 // W chunk: 128 rows x 256 B
+constexpr int RT_STAGE = RT_XB + RT_WB;            // 48 KB, three stages
+constexpr int RT_LOADS = RT_STAGE / (512 * 16);    // 6 loads / thread / stage
+constexpr int RT_GATE_MAX = 4096;                  // gate weights in LDS
+constexpr int RG_LT = 132;  // row stride (floats) of the tile's logits in LDS
+
+// LDS byte offset of 16-byte chunk c (columns [8 c, +8)) of row r of a
+// 256-byte-row tile: the chunk index is XOR-swizzled with the row's low
+// four bits, so the 16 rows an MFMA fragment read takes (one chunk of
+// each) fall on 16 different bank groups.
+__device__ __forceinline__ int rt_off(int r, int c) {
+  return r * 256 + ((c ^ (r & 15)) << 4);
+}
+
+// Fused prefill router (RouterPart): workgroup (bx, y) computes the logits
+// of tokens [64 bx, +64) x experts [128 y, +128) as router_gemm_kernel's
+// waves do (2 x 4 waves of 32 x 32, MFMA 16x16x32 bf16), with the operands
+// brought into LDS by direct-to-LDS loads: three 48 KB stages, two K chunks
+// in flight ahead of the one multiplied, every thread issuing six 16-byte
+// loads per stage (slot p = 512 j + tid of the stage holds x row p / 16 for
+// p < 1024, else W row (p - 1024) / 16, chunk (p % 16) ^ (row % 16)).
+//
+// Activation quantization (rp.q): chunk kc of the x tile is quantization
+// block kc of each row (act_quant.h: the same operations, so the same
+// codes and scales); tile column y quantizes rows [qr0, qr1) (its share,
+// 64 / ny) of every chunk while the chunk is in LDS: x is not read again
+// and every step gets the same share. A 16-lane row per x row, 8 columns
+// per lane. rp.gate_w: the same lanes form those rows' shared-expert gate
+// logits (gate weights copied to LDS once), each lane adding its columns'
+// products chunk by chunk, then the row's lanes (row16_sum);
+// gate_out[t] = sigmoid(logit).
+//
+// Epilogue: the tile's logits go to LDS (logits, when not null, also gets
+// them for the caller's copy); each wave takes 8 tokens, two per 16-lane
+// row (row lane r holds experts e0 + r + 16 i, i < 8): the tile's maximum
+// m, sum of exp(l - m) and top-k keys (row16_topk_keys2). The sum takes
+// the hardware exponential (__expf): it only normalises the probabilities,
+// whose scale cancels in the weights p_j / (sum of the picks' p); the
+// picks' own probabilities take expf.
+__global__ __launch_bounds__(512, 1) void router_topk_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    float* __restrict__ logits, int T, int E, int H, int* __restrict__ zero,
+    long zero_n, RouterPart rp) {
+  __shared__ __attribute__((aligned(16))) uint8_t stg0[RT_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stg1[RT_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stg2[RT_STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t gsl[RT_GATE_MAX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  {  // the permutation's chunk histograms, filled by the routing launch
+    const long nthr = (long)gridDim.x * gridDim.y * 512;
+    for (long i = ((long)blockIdx.y * gridDim.x + blockIdx.x) * 512 + tid;
+         i < zero_n; i += nthr)
+      zero[i] = 0;
+  }
+  const int t0 = blockIdx.x * RG_TT, e0 = blockIdx.y * RG_TE;
+  const int nk = H / RG_KC;
+  auto stage = [&](int kc) __attribute__((always_inline)) -> uint8_t* {
+    const int sidx = kc % 3;
+    return sidx == 0 ? stg0 : sidx == 1 ? stg1 : stg2;
+  };
+  const uint16_t* src[RT_LOADS];
+#pragma unroll
+  for (int j = 0; j < RT_LOADS; ++j) {
+    const int p = 512 * j + tid;
+    if (p < RT_XB / 16) {
+      const int r = p >> 4, c = (p & 15) ^ (r & 15);
+      src[j] = x + (size_t)min(t0 + r, T - 1) * H + c * 8;
+    } else {
+      const int q = p - RT_XB / 16, r = q >> 4, c = (q & 15) ^ (r & 15);
+      src[j] = w + (size_t)min(e0 + r, E - 1) * H + c * 8;
+    }
+  }
+  auto issue = [&](int kc) __attribute__((always_inline)) {
+    uint8_t* base = stage(kc) + wave * 1024;
+#pragma unroll
+    for (int j = 0; j < RT_LOADS; ++j)
+      dma::to_lds(src[j] + kc * RG_KC, base + j * 8192, 16);
+  };
+  issue(0);
+  if (nk > 1) issue(1);
+  const bool quant_on = rp.q != nullptr, gate_on = rp.gate_w != nullptr;
+  if (gate_on) {  // visible to every wave after the first step's barrier
+    for (int i = tid * 8; i < H; i += 512 * 8)
+      *(u32x4*)(gsl + i) = *(const u32x4*)(rp.gate_w + i);
+  }
+  const int lr = lane & 15, lg = lane >> 4;
+  const int wm = wave >> 2, we = wave & 3;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int rpy = (RG_TT + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int qr0 = min(RG_TT, (int)blockIdx.y * rpy), qr1 = min(RG_TT, qr0 + rpy);
+  const int qslot = tid >> 4, q16 = tid & 15;
+  float gdot[2] = {0.f, 0.f};
+  // a step's quantized rows are stored at the start of the next step,
+  // before that step's loads: the loads then remain the newest memory
+  // operations whenever a step waits, so each wait is for its own stage
+  uint2 qpk[2];
+  float qsc[2];
+  int qkc = -1;
+  auto flush = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int r = qr0 + qslot + 32 * ps;
+      if (qkc >= 0 && r < qr1 && t0 + r < T) {
+        const int t = t0 + r;
+        *(uint2*)(rp.q + (size_t)t * H + qkc * RG_KC + q16 * 8) = qpk[ps];
+        if (q16 == 0) rp.s[(size_t)t * (H / RG_KC) + qkc] = qsc[ps];
+      }
+    }
+  };
+  for (int kc = 0; kc < nk; ++kc) {
+    // this thread's loads of chunk kc are done once at most the six of
+    // chunk kc + 1 are outstanding; the barrier makes every thread's done
+    if (kc + 1 < nk) dma::wait_vm<RT_LOADS>();
+    else dma::wait_vm<0>();
+    dma::bar_lds();
+    if (quant_on) flush();
+    // stage (kc + 2) % 3 was last read in step kc - 1, which every wave
+    // finished before the barrier
+    if (kc + 2 < nk) issue(kc + 2);
+    const uint8_t* sx = stage(kc);
+    const uint8_t* sw = sx + RT_XB;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 a[2], bb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *(const bf16x8*)(sx + rt_off(wm * 32 + i * 16 + lr, q * 4 + lg));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bb[j] = *(const bf16x8*)(sw + rt_off(we * 32 + j * 16 + lr, q * 4 + lg));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bb[j], acc[i][j], 0, 0, 0);
+    }
+    if (quant_on) {
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) {
+        const int r = qr0 + qslot + 32 * ps;  // the same on the row's 16 lanes
+        if (r >= qr1) continue;
+        const u32x4 raw = *(const u32x4*)(sx + rt_off(r, q16));
+        const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+        float v[8];
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(wd[i] << 16);
+          v[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = row16_max(amax);
+        if (gate_on) {
+          const u32x4 gr = *(const u32x4*)(gsl + kc * RG_KC + q16 * 8);
+          const uint32_t gd[4] = {gr.x, gr.y, gr.z, gr.w};
+          float gsum = gdot[ps];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            gsum += v[2 * i] * __uint_as_float(gd[i] << 16);
+            gsum += v[2 * i + 1] * __uint_as_float(gd[i] & 0xFFFF0000u);
+          }
+          gdot[ps] = gsum;
+        }
+        const float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+        // x / sc correctly rounded without a division per value (Markstein:
+        // with ry = RN(1 / sc), q0 = RN(x ry) and the exact residual
+        // r = x - q0 sc (one FMA), RN(q0 + r ry) = RN(x / sc) while no
+        // value under- or overflows, and x's sign restores -0 / sc = -0);
+        // the IEEE divisions' VCC-serialised sequences cost 2.5 us of this
+        // launch at 4096 x 2048. tests/test_quant_division.py checks the
+        // formula against IEEE division exhaustively over bf16 inputs.
+        const float ry = 1.0f / sc;
+        float yq[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float q0 = v[i] * ry;
+          const float rr = __builtin_fmaf(-q0, sc, v[i]);
+          const float qt = __builtin_copysignf(__builtin_fmaf(rr, ry, q0), v[i]);
+          yq[i] = fminf(fmaxf(qt, -448.f), 448.f);
+        }
+        qpk[ps].x = f32x4_to_e4m3(yq[0], yq[1], yq[2], yq[3]);
+        qpk[ps].y = f32x4_to_e4m3(yq[4], yq[5], yq[6], yq[7]);
+        qsc[ps] = sc;
+      }
+      qkc = kc;
+    }
+  }
+  if (quant_on) flush();
+  if (gate_on) {
+#pragma unroll 1
+    for (int ps = 0; ps < 2; ++ps) {
+      const int r = qr0 + qslot + 32 * ps;
+      if (r >= qr1) break;
+      const float g = row16_sum(gdot[ps]);
+      if (q16 == 0 && t0 + r < T) rp.gate_out[t0 + r] = sigmoid_f32(g);
+    }
+  }
+  dma::bar_lds();  // every wave is done with the last chunk
+  float* lt = reinterpret_cast<float*>(stg0);
+  uint64_t* kl = reinterpret_cast<uint64_t*>(stg1);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = wm * 32 + i * 16 + lg * 4 + v, c = we * 32 + j * 16 + lr;
+        lt[r * RG_LT + c] = acc[i][j][v];
+        if (logits && t0 + r < T && e0 + c < E)
+          logits[(size_t)(t0 + r) * E + e0 + c] = acc[i][j][v];
+      }
+  dma::bar_lds();
+  const int r16 = lane & 15, rg = lane >> 4;
+  const int ny = gridDim.y, y = blockIdx.y;
+  int tl[2];
+  float m[2], sm[2];
+  uint64_t key[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    tl[h] = wave * 8 + 4 * h + rg;
+    float v[8];
+    float mm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = e0 + r16 + 16 * i;
+      v[i] = e < E ? lt[tl[h] * RG_LT + r16 + 16 * i] : -INFINITY;
+      mm = fmaxf(mm, v[i]);
+    }
+    m[h] = row16_max(mm);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = e0 + r16 + 16 * i;
+      ss += e < E ? __expf(v[i] - m[h]) : 0.f;
+      key[h][i] = e < E ? topk_key(v[i], e) : 0ull;
+    }
+    sm[h] = row16_sum(ss);
+  }
+  row16_topk_keys2(key, rp.topk, kl + tl[0] * 16, kl + tl[1] * 16);
+  dma::bar_lds();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = t0 + tl[h];
+    if (t < T) {
+      const size_t at = (size_t)t * ny + y;
+      if (r16 < rp.topk) rp.keys[at * rp.topk + r16] = kl[tl[h] * 16 + r16];
+      if (r16 == 0) {
+        rp.stat[2 * at] = m[h];
+        rp.stat[2 * at + 1] = sm[h];
+      }
+    }
+  }
 }
 
 // The calling wave's logits of one row (lane holds experts lane + 64 i;
@@ -377,6 +706,28 @@ __device__ __forceinline__ void logit_sums(float* row, int ks, long kstride,
   }
 }
 
+// Lane j < topk holds pick j; m and s are the row's largest logit and sum
+// of exp(l - m): pick j's probability is exp(l - m) / s, and the weights
+// are those probabilities over their sum in pick order plus eps
+// (ref/qwen4_exp.py:118-140).
+__device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
+                                             int topk, float eps,
+                                             float* __restrict__ w_row,
+                                             int* __restrict__ id_row,
+                                             int* id_lds) {
+  const int lane = threadIdx.x & 63;
+  const float pn = expf(topk_key_value(pick) - m) / s;  // lane j: pick j
+  float wsum = 0.f;
+  for (int j = 0; j < topk; ++j)
+    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pn), j));
+  if (lane < topk) {
+    const int myid = topk_key_id(pick);
+    w_row[lane] = pn / (wsum + eps);
+    id_row[lane] = myid;
+    if (id_lds) id_lds[lane] = myid;
+  }
+}
+
 // One token's softmax top-k on the calling wave: row = the token's E logits;
 // lanes j < topk write slot j of w_row / id_row (and of id_lds when given).
 // The selection runs on the logits (softmax is monotone in them); pick j's
@@ -404,16 +755,7 @@ __device__ __forceinline__ void route_softmax_token(
   }
   s = wave_sum(s);
   const uint64_t pick = wave_topk_keys<EPL>(key, topk);
-  const float pn = expf(topk_key_value(pick) - m) / s;  // lane j: pick j
-  float wsum = 0.f;
-  for (int j = 0; j < topk; ++j)
-    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pn), j));
-  if (lane < topk) {
-    const int myid = topk_key_id(pick);
-    w_row[lane] = pn / (wsum + eps);
-    id_row[lane] = myid;
-    if (id_lds) id_lds[lane] = myid;
-  }
+  softmax_emit(pick, m, s, topk, eps, w_row, id_row, id_lds);
 }
 
 // Token t's shared-expert gate from the split router GEMM's ks partial
@@ -443,6 +785,41 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
   if (chunk_hist && lane < topk) {  // lane reads back its own id
     const int a = t * topk + lane;
     atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + id_out[a]], 1);
+  }
+}
+
+// The fused prefill router's second launch: token t's routing from the
+// tiles' partials (RouterPart, ny tiles). The ny * topk candidate keys
+// (at most 64 EPL) go one per lane slot; their top-k is the top-k of the
+// whole logits row, as every expert outside a tile's top-k has topk
+// larger keys in its own tile. The softmax normaliser is
+// M = max m_y, S = sum over y in order of s_y exp(m_y - M).
+template <int EPL>
+__global__ __launch_bounds__(256) void route_merge_kernel(
+    RouterPart rp, int ny, float* __restrict__ w_out, int* __restrict__ id_out,
+    int T, int E, float eps, int* __restrict__ chunk_hist) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int topk = rp.topk, nk = ny * topk;
+  const uint64_t* kr = rp.keys + (size_t)t * nk;
+  uint64_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int j = lane + 64 * i;
+    key[i] = j < nk ? kr[j] : 0ull;
+  }
+  const float* sr = rp.stat + (size_t)t * ny * 2;
+  float m = -INFINITY;
+  for (int y = 0; y < ny; ++y) m = fmaxf(m, sr[2 * y]);
+  float s = 0.f;
+  for (int y = 0; y < ny; ++y) s += sr[2 * y + 1] * expf(sr[2 * y] - m);
+  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
+  softmax_emit(pick, m, s, topk, eps, w_out + (size_t)t * topk,
+               id_out + (size_t)t * topk, nullptr);
+  if (chunk_hist && lane < topk) {
+    const int a = t * topk + lane;
+    atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + topk_key_id(pick)], 1);
   }
 }
 
@@ -701,6 +1078,69 @@ int launch_router_gemm(const uint16_t* x, const uint16_t* w, float* logits,
     dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
     router_gemm_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, zero,
                                              zero_n);
+  }
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+static bool topk_ok(int E, int topk) {
+  return E > 0 && topk > 0 && topk <= 16 && topk <= E &&
+         (long)ceil_div(E, RG_TE) * topk <= 512;
+}
+
+bool router_topk_fits(int T, int E, int topk, int H) {
+  return T > RG_SMALL_T && topk_ok(E, topk) && H > 0 && H % RG_KC == 0 &&
+         H <= RT_GATE_MAX;
+}
+
+size_t router_part_bytes(int T, int E, int topk) {
+  const size_t n = (size_t)T * ceil_div(E, RG_TE);
+  return n * 8 + n * topk * 8;
+}
+
+RouterPart router_part_at(char* base, int T, int E, int topk) {
+  const size_t n = (size_t)T * ceil_div(E, RG_TE);
+  RouterPart rp{};
+  rp.stat = (float*)base;
+  rp.keys = (uint64_t*)(base + n * 8);
+  rp.topk = topk;
+  return rp;
+}
+
+int launch_router_topk(const uint16_t* x, const uint16_t* w, float* logits,
+                       int T, int E, int H, const RouterPart& rp,
+                       hipStream_t st, int* zero, long zero_n) {
+  SLLM_REQUIRE(x && w && rp.stat && rp.keys, "router_topk: null pointer");
+  SLLM_REQUIRE(router_topk_fits(T, E, rp.topk, H),
+               "router_topk: need T > %d, H %% 128 == 0, H <= %d, topk <= 16, "
+               "ceil(E / 128) * topk <= 512 (T=%d E=%d H=%d k=%d)",
+               RG_SMALL_T, RT_GATE_MAX, T, E, H, rp.topk);
+  SLLM_REQUIRE(!rp.q || rp.s, "router_topk: quantized rows without scales");
+  SLLM_REQUIRE(!rp.gate_w || (rp.q && rp.gate_out),
+               "router_topk: gate needs the quantization and gate buffers");
+  SLLM_REQUIRE(zero_n == 0 || zero, "router_topk: null zero range");
+  dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
+  router_topk_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, zero,
+                                           zero_n, rp);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
+                       float* w, int* ids, hipStream_t st, int* chunk_hist) {
+  SLLM_REQUIRE(rp.stat && rp.keys && w && ids, "route_merge: null pointer");
+  SLLM_REQUIRE(T > RG_SMALL_T && topk_ok(E, rp.topk),
+               "route_merge: bad sizes (T=%d E=%d k=%d)", T, E, rp.topk);
+  const int ny = ceil_div(E, RG_TE);
+  dim3 grid(ceil_div(T, 4));
+  switch (epl_for(ny * rp.topk)) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_merge_kernel<n><<<grid, 256, 0, st>>>(rp, ny, w, ids, T, E, eps,    \
+                                                chunk_hist);                  \
+    break;
+    CASE(1) CASE(2) CASE(4) CASE(8)
+#undef CASE
   }
   SLLM_LAUNCHED();
   return 0;

@@ -107,7 +107,9 @@ def test_decode_workspace_holds_split_router_slices():
     multi-workgroup kernels (17 <= T <= 64 here), so its workspace holds 2
     partial-logit slices of T * E floats and 2 partial gate slices of T
     floats beyond a call given the logits. Batches routed in one fused
-    workgroup (T <= 16) and prefill keep one slice."""
+    workgroup (T <= 16) and prefill keep one slice; prefill also holds the
+    fused router's partials: per token and 128-expert tile, a (max, sum)
+    pair and k top-k keys of 8 bytes."""
     from sllm_amd.moe import qwen_workspace_bytes as wsb
 
     def up256(n):
@@ -120,4 +122,6 @@ def test_decode_workspace_holds_split_router_slices():
         given = wsb(T, H, E, I, Is, k, mode, logits_given=True)
         want = (up256(2 * T * E * 4) + up256(3 * T * 4) - up256(T * 4)
                 if split else up256(T * E * 4))
+        if mode == "prefill":
+            want += up256(T * (E // 128) * 8 * (1 + k))
         assert own - given == want, T

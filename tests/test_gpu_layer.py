@@ -74,6 +74,34 @@ def test_qwen_prefill_c2_shapes():
           f"rel-L2 {rel_l2(y, info):.3e}")
 
 
+@pytest.mark.parametrize("T,E,k", [(200, 200, 8), (300, 512, 10),
+                                   (130, 1024, 10), (257, 96, 16), (65, 128, 1)])
+def test_qwen_fused_router_matches_full_row_routing(T, E, k):
+    """Prefill router fused with routing: each 128-expert tile's top-k keys
+    and softmax partials, merged by the routing launch, against the
+    full-row routing kernel on the same logits (the layer given the logits
+    the first call copied out). Ids bit-exact, weights to 2e-6 (only the
+    normaliser's summation order differs), outputs within a few bf16 ulps;
+    the default call (no logits copy) gives the same output bit for bit.
+    Cases: a partial last tile (E 200, 96), 80 candidate keys (E 1024),
+    top-16 from one tile, top-1, ragged 64-token tiles."""
+    x, W = qwen_fp8_gpu(seed=T + E, T=T, H=512, E=E, I=128, Is=128)
+    layer = qwen_layer(W, k)
+    y_f, r_f = layer.forward(x, mode="prefill", return_routing=True)
+    assert _check_routing(r_f, E, k) == 0
+    y_g, r_g = layer.forward(x, logits=r_f["logits"], mode="prefill",
+                             return_routing=True)
+    np.testing.assert_array_equal(r_f["ids"], r_g["ids"])
+    np.testing.assert_array_equal(r_f["counts"], r_g["counts"])
+    np.testing.assert_allclose(r_f["w"], r_g["w"], rtol=2e-6, atol=1e-9)
+    rel = rel_l2(y_f, y_g)
+    print(f"fused router T={T} E={E} k={k}: output vs full-row routing "
+          f"rel-L2 {rel:.3e}")
+    assert rel < 1e-4
+    y_d = layer.forward(x, mode="prefill")
+    np.testing.assert_array_equal(y_d, y_f)
+
+
 @pytest.mark.parametrize("B", [1, 8, 32, 64])
 def test_qwen_decode_c3_shapes(B):
     """C3 decode batches on C2 geometry (fp32-activation GEMV path)."""
