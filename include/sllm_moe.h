@@ -262,7 +262,9 @@ int sllm_quantize_weight_mxfp4(const float* w, int N, int K, void* packed,
  *   logits_given]; wg/wu (E,I,H) + (E,I/128,H/128); wd (E,H,I) +
  *   (E,H/128,I/128); shared sg/su (Is,H), sd (H,Is) + scales; sgl (H) bf16.
  *   out (T,H) bf16 or f32. Optional debug copies: logits_out (T,E),
- *   w_out (T,k) f32, ids_out (T,k) i32, counts_out (E) i32.
+ *   w_out (T,k) f32, ids_out (T,k) i32, counts_out (E) i32. Prefill
+ *   (T > 64, topk <= 16, H <= 4096) routes without materialising the
+ *   logits; logits_out then makes the router launch write them as well.
  * Replaces qwen4_exp.moe_block_forward (the numpy oracle that runs today)
  * and kernels/q4_device_decode.py:316-339 (_moe). */
 typedef struct sllm_moe_qwen_args {

@@ -817,9 +817,12 @@ __global__ __launch_bounds__(256) void route_merge_kernel(
   const uint64_t pick = wave_topk_keys<EPL>(key, topk);
   softmax_emit(pick, m, s, topk, eps, w_out + (size_t)t * topk,
                id_out + (size_t)t * topk, nullptr);
-  if (chunk_hist && lane < topk) {
+  // every pick is an expert (the tiles hold at least topk candidates, as
+  // E >= topk); the range check keeps a damaged partial from indexing out
+  const int id = topk_key_id(pick);
+  if (chunk_hist && lane < topk && (unsigned)id < (unsigned)E) {
     const int a = t * topk + lane;
-    atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + topk_key_id(pick)], 1);
+    atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + id], 1);
   }
 }
 
