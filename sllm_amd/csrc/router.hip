@@ -826,6 +826,75 @@ __global__ __launch_bounds__(256) void route_merge_kernel(
   }
 }
 
+// Descending top-k (topk <= 16) of one token's keys per 16-lane row (N per
+// lane, 0 = none, distinct), as row16_topk_keys2 for a single token: pick
+// j goes to kl[j].
+template <int N>
+__device__ __forceinline__ void row16_topk_into(uint64_t (&key)[N], int topk,
+                                                uint64_t* kl) {
+  sort_desc<N>(key);
+  for (int kk = 0; kk < topk; ++kk) {
+    const uint32_t hi = (uint32_t)(key[0] >> 32);
+    bool own = hi == row16_max_u32(hi);
+    if (__popcll(__ballot(own)) != 4) {
+      const uint32_t mlo = row16_max_u32(own ? (uint32_t)key[0] : 0u);
+      own = own && (uint32_t)key[0] == mlo;
+    }
+    if (own) {
+      kl[kk] = key[0];
+#pragma unroll
+      for (int i = 0; i + 1 < N; ++i) key[i] = key[i + 1];
+      key[N - 1] = 0;
+    }
+  }
+}
+
+// route_merge_kernel for ny * topk <= 128 candidates: a 16-lane row per
+// token (KPL keys per lane), 16 tokens per workgroup; a pick is a row
+// reduction of four DPP steps rather than a wave's six, and one wave
+// instruction serves four tokens. Rows past T run on token T - 1 (the
+// picks' ballot counts the wave's four rows) and write nothing. The
+// picks' probabilities are added over the row (lanes past topk add 0).
+template <int KPL>
+__global__ __launch_bounds__(256) void route_merge_row_kernel(
+    RouterPart rp, int ny, float* __restrict__ w_out, int* __restrict__ id_out,
+    int T, int E, float eps, int* __restrict__ chunk_hist) {
+  __shared__ uint64_t kl[16][16];
+  const int r16 = threadIdx.x & 15, slot = threadIdx.x >> 4;
+  const int t_raw = blockIdx.x * 16 + slot;
+  const bool live = t_raw < T;
+  const int t = live ? t_raw : T - 1;
+  const int topk = rp.topk, nk = ny * topk;
+  const uint64_t* kr = rp.keys + (size_t)t * nk;
+  uint64_t key[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int j = r16 + 16 * i;
+    key[i] = j < nk ? kr[j] : 0ull;
+  }
+  const float* sr = rp.stat + (size_t)t * ny * 2;
+  float m = -INFINITY;
+  for (int y = 0; y < ny; ++y) m = fmaxf(m, sr[2 * y]);
+  float s = 0.f;
+  for (int y = 0; y < ny; ++y) s += sr[2 * y + 1] * expf(sr[2 * y] - m);
+  row16_topk_into<KPL>(key, topk, kl[slot]);
+  __syncthreads();
+  const uint64_t pick = r16 < topk ? kl[slot][r16] : 0ull;
+  const float pn = r16 < topk ? expf(topk_key_value(pick) - m) / s : 0.f;
+  const float wsum = row16_sum(pn);
+  const int id = topk_key_id(pick);
+  if (live && r16 < topk) {
+    w_out[(size_t)t * topk + r16] = pn / (wsum + eps);
+    id_out[(size_t)t * topk + r16] = id;
+    // every pick is an expert (E >= topk); the range check keeps a damaged
+    // partial from indexing out
+    if (chunk_hist && (unsigned)id < (unsigned)E) {
+      const int a = t * topk + r16;
+      atomicAdd(&chunk_hist[(size_t)(a / PERM_CHUNK) * E + id], 1);
+    }
+  }
+}
+
 // Decode (T * topk <= PERM_FUSED_MAX_N, E <= PERM_FUSED_MAX_E): softmax
 // top-k of every token (wave w takes tokens w, w + 16, ...) and the
 // expert-major permutation in one workgroup, the ids passed through LDS.
@@ -1134,9 +1203,24 @@ int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
   SLLM_REQUIRE(rp.stat && rp.keys && w && ids, "route_merge: null pointer");
   SLLM_REQUIRE(T > RG_SMALL_T && topk_ok(E, rp.topk),
                "route_merge: bad sizes (T=%d E=%d k=%d)", T, E, rp.topk);
-  const int ny = ceil_div(E, RG_TE);
+  const int ny = ceil_div(E, RG_TE), nk = ny * rp.topk;
+  if (nk <= 128) {
+    const int kpl = nk <= 16 ? 1 : nk <= 32 ? 2 : nk <= 64 ? 4 : 8;
+    dim3 grid(ceil_div(T, 16));
+    switch (kpl) {
+#define CASE(n)                                                               \
+  case n:                                                                     \
+    route_merge_row_kernel<n><<<grid, 256, 0, st>>>(rp, ny, w, ids, T, E,     \
+                                                    eps, chunk_hist);         \
+    break;
+      CASE(1) CASE(2) CASE(4) CASE(8)
+#undef CASE
+    }
+    SLLM_LAUNCHED();
+    return 0;
+  }
   dim3 grid(ceil_div(T, 4));
-  switch (epl_for(ny * rp.topk)) {
+  switch (epl_for(nk)) {
 #define CASE(n)                                                               \
   case n:                                                                     \
     route_merge_kernel<n><<<grid, 256, 0, st>>>(rp, ny, w, ids, T, E, eps,    \
