@@ -54,6 +54,7 @@ struct RouterPart {
   float* s;
   const uint16_t* gate_w;
   float* gate_out;
+  int pow2;  // quantization scales rounded up to powers of two
 };
 bool router_topk_fits(int T, int E, int topk, int H);
 size_t router_part_bytes(int T, int E, int topk);
@@ -61,6 +62,13 @@ RouterPart router_part_at(char* base, int T, int E, int topk);
 int launch_router_topk(const uint16_t* x, const uint16_t* w, float* logits,
                        int T, int E, int H, const RouterPart& rp,
                        hipStream_t st, int* zero = nullptr, long zero_n = 0);
+// The same launch in logits mode (DeepSeek prefill): the router logits,
+// as launch_router_gemm writes them, and the activation quantization of
+// launch_act_quant(x, T, H, pow2, q, s) in the same pass over x.
+bool router_logits_quant_fits(int T, int H);
+int launch_router_logits_quant(const uint16_t* x, const uint16_t* w,
+                               float* logits, int T, int E, int H, uint8_t* q,
+                               float* s, int pow2, hipStream_t st);
 int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
                        float* w, int* ids, hipStream_t st,
                        int* chunk_hist = nullptr);

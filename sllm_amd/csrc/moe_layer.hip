@@ -798,13 +798,22 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   int* ntiles = (int*)(ws + p.ntiles);
 
   const StageClock clk{a->stage_events, st};
+  // Prefill: the router launch also quantizes the activations (power-of-two
+  // scales) from the x chunks it stages, in place of the activation-quant
+  // launch, which would read x again (C4: 117 MB).
+  const bool rq_fused = !p.decode && !a->logits_given &&
+                        router_logits_quant_fits(T, H);
   // with caller-provided logits the router stage is recorded with zero
   // length, so every stage's events exist on every call
   STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
         a->logits_given ? 0
-                        : launch_router_gemm((const uint16_t*)a->x,
-                                             (const uint16_t*)a->router_w,
-                                             logits, T, E, H, st, p.ks_r));
+        : rq_fused
+            ? launch_router_logits_quant(
+                  (const uint16_t*)a->x, (const uint16_t*)a->router_w, logits,
+                  T, E, H, (uint8_t*)(ws + p.xq), (float*)(ws + p.sx), 1, st)
+            : launch_router_gemm((const uint16_t*)a->x,
+                                 (const uint16_t*)a->router_w, logits, T, E,
+                                 H, st, p.ks_r));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
         a->tid2eid
             ? launch_route_hash(logits, a->token_ids, a->tid2eid, a->vocab, w,
@@ -910,8 +919,9 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     float* hs = (float*)(ws + p.hs);
     uint16_t* y = (uint16_t*)(ws + p.y);
     STAGE(clk, SLLM_MOE_STAGE_ACT_QUANT,
-          launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx, nullptr,
-          nullptr, st));
+          rq_fused ? 0
+                   : launch_act_quant((const uint16_t*)a->x, T, H, 1, xq, sx,
+                                      nullptr, nullptr, st));
     uint16_t* y_sh = nullptr;
     uint8_t* hq_sh = nullptr;
     float* hs_sh = nullptr;

@@ -438,6 +438,11 @@ __device__ __forceinline__ int rt_off(int r, int c) {
 // products chunk by chunk, then the row's lanes (row16_sum);
 // gate_out[t] = sigmoid(logit).
 //
+// Logits mode (rp.keys null; DeepSeek's grouped routing): the logits go
+// out as router_gemm_kernel writes them (the same MFMA order, so the same
+// values) and the quantization is the launch's other output (rp.pow2:
+// power-of-two scales).
+//
 // Epilogue: the tile's logits go to LDS (logits, when not null, also gets
 // them for the caller's copy); each wave takes 8 tokens, two per 16-lane
 // row (row lane r holds experts e0 + r + 16 i, i < 8): the tile's maximum
@@ -574,7 +579,8 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
           }
           gdot[ps] = gsum;
         }
-        const float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+        float sc = fmaxf(amax, 1e-4f) * (1.0f / 448.0f);
+        if (rp.pow2) sc = pow2_ceil(sc);
         // x / sc correctly rounded without a division per value (Markstein:
         // with ry = RN(1 / sc), q0 = RN(x ry) and the exact residual
         // r = x - q0 sc (one FMA), RN(q0 + r ry) = RN(x / sc) while no
@@ -607,6 +613,19 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
       const float g = row16_sum(gdot[ps]);
       if (q16 == 0 && t0 + r < T) rp.gate_out[t0 + r] = sigmoid_f32(g);
     }
+  }
+  if (!rp.keys) {  // logits mode: the logits for a routing launch of its own
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = wm * 32 + i * 16 + lg * 4 + v, c = we * 32 + j * 16 + lr;
+          if (t0 + r < T && e0 + c < E)
+            logits[(size_t)(t0 + r) * E + e0 + c] = acc[i][j][v];
+        }
+    return;
   }
   dma::bar_lds();  // every wave is done with the last chunk
   float* lt = reinterpret_cast<float*>(stg0);
@@ -1194,6 +1213,27 @@ int launch_router_topk(const uint16_t* x, const uint16_t* w, float* logits,
   dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
   router_topk_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, zero,
                                            zero_n, rp);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+bool router_logits_quant_fits(int T, int H) {
+  return T > RG_SMALL_T && H > 0 && H % RG_KC == 0;
+}
+
+int launch_router_logits_quant(const uint16_t* x, const uint16_t* w,
+                               float* logits, int T, int E, int H, uint8_t* q,
+                               float* s, int pow2, hipStream_t st) {
+  SLLM_REQUIRE(x && w && logits && q && s, "router_logits_quant: null pointer");
+  SLLM_REQUIRE(E > 0 && router_logits_quant_fits(T, H),
+               "router_logits_quant: need T > %d, H %% 128 == 0 (T=%d E=%d H=%d)",
+               RG_SMALL_T, T, E, H);
+  RouterPart rp{};
+  rp.q = q;
+  rp.s = s;
+  rp.pow2 = pow2 ? 1 : 0;
+  dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
+  router_topk_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, nullptr, 0, rp);
   SLLM_LAUNCHED();
   return 0;
 }

@@ -220,6 +220,33 @@ def test_deepseek_prefill_small(T, G, kg, L, packed):
     assert rel < 3e-3 and mabs < 0.05 * scale
 
 
+@pytest.mark.parametrize("T,E,H", [(200, 16, 512), (777, 200, 768), (96, 256, 1024)])
+def test_deepseek_router_quant_matches_separate_launches(T, E, H):
+    """Prefill from router_w: the router launch also quantizes the
+    activations (power-of-two scales) from the x chunks it stages. Given
+    the logits that call copied out, the layer runs the separate
+    activation-quant launch instead. The router launch's logits are the
+    logits GEMM's (same MFMA order), so the two calls route alike and, with
+    the same quantized activations, give the same output bit for bit.
+    E 200: a partial expert tile; T 777: a partial token tile; H 1024.
+    The first case is also checked against the oracle."""
+    small = E <= 16
+    x, W = (deepseek_mxfp4(seed=T + E, T=T, H=H, E=E, I=256, Is=256) if small
+            else deepseek_mxfp4_gpu(seed=T + E, T=T, H=H, E=E, I=256, Is=256))
+    route = dict(n_group=1, topk_group=1, scoring="sigmoid", route_scale=2.5,
+                 swiglu_limit=10.0)
+    layer = deepseek_layer(W, 6, **route)
+    y_f, r_f = layer.forward(x, mode="prefill", return_routing=True)
+    y_g, r_g = layer.forward(x, logits=r_f["logits"], mode="prefill",
+                             return_routing=True)
+    np.testing.assert_array_equal(r_f["ids"], r_g["ids"])
+    np.testing.assert_array_equal(y_f, y_g)
+    if small:
+        want = dm.moe_layer_mxfp4(x, r_f["logits"], W, 6, 10.0, "sigmoid", 2.5, 1, 1)
+        rel, mabs, scale = _report(f"deepseek router+quant T={T} E={E}", y_f, want)
+        assert rel < 3e-3 and mabs < 0.05 * scale
+
+
 @pytest.mark.parametrize("T,L", [(1024, 10.0), (777, 0.0)])
 def test_deepseek_dense_kernel_matches_stream(T, L, monkeypatch):
     """Prefill whose experts average more than one 128-row tile runs the
