@@ -16,7 +16,8 @@
 // that contract; the contract is what is implemented.
 //
 // These are parity surfaces, not the layer's hot path: a 32x32 LDS-tiled
-// fp32 kernel with on-the-fly dequantization of B.
+// fp32 kernel with on-the-fly dequantization of B (bf16 gemm_ex with
+// k % 128 == 0 takes the MFMA router kernels instead).
 #include "launch.h"
 
 namespace sllm {
@@ -209,9 +210,19 @@ int sllm_ds_fp4_gemm_packed(float* o, const float* a, const void* packed,
 
 // c (m, n) fp32 = a (m, k) . w (n, k)^T; atype 0 = fp32, 1 = bf16 for both a
 // and w (dtype tags of kernels/_sllm_cuda.py:490-491). Device pointers.
+// bf16 with k % 128 == 0 runs on the router GEMM kernels (the same contract:
+// bf16 products on the matrix cores, fp32 accumulation; m <= 64, the decode
+// loops' GEMVs, on the K-split small-batch kernel); other shapes and fp32
+// on the tiled kernel.
 int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
                  int n, int k) {
   SLLM_REQUIRE(atype == 0 || atype == 1, "sllm_gemm_ex: atype must be 0 or 1");
+  SLLM_REQUIRE(a && w && c && m > 0 && n > 0 && k > 0,
+               "sllm_gemm_ex: null pointer or empty shape (m=%d n=%d k=%d)",
+               m, n, k);
+  if (atype == 1 && k % 128 == 0)
+    return launch_router_gemm((const uint16_t*)a, (const uint16_t*)w,
+                              (float*)c, m, n, k, nullptr, 1);
   BDesc bd{atype == 1 ? B_BF16 : B_F32, w, nullptr, 0, 0};
   return launch_tiled_gemm(a, atype, bd, (float*)c, m, n, k, 0);
 }

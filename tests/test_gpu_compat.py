@@ -132,6 +132,28 @@ def test_gemm_ex_f32_and_bf16():
     np.testing.assert_allclose(c.copy_host().reshape(m, n), ab @ wb.T, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 2048), (17, 300, 256), (64, 77, 128),
+                                   (65, 200, 384), (300, 129, 1024)])
+def test_gemm_ex_bf16_mfma_shapes(m, n, k):
+    """bf16 gemm_ex with k % 128 == 0 (the MFMA router kernels: the K-split
+    small-batch kernel for m <= 64, the 64 x 128 tiles above; ragged n and
+    m): against the fp64 product of the bf16-rounded operands. bf16 products
+    are exact in fp32, so only the fp32 accumulation order differs."""
+    from sllm_amd.runtime import DeviceBuffer, T_BF16, gemm_ex, sync, to_bf16, to_device_raw
+    rng = np.random.default_rng(m * n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    c = DeviceBuffer(m * n * 4)
+    gemm_ex(to_device_raw(to_bf16(a)), to_device_raw(to_bf16(w)), c, m, n, k, T_BF16)
+    sync()
+    want = (codecs.round_bf16(a).astype(np.float64)
+            @ codecs.round_bf16(w).astype(np.float64).T)
+    got = c.copy_host().reshape(m, n)
+    err = np.abs(got - want).max() / np.sqrt(k)
+    print(f"gemm_ex bf16 {m}x{n}x{k}: max |err| / sqrt(k) {err:.2e}")
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(k))
+
+
 def test_buf_copy_exact_with_tail():
     """sllm_buf_copy (the calibration copy kernel): byte-exact over a size
     with a non-multiple-of-16 tail and over an empty copy."""
