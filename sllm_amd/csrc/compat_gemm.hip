@@ -126,6 +126,14 @@ int sllm_fp8_gemm_dev(const float* A, const unsigned char* B,
   SLLM_REQUIRE(M > 0 && N > 0 && K > 0 && block_h > 0 && block_w > 0,
                "sllm_fp8_gemm: bad dims");
   SLLM_REQUIRE(scale_inv, "sllm_fp8_gemm: null scale");
+  // decode-size batches with the loader's 128 x 128 blocks: the layer's
+  // unpacked-weight GEMV (one wave per four weight rows, 16-byte weight
+  // loads dequantized in registers), which streams B once per launch
+  if (block_h == 128 && block_w == 128 && M <= 64 && N % 128 == 0 &&
+      K % 128 == 0)
+    return launch_gemv(0, 0, A, 0, 0, nullptr, 1, M, nullptr, nullptr, 1,
+                       nullptr, B, scale_inv, nullptr, nullptr, N, K, nullptr,
+                       0.f, C, nullptr);
   BDesc bd{B_FP8_BLOCK, B, scale_inv, block_h, block_w};
   return launch_tiled_gemm(A, 0, bd, C, M, N, K, 0);
 }

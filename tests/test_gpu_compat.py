@@ -101,6 +101,24 @@ def test_fp8_gemm_scale_orientation():
     np.testing.assert_allclose(got2, want2, rtol=1e-4, atol=1e-3)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 256, 512), (33, 384, 1024), (64, 128, 128)])
+def test_fp8_gemm_decode_shapes(M, N, K):
+    """sllm_fp8_gemm at decode sizes with 128 x 128 blocks (M <= 64, N and K
+    multiples of 128: the unpacked-weight GEMV path) against the fp64
+    product with the dequantized weight."""
+    from sllm_amd import fp8
+    rng = np.random.default_rng(M + N + K)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b8 = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    b8[(b8 & 0x7F) == 0x7F] = 0x30
+    scale = (rng.random((N // 128, K // 128)) + 0.5).astype(np.float32)
+    wd = codecs.dequant_fp8_block(b8, scale).astype(np.float64)
+    want = a.astype(np.float64) @ wd.T
+    got = fp8.fp8_gemm(a, b8, scale)
+    mag = np.abs(a) @ np.abs(wd).T
+    assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6)
+
+
 def test_fp4_linear_matches_dequant():
     from sllm_amd import deepseek
     rng = np.random.default_rng(5)
