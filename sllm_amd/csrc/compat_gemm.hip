@@ -188,6 +188,13 @@ int sllm_ds_fp4_gemm_packed_dev(float* o, const float* a, const void* packed,
                                 const void* scale_e8m0, int M, int N, int K,
                                 int block_w) {
   SLLM_REQUIRE(K % 2 == 0 && block_w > 0, "fp4 gemm: K even, block_w > 0");
+  // decode-size batches with 32-column scale blocks: the layer's
+  // unpacked-weight GEMV in its MXFP4 form (the same nibble order, E2M1
+  // values and 0x00 / 0xFF scale convention)
+  if (block_w == 32 && M <= 64 && K % 32 == 0 && N % 16 == 0)
+    return launch_gemv(1, 0, a, 0, 0, nullptr, 1, M, nullptr, nullptr, 1,
+                       nullptr, (const uint8_t*)packed, scale_e8m0, nullptr,
+                       nullptr, N, K, nullptr, 0.f, o, nullptr);
   BDesc bd{B_FP4_PACKED, packed, scale_e8m0, 1, block_w};
   return launch_tiled_gemm(a, 0, bd, o, M, N, K, 0);
 }

@@ -132,6 +132,28 @@ def test_fp4_linear_matches_dequant():
     np.testing.assert_allclose(got2, want, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 256, 512), (40, 128, 1024), (64, 48, 96)])
+def test_fp4_linear_decode_shapes(M, N, K):
+    """Packed MXFP4 linear at decode sizes (M <= 64, 32-column scale blocks:
+    the unpacked-weight GEMV path), including e8m0 scale codes 0 (-> 0)
+    and 255 (-> NaN, a NaN row), against the fp64 product."""
+    from sllm_amd import deepseek
+    rng = np.random.default_rng(M * N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.1).astype(np.float32)
+    packed, s = quant.quantize_weight_mxfp4(w)
+    s = s.copy()
+    s[3, 0] = 0
+    s[5, 1] = 255
+    got = deepseek.fp4_moe_linear(x, packed, s)
+    wd = codecs.dequant_fp4_block(packed, s).astype(np.float64)
+    want = x.astype(np.float64) @ wd.T
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    mag = np.abs(x) @ np.abs(np.nan_to_num(wd)).T
+    assert np.all(np.abs(got - want)[ok] <= (1e-5 * mag + 1e-6)[ok])
+
+
 def test_gemm_ex_f32_and_bf16():
     from sllm_amd.runtime import DeviceBuffer, T_BF16, T_F32, gemm_ex, sync, to_bf16, to_device, to_device_raw
     rng = np.random.default_rng(9)
