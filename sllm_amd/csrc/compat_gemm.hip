@@ -227,7 +227,8 @@ int sllm_ds_fp4_gemm_packed(float* o, const float* a, const void* packed,
 // and w (dtype tags of kernels/_sllm_cuda.py:490-491). Device pointers.
 // bf16 with k % 128 == 0 runs on the router GEMM kernels (the same contract:
 // bf16 products on the matrix cores, fp32 accumulation; m <= 64, the decode
-// loops' GEMVs, on the K-split small-batch kernel); other shapes and fp32
+// loops' GEMVs, on the K-split small-batch kernel); other batches of at most
+// 64 rows (fp32, or bf16 with other k) on the unpacked-weight GEMV; the rest
 // on the tiled kernel.
 int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
                  int n, int k) {
@@ -238,6 +239,12 @@ int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
   if (atype == 1 && k % 128 == 0)
     return launch_router_gemm((const uint16_t*)a, (const uint16_t*)w,
                               (float*)c, m, n, k, nullptr, 1);
+  // other decode-size batches: the unpacked-weight GEMV (bf16 or fp32 rows)
+  if (m <= 64 && n % 16 == 0 && k % (atype == 1 ? 8 : 4) == 0)
+    return launch_gemv(atype == 1 ? 2 : 3, 0, a, atype, 0, nullptr, 1, m,
+                       nullptr, nullptr, 1, nullptr, (const uint8_t*)w,
+                       nullptr, nullptr, nullptr, n, k, nullptr, 0.f,
+                       (float*)c, nullptr);
   BDesc bd{atype == 1 ? B_BF16 : B_F32, w, nullptr, 0, 0};
   return launch_tiled_gemm(a, atype, bd, (float*)c, m, n, k, 0);
 }

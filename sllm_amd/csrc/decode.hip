@@ -20,7 +20,8 @@
 
 namespace sllm {
 
-enum WFmt { WF_FP8_BLOCK = 0, WF_MXFP4 = 1, WF_BF16 = 2 };
+// WF_F32: fp32 weight rows (sllm_gemm_ex's fp32 GEMV; no scales)
+enum WFmt { WF_FP8_BLOCK = 0, WF_MXFP4 = 1, WF_BF16 = 2, WF_F32 = 3 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -34,7 +35,7 @@ __device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
 template <int WF>
 struct ChunkK {  // K values in one 16-byte chunk of a weight row
   static constexpr int value =
-      WF == WF_FP8_BLOCK ? 16 : (WF == WF_MXFP4 ? 32 : 8);
+      WF == WF_FP8_BLOCK ? 16 : (WF == WF_MXFP4 ? 32 : (WF == WF_F32 ? 4 : 8));
 };
 
 // Dequantized chunk of one weight row: KPC values, already scaled.
@@ -62,6 +63,10 @@ __device__ __forceinline__ void load_w_chunk(const uint8_t* row, int k0,
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         w[8 * i + j] = e2m1_to_f32((d[i] >> (4 * j)) & 15u) * scale;
+  } else if constexpr (WF == WF_F32) {
+    (void)scale;
+    const float4 r = *(const float4*)(row + 4 * k0);
+    w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
   } else {
     (void)scale;
     const uint4 r = *(const uint4*)(row + 2 * k0);
@@ -100,7 +105,7 @@ __device__ __forceinline__ void load_act(const TA* p, float (&a)[N]) {
 template <int WF>
 __device__ __forceinline__ float w_scale(const void* s, size_t e, int n, int k0,
                                          int N, int K) {
-  if constexpr (WF == WF_BF16) {
+  if constexpr (WF == WF_BF16 || WF == WF_F32) {
     return 1.f;
   } else if constexpr (WF == WF_FP8_BLOCK) {
     const int KB = K / 128, NB = N / 128;
@@ -145,7 +150,8 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(
   const void* srow[4];
   int nrow[4];
   const size_t rb = WF == WF_FP8_BLOCK ? (size_t)K
-                    : (WF == WF_MXFP4 ? (size_t)K / 2 : (size_t)K * 2);
+                    : (WF == WF_MXFP4 ? (size_t)K / 2
+                                      : (WF == WF_F32 ? (size_t)K * 4 : (size_t)K * 2));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (SWIGLU) {
@@ -234,8 +240,8 @@ int launch_gemv(int wf, int swiglu, const void* act, int act_bf16,
                 const void* s0, const uint8_t* w1, const void* s1, int N,
                 int K, const float* row_w, float limit, float* out,
                 hipStream_t st) {
-  SLLM_REQUIRE(wf >= 0 && wf <= 2, "gemv: bad weight format %d", wf);
-  const int kpc = wf == WF_FP8_BLOCK ? 16 : (wf == WF_MXFP4 ? 32 : 8);
+  SLLM_REQUIRE(wf >= 0 && wf <= 3, "gemv: bad weight format %d", wf);
+  const int kpc = wf == WF_FP8_BLOCK ? 16 : (wf == WF_MXFP4 ? 32 : (wf == WF_F32 ? 4 : 8));
   SLLM_REQUIRE(K % kpc == 0 && K > 0 && N > 0,
                "gemv: K must be a multiple of %d (K=%d)", kpc, K);
   SLLM_REQUIRE(wf != WF_FP8_BLOCK || (K % 128 == 0 && N % 128 == 0),
@@ -260,6 +266,9 @@ int launch_gemv(int wf, int swiglu, const void* act, int act_bf16,
     } else {
       if (swiglu) GO(WF_BF16, float, 1); else GO(WF_BF16, float, 0);
     }
+  } else if (wf == WF_F32) {
+    SLLM_REQUIRE(!swiglu && !act_bf16, "gemv: fp32 weights take fp32 rows, no SwiGLU");
+    GO(WF_F32, float, 0);
   } else {
     if (act_bf16) {
       if (swiglu) GO(WF_MXFP4, uint16_t, 1); else GO(WF_MXFP4, uint16_t, 0);

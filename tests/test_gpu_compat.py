@@ -172,6 +172,28 @@ def test_gemm_ex_f32_and_bf16():
     np.testing.assert_allclose(c.copy_host().reshape(m, n), ab @ wb.T, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("atype,m,n,k", [(0, 1, 4096, 2048), (0, 33, 160, 100),
+                                         (0, 64, 48, 4), (1, 5, 64, 264), (1, 64, 32, 8)])
+def test_gemm_ex_gemv_shapes(atype, m, n, k):
+    """gemm_ex at m <= 64 outside the MFMA kernels' shapes (fp32 operands;
+    bf16 with k % 128 != 0): the unpacked-weight GEMV, against fp64."""
+    from sllm_amd.runtime import DeviceBuffer, T_BF16, T_F32, gemm_ex, sync, to_bf16, to_device, to_device_raw
+    rng = np.random.default_rng(m * n + k + atype)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    c = DeviceBuffer(m * n * 4)
+    if atype == 1:
+        a, w = codecs.round_bf16(a), codecs.round_bf16(w)
+        gemm_ex(to_device_raw(to_bf16(a)), to_device_raw(to_bf16(w)), c, m, n, k, T_BF16)
+    else:
+        gemm_ex(to_device(a), to_device(w), c, m, n, k, T_F32)
+    sync()
+    want = a.astype(np.float64) @ w.astype(np.float64).T
+    mag = np.abs(a) @ np.abs(w).T
+    got = c.copy_host().reshape(m, n)
+    assert np.all(np.abs(got - want) <= 2e-6 * mag + 1e-6)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 2048), (17, 300, 256), (64, 77, 128),
                                    (65, 200, 384), (300, 129, 1024)])
 def test_gemm_ex_bf16_mfma_shapes(m, n, k):
