@@ -102,6 +102,13 @@ int sllm_q4_moe_router_dev(const float* logits, float* w_out, int* id_out,
 /* out = silu(g) * u, n floats. ref qwen4.cu:308-320, :795-799 */
 int sllm_q4_swiglu(const float* g, const float* u, float* out, long n);
 int sllm_q4_swiglu_dev(const float* g, const float* u, float* out, long n);
+/* out (rows,O) f32 = A (rows,K) . W (O,K)^T, then post 1: silu(x/scale),
+ * 2: sigmoid(x/scale). rows, K, O <= 0: -1. ref qwen4.cu:95-136 (host
+ * pointers), :699-708 (_dev: device pointers). */
+int sllm_q4_gemv_rows(const float* A, const float* W, float* out, int rows,
+                      int K, int O, int post, float scale);
+int sllm_q4_gemv_rows_dev(const float* A, const float* W, float* out, int rows,
+                          int K, int O, int post, float scale);
 /* out[t,:] += w[t] * y[t,:]. ref qwen4.cu:332-351, :801-806 */
 int sllm_q4_axpy_rows(float* out, const float* y, const float* w, int n,
                       int H);
@@ -145,6 +152,11 @@ int sllm_ds_fp4_gemm_packed_dev(float* o, const float* a, const void* packed,
  * (cublasGemmEx), kernels/_sllm_cuda.py:503-506. */
 int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
                  int n, int k);
+/* out = silu(g) * u for n fp32 elements of g and u (device pointers),
+ * stored as fp32 (out_type 0) or bf16 (out_type 1). ref kernels.cu:897-919,
+ * kernels/_sllm_cuda.py:529-532. */
+int sllm_silu_mul(const void* g, const void* u, void* out, long n,
+                  int out_type);
 
 /* ---------------------------------------------------------------------- */
 /* MoE building blocks (device pointers, stream-ordered, no sync)          */

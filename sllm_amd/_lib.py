@@ -96,6 +96,9 @@ SIGNATURES = {
     "sllm_q4_moe_router_dev": (c_int, [P, P, P, c_int, c_int, c_int]),
     "sllm_q4_swiglu": (c_int, [F, F, F, c_long]),
     "sllm_q4_swiglu_dev": (c_int, [P, P, P, c_long]),
+    "sllm_q4_gemv_rows": (c_int, [F, F, F, c_int, c_int, c_int, c_int, c_float]),
+    "sllm_q4_gemv_rows_dev": (c_int, [P, P, P, c_int, c_int, c_int, c_int,
+                                      c_float]),
     "sllm_q4_axpy_rows": (c_int, [F, F, F, c_int, c_int]),
     "sllm_q4_axpy_rows_dev": (c_int, [P, P, P, c_int, c_int]),
     "sllm_q4_shared_gate_accum": (c_int, [F, F, F, c_int, c_int]),
@@ -109,6 +112,7 @@ SIGNATURES = {
     "sllm_ds_fp4_gemm_packed_dev": (c_int, [P, P, P, P, c_int, c_int, c_int,
                                             c_int]),
     "sllm_gemm_ex": (c_int, [P, c_int, P, P, c_int, c_int, c_int]),
+    "sllm_silu_mul": (c_int, [P, P, P, c_long, c_int]),
     "sllm_moe_router_gemm": (c_int, [P, P, P, c_int, c_int, c_int, P]),
     "sllm_moe_route_hash": (c_int, [P, P, P, c_int, P, P, c_int, c_int, c_int,
                                     c_int, c_float, P]),

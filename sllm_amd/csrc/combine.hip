@@ -190,6 +190,16 @@ __global__ void swiglu_elem_kernel(const float* __restrict__ g,
   if (i < n) out[i] = silu_f32(g[i]) * u[i];
 }
 
+__global__ void silu_mul_kernel(const float* __restrict__ g,
+                                const float* __restrict__ u,
+                                void* __restrict__ out, long n, int bf16) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = silu_f32(g[i]) * u[i];
+  if (bf16) ((uint16_t*)out)[i] = f32_to_bf16(v);
+  else ((float*)out)[i] = v;
+}
+
 __global__ void axpy_rows_kernel(float* __restrict__ out,
                                  const float* __restrict__ y,
                                  const float* __restrict__ w, int n, int H) {
@@ -259,6 +269,19 @@ int sllm_q4_swiglu_dev(const float* g, const float* u, float* out, long n) {
   SLLM_REQUIRE(g && u && out && n >= 0, "sllm_q4_swiglu_dev: bad args");
   if (n == 0) return 0;
   swiglu_elem_kernel<<<blocks_for(n), 256>>>(g, u, out, n);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+// ref: kernels/cuda/kernels.cu:897-919 (sllm_silu_mul): out = silu(g) * u
+// from fp32 g, u, stored as fp32 (out_type 0) or bf16 (out_type 1, RNE);
+// device pointers; n <= 0 does nothing.
+int sllm_silu_mul(const void* g, const void* u, void* out, long n,
+                  int out_type) {
+  if (n <= 0) return 0;
+  SLLM_REQUIRE(g && u && out, "sllm_silu_mul: null pointer");
+  silu_mul_kernel<<<blocks_for(n), 256>>>((const float*)g, (const float*)u,
+                                         out, n, out_type == 1);
   SLLM_LAUNCHED();
   return 0;
 }

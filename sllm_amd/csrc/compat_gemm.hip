@@ -57,6 +57,15 @@ __device__ __forceinline__ float load_b_elem(const BDesc& d, int n, int k,
   }
 }
 
+// sllm_q4_gemv_rows' post-op, in place: 1 silu(x / scale), 2 sigmoid.
+__global__ void post_act_kernel(float* __restrict__ v, long n, int post,
+                                float scale) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = v[i] / scale;
+  v[i] = post == 1 ? silu_f32(x) : sigmoid_f32(x);
+}
+
 // 32x32 output tile per 256-thread block; each thread 4 outputs (rows).
 __global__ __launch_bounds__(256) void tiled_gemm_kernel(
     const void* __restrict__ a, int a_bf16, BDesc bd, float* __restrict__ c,
@@ -247,6 +256,52 @@ int sllm_gemm_ex(const void* a, int atype, const void* w, void* c, int m,
                        (float*)c, nullptr);
   BDesc bd{atype == 1 ? B_BF16 : B_F32, w, nullptr, 0, 0};
   return launch_tiled_gemm(a, atype, bd, (float*)c, m, n, k, 0);
+}
+
+// ref: kernels/cuda/qwen4.cu:98-136, :699-708 (sllm_q4_gemv_rows[_dev]):
+// out (rows, O) fp32 = A (rows, K) . W (O, K)^T, then post 1: silu(x /
+// scale), post 2: sigmoid(x / scale), other values: none. rows, K or O
+// not positive: -1, as the reference. Batches of at most 64 rows on the
+// unpacked-weight GEMV (fp32 weight rows), larger ones on the tiled kernel.
+int sllm_q4_gemv_rows_dev(const float* A, const float* W, float* out, int rows,
+                          int K, int O, int post, float scale) {
+  SLLM_REQUIRE(rows > 0 && K > 0 && O > 0,
+               "sllm_q4_gemv_rows: rows, K, O must be positive");
+  SLLM_REQUIRE(A && W && out, "sllm_q4_gemv_rows: null pointer");
+  int rc;
+  if (rows <= 64 && O % 16 == 0 && K % 4 == 0) {
+    rc = launch_gemv(3, 0, A, 0, 0, nullptr, 1, rows, nullptr, nullptr, 1,
+                     nullptr, (const uint8_t*)W, nullptr, nullptr, nullptr, O,
+                     K, nullptr, 0.f, out, nullptr);
+  } else {
+    BDesc bd{B_F32, W, nullptr, 0, 0};
+    rc = launch_tiled_gemm(A, 0, bd, out, rows, O, K, 0);
+  }
+  if (rc || (post != 1 && post != 2)) return rc;
+  const long n = (long)rows * O;
+  post_act_kernel<<<(unsigned)((n + 255) / 256), 256>>>(out, n, post, scale);
+  SLLM_LAUNCHED();
+  return 0;
+}
+
+int sllm_q4_gemv_rows(const float* A, const float* W, float* out, int rows,
+                      int K, int O, int post, float scale) {
+  SLLM_REQUIRE(rows > 0 && K > 0 && O > 0,
+               "sllm_q4_gemv_rows: rows, K, O must be positive");
+  SLLM_REQUIRE(A && W && out, "sllm_q4_gemv_rows: null pointer");
+  const size_t sa = (size_t)rows * K * 4, sw = (size_t)O * K * 4,
+               so = (size_t)rows * O * 4;
+  Tmp dA, dW, dO;
+  SLLM_HIP(hipMalloc(&dA.p, sa));
+  SLLM_HIP(hipMalloc(&dW.p, sw));
+  SLLM_HIP(hipMalloc(&dO.p, so));
+  SLLM_HIP(hipMemcpy(dA.p, A, sa, hipMemcpyHostToDevice));
+  SLLM_HIP(hipMemcpy(dW.p, W, sw, hipMemcpyHostToDevice));
+  if (sllm_q4_gemv_rows_dev((const float*)dA.p, (const float*)dW.p,
+                            (float*)dO.p, rows, K, O, post, scale))
+    return -1;
+  SLLM_HIP(hipMemcpy(out, dO.p, so, hipMemcpyDeviceToHost));
+  return 0;
 }
 
 }  // extern "C"

@@ -72,6 +72,23 @@ def shared_gate_accum(out, shared, g) -> np.ndarray:
     return out
 
 
+def gemv_rows(A, W, post=0, scale=1.0) -> np.ndarray:
+    """out (rows, O) = A (rows, K) . W (O, K)^T, then post 1: silu(x /
+    scale), 2: sigmoid(x / scale) (ref kernels/_q4_cuda.py:167-175)."""
+    A, W = _f(A), _f(W)
+    rows, K = A.shape
+    O = W.shape[0]
+    out = np.empty((rows, O), np.float32)
+    _check(_lib.lib().sllm_q4_gemv_rows(_fp(A), _fp(W), _fp(out), rows, K, O,
+                                        int(post), float(scale)))
+    return out
+
+
+def gemv_rows_dev(A, W, out, rows, K, O, post=0, scale=1.0):
+    _check(_lib.lib().sllm_q4_gemv_rows_dev(ptr(A), ptr(W), ptr(out), rows, K,
+                                            O, int(post), float(scale)))
+
+
 def moe_router_dev(logits, w_out, id_out, n, E, topk):
     _check(_lib.lib().sllm_q4_moe_router_dev(ptr(logits), ptr(w_out),
                                              ptr(id_out), n, E, int(topk)))

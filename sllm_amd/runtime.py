@@ -237,6 +237,14 @@ def memset(buf, value: int, nbytes: int, stream=None) -> None:
                                       stream_handle(stream)), "sllm_memset")
 
 
+def silu_mul(g, u, out, out_type: int = T_F32) -> None:
+    """out = silu(g) * u over g's floats, stored as `out_type` (fp32 or bf16)
+    (ref kernels/_sllm_cuda.py:529-532)."""
+    n = g.nbytes // 4
+    _lib.check(_lib.lib().sllm_silu_mul(ptr(g), ptr(u), ptr(out), int(n),
+                                        int(out_type)), "sllm_silu_mul")
+
+
 def gemm_ex(a, w, c, m: int, n: int, k: int, atype: int = T_F32) -> None:
     """c (m,n) fp32 = a (m,k) . w (n,k)^T with a, w in dtype `atype`
     (ref kernels/_sllm_cuda.py:503-506)."""

@@ -119,6 +119,55 @@ def test_fp8_gemm_decode_shapes(M, N, K):
     assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-6)
 
 
+@pytest.mark.parametrize("rows,K,O", [(1, 2048, 512), (7, 100, 48), (80, 64, 30)])
+@pytest.mark.parametrize("post,scale", [(0, 1.0), (1, 2.0), (2, 0.5)])
+def test_q4_gemv_rows(rows, K, O, post, scale):
+    """sllm_q4_gemv_rows (host) and _dev: A . W^T then silu / sigmoid of
+    x / scale (ref kernels/cuda/qwen4.cu:95-136), against fp64; bad sizes
+    return -1. Shapes take the GEMV path (rows <= 64, O % 16 == 0) and the
+    tiled one."""
+    from sllm_amd import q4
+    from sllm_amd.runtime import DeviceBuffer, sync, to_device
+    rng = np.random.default_rng(rows * K + O + post)
+    A = rng.standard_normal((rows, K)).astype(np.float32)
+    W = (rng.standard_normal((O, K)) * 0.05).astype(np.float32)
+    x = A.astype(np.float64) @ W.astype(np.float64).T
+    if post == 1:
+        want = (x / scale) / (1 + np.exp(-(x / scale)))
+    elif post == 2:
+        want = 1 / (1 + np.exp(-(x / scale)))
+    else:
+        want = x
+    np.testing.assert_allclose(q4.gemv_rows(A, W, post, scale), want, rtol=2e-5, atol=2e-5)
+    out = DeviceBuffer(rows * O * 4)
+    q4.gemv_rows_dev(to_device(A), to_device(W), out, rows, K, O, post, scale)
+    sync()
+    np.testing.assert_allclose(out.copy_host().reshape(rows, O), want, rtol=2e-5, atol=2e-5)
+    with pytest.raises(RuntimeError):
+        q4.gemv_rows(np.zeros((0, 4), np.float32), np.zeros((4, 4), np.float32))
+
+
+def test_silu_mul_f32_and_bf16():
+    """sllm_silu_mul: out = silu(g) * u stored as fp32 or bf16 (RNE), with
+    an odd element count (ref kernels/cuda/kernels.cu:897-919)."""
+    from sllm_amd.runtime import DeviceBuffer, T_BF16, T_F32, silu_mul, sync, to_device
+    rng = np.random.default_rng(3)
+    n = 1001
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+    gd, ud = to_device(g), to_device(u)
+    o32 = DeviceBuffer(n * 4)
+    silu_mul(gd, ud, o32, T_F32)
+    o16 = DeviceBuffer(n * 2 + 2)
+    silu_mul(gd, ud, o16, T_BF16)
+    sync()
+    np.testing.assert_allclose(o32.copy_host()[:n], want, rtol=1e-5, atol=1e-6)
+    got16 = o16.copy_host_raw(np.uint16, (n + 1,))[:n]
+    want16 = (codecs.round_bf16(o32.copy_host()[:n]).view(np.uint32) >> 16).astype(np.uint16)
+    np.testing.assert_array_equal(got16, want16)
+
+
 def test_fp4_linear_matches_dequant():
     from sllm_amd import deepseek
     rng = np.random.default_rng(5)
