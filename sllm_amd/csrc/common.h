@@ -172,6 +172,22 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Maximum over the wave's four 16-lane rows at each row position (lanes
+// l, l ^ 16, l ^ 32, l ^ 48), by gfx950's row-swap permutes: one VALU
+// instruction each instead of an LDS shuffle's round trip. Given the same
+// value as both operands, v_permlane16_swap returns rows (2i, 2i + 1) as
+// (even, even) and (odd, odd), so the maximum of its two results is the
+// pair's maximum on both rows; v_permlane32_swap does the same for the row
+// pairs (0, 1) and (2, 3).
+__device__ __forceinline__ float rows4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float silu_f32(float x) {
   return x / (1.0f + expf(-x));
 }

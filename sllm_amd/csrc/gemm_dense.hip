@@ -225,8 +225,7 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
                 amax = fmaxf(amax, fabsf(h));
               }
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            amax = rows4_max(amax);
             if (lg == 0) red[t][wave] = amax;
           }
         }

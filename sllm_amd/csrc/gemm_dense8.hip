@@ -203,8 +203,7 @@ __global__ __launch_bounds__(D8_THREADS, 1) void moe_dense8_kernel(
                 amax = fmaxf(amax, fabsf(h));
               }
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            amax = rows4_max(amax);
             if (lg == 0) red[t][wc] = amax;
           }
         }

@@ -463,8 +463,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
             acc[mi][0][v] = h;
             amax = fmaxf(amax, fabsf(h));
           }
-          amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+          amax = rows4_max(amax);
           if (lg == 0) red[t][wave] = amax;
         }
       }
