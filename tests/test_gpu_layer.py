@@ -76,7 +76,7 @@ def test_qwen_prefill_c2_shapes():
 
 @pytest.mark.parametrize("T,E,k", [(200, 200, 8), (300, 512, 10),
                                    (130, 1024, 10), (257, 96, 16), (65, 128, 1),
-                                   (100, 2048, 10)])
+                                   (100, 2048, 10), (80, 16, 16), (70, 129, 4)])
 def test_qwen_fused_router_matches_full_row_routing(T, E, k):
     """Prefill router fused with routing: each 128-expert tile's top-k keys
     and softmax partials, merged by the routing launch, against the
@@ -86,7 +86,8 @@ def test_qwen_fused_router_matches_full_row_routing(T, E, k):
     the default call (no logits copy) gives the same output bit for bit.
     Cases: a partial last tile (E 200, 96), 80 candidate keys (E 1024),
     top-16 from one tile, top-1, ragged 64-token tiles, 160 candidates
-    (E 2048: the merge's wave-per-token form)."""
+    (E 2048: the merge's wave-per-token form), every expert picked (E 16,
+    top-16), a last tile of one expert (E 129)."""
     x, W = qwen_fp8_gpu(seed=T + E, T=T, H=512, E=E, I=128, Is=128)
     layer = qwen_layer(W, k)
     y_f, r_f = layer.forward(x, mode="prefill", return_routing=True)
