@@ -67,8 +67,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
       uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f32_to_bf16(acc[2 * i]) |
-               ((uint32_t)f32_to_bf16(acc[2 * i + 1]) << 16);
+        w[i] = pk_bf16(acc[2 * i], acc[2 * i + 1]);
       *(uint4*)((uint16_t*)out + (size_t)t * H + c) =
           make_uint4(w[0], w[1], w[2], w[3]);
     }
@@ -138,8 +137,7 @@ __global__ __launch_bounds__(64 * CF_WAVES) void combine_f32_kernel(
     *(float4*)((float*)out + (size_t)t * H + c) = acc;
   } else {
     *(uint2*)((uint16_t*)out + (size_t)t * H + c) =
-        make_uint2((uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16),
-                   (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16));
+        make_uint2(pk_bf16(acc.x, acc.y), pk_bf16(acc.z, acc.w));
   }
 }
 

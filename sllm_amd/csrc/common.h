@@ -68,11 +68,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even (inputs are finite).
+// fp32 -> bf16 bits, round to nearest even, by the gfx950 conversion
+// instruction (v_cvt_pk_bf16_f32; a NaN stays a NaN). pk_bf16 converts two
+// values in one instruction, a in the low half.
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(
+      uint32_t, __builtin_convertvector((f32x2_cvt){a, b}, bf16x2_cvt));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // One OCP E4M3FN byte (selected by `sel`, 0..3 of a dword) -> fp32, using the

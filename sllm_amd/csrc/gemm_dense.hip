@@ -273,10 +273,8 @@ __global__ __launch_bounds__(DN_THREADS, 1) void moe_dense_kernel(
               uint16_t* yrow = S.y + (size_t)(rb + t) * N + slab * 256 + ow0 * 32;
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
-                const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][j][0] * rw) |
-                                    ((uint32_t)f32_to_bf16(acc[mi][j][1] * rw) << 16);
-                const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][j][2] * rw) |
-                                    ((uint32_t)f32_to_bf16(acc[mi][j][3] * rw) << 16);
+                const uint32_t lo = pk_bf16(acc[mi][j][0] * rw, acc[mi][j][1] * rw);
+                const uint32_t hi = pk_bf16(acc[mi][j][2] * rw, acc[mi][j][3] * rw);
                 *(uint2*)(yrow + j * 16 + lg * 4) = make_uint2(lo, hi);
               }
             }

@@ -247,10 +247,8 @@ __global__ __launch_bounds__(D8_THREADS, 1) void moe_dense8_kernel(
               uint16_t* yrow = S.y + (size_t)(rb + t) * N + np * 256 + 64 * wc;
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
-                const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][q][0] * rw) |
-                                    ((uint32_t)f32_to_bf16(acc[mi][q][1] * rw) << 16);
-                const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][q][2] * rw) |
-                                    ((uint32_t)f32_to_bf16(acc[mi][q][3] * rw) << 16);
+                const uint32_t lo = pk_bf16(acc[mi][q][0] * rw, acc[mi][q][1] * rw);
+                const uint32_t hi = pk_bf16(acc[mi][q][2] * rw, acc[mi][q][3] * rw);
                 *(uint2*)(yrow + 16 * q + lg * 4) = make_uint2(lo, hi);
               }
             }

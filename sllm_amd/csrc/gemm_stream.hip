@@ -516,10 +516,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
           const float w = rwl[i][t];
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
-            const uint32_t lo = (uint32_t)f32_to_bf16(acc[mi][s][0] * w) |
-                                ((uint32_t)f32_to_bf16(acc[mi][s][1] * w) << 16);
-            const uint32_t hi = (uint32_t)f32_to_bf16(acc[mi][s][2] * w) |
-                                ((uint32_t)f32_to_bf16(acc[mi][s][3] * w) << 16);
+            const uint32_t lo = pk_bf16(acc[mi][s][0] * w, acc[mi][s][1] * w);
+            const uint32_t hi = pk_bf16(acc[mi][s][2] * w, acc[mi][s][3] * w);
             *(uint2*)(ystage + t * YS + wave * 32 + s * 16 + lg * 4) =
                 make_uint2(lo, hi);
           }
