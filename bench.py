@@ -10,7 +10,10 @@ region; weights are synthetic N(0, 0.02) quantized to e4m3 with fp32 128x128
 block scales, activations bf16 N(0, 1).
 
 Timing: HIP events on the stream the layer is launched on, K steps after W
-warm-up steps, bracketed by device synchronisation. Then, outside the headline
+warm-up steps, bracketed by device synchronisation. The default W (100) is
+long enough for the GPU's clocks to settle after idle (~40 ms of
+uninterrupted work), so the default K steps time the steady state of
+back-to-back layer calls. Then, outside the headline
 number: a per-stage event breakdown (the roofline of the dominant kernel),
 the C3 decode batches (B = 1, 8, 32, 64; per-call events, L2/MALL flushed with
 a 512 MiB fill between calls), and the CPU baseline (the numpy restatement of
@@ -798,8 +801,11 @@ def run_decode_batch(args):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    # the GPU's clocks take ~40 ms of uninterrupted work to settle after
+    # idle (C2 calls: 0.475 ms in the first 10 ms, 0.41 ms from ~40 ms on);
+    # 100 warm-up calls are ~45 ms at C2
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--decode-iters", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
