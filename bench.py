@@ -590,7 +590,7 @@ def c5_result(args):
 
 
 # --------------------------------------------------------------------------
-# algorithmic work (formulas as in SURVEY section 8(d))
+# algorithmic work: FLOPs of the GEMMs, bytes of the weights, scales and rows moved
 # --------------------------------------------------------------------------
 def prefill_work(c, touched):
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
@@ -631,7 +631,7 @@ def cpu_baseline(layer, x_host):
     quantized layer in expert-grouped form (oracle act_quant, fp32 BLAS),
     router GEMM and softmax top-k, activation quant, all routed experts with
     their tokens, the shared expert and its gate. Weights are dequantized to
-    fp32 outside the timed region (SURVEY's plan: 6.4 GB for C2). One warm-up,
+    fp32 outside the timed region (6.4 GB for C2). One warm-up,
     then the median of 3 runs; no extrapolation."""
     import numpy as np
     from threadpoolctl import threadpool_limits
