@@ -498,25 +498,27 @@ C5_EMPTY_FRAC = 20   # the lowest-ranked E / 20 experts receive no tokens
 
 
 def c5_inputs(layer):
-    """C5 activations and skewed router logits: x as c2_inputs, logits =
-    x . router_w^T - beta ln(rank_e) with ranks a seeded permutation of
-    1..E and beta calibrated (bisection on the first 2048 tokens) so that the
-    top 10% of experts receive 60% of the assignments; the E / 20 experts of
-    the lowest ranks get a further -64 (a softmax weight below 1e-27 of the
-    others), so that they receive no tokens. Returns (x, logits, beta) on
-    the host."""
+    """C5 activations and the skewed routing bias: x as c2_inputs; the
+    router logits x . router_w^T get the per-expert bias
+    b_e = -beta ln(rank_e) with ranks a seeded permutation of 1..E and beta
+    calibrated (bisection on the first 2048 tokens' host logits) so that
+    the top 10% of experts receive 60% of the assignments; the E / 20
+    experts of the lowest ranks get a further -64 (a softmax weight below
+    1e-27 of the others), so that they receive no tokens. The layer adds
+    the bias to the logits its router GEMM computes (router_bias). Returns
+    (x, bias (E,) float32, beta) on the host."""
     import numpy as np
     c = layer.cfg
     E, k = c["E"], c["k"]
     xh = c2_inputs(layer)
     rwh = to_bf16_values(layer.router_w_host)
-    logits0 = (xh @ rwh.T).astype(np.float32)
+    logits0 = (xh[:2048] @ rwh.T).astype(np.float32)
     rank = layer.rng.permutation(E) + 1
     off = np.where(rank > E - E // C5_EMPTY_FRAC, 64.0, 0.0)
     top = E // 10
 
-    def share(beta, n=2048):
-        lg = logits0[:n] - beta * np.log(rank)[None, :] - off[None, :]
+    def share(beta):
+        lg = logits0 - beta * np.log(rank)[None, :] - off[None, :]
         ids = np.argpartition(-lg, k, axis=1)[:, :k]
         cnt = np.bincount(ids.ravel(), minlength=E)
         return np.sort(cnt)[::-1][:top].sum() / cnt.sum()
@@ -526,8 +528,8 @@ def c5_inputs(layer):
         mid = 0.5 * (lo + hi)
         lo, hi = (mid, hi) if share(mid) < 0.6 else (lo, mid)
     beta = 0.5 * (lo + hi)
-    logits = (logits0 - beta * np.log(rank)[None, :] - off[None, :]).astype(np.float32)
-    return xh, logits, beta
+    bias = (-beta * np.log(rank) - off).astype(np.float32)
+    return xh, bias, beta
 
 
 def run_c5(args):
@@ -536,10 +538,11 @@ def run_c5(args):
 
 
 def c5_result(args):
-    """C5: C2 shapes at T=16384 with Zipf-skewed routing (logit bias
-    -beta ln(rank_e), ranks a seeded permutation of 1..E, beta calibrated so
-    the top 10% of experts take ~60% of assignments); logits are computed on
-    the host and passed in, so the timed layer excludes the router GEMM."""
+    """C5: C2 shapes at T=16384 with Zipf-skewed routing: the whole layer
+    from bf16 x, router GEMM included, with the per-expert routing bias
+    -beta ln(rank_e) added to its logits (ranks a seeded permutation of
+    1..E, beta calibrated so the top 10% of experts take ~60% of the
+    assignments)."""
     import numpy as np
     from sllm_amd.moe import STAGES, qwen_workspace_bytes
     from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
@@ -547,18 +550,17 @@ def c5_result(args):
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     t0 = time.perf_counter()
     layer = DeviceLayer(c, seed=args.seed)
-    xh, logits, beta = c5_inputs(layer)
+    xh, bias, beta = c5_inputs(layer)
     top = E // 10
     x = to_device_raw(to_bf16(xh))
-    lg = to_device_raw(logits)
+    wts = dict(layer.w, router_bias=to_device_raw(bias))
     out = DeviceBuffer(T * H * 2)
-    ws = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, "prefill",
-                                           logits_given=True))
+    ws = DeviceBuffer(qwen_workspace_bytes(T, H, E, I, Is, k, "prefill"))
     from sllm_amd.moe import qwen_forward_dev
 
     def call(debug=None, ev=None):
-        qwen_forward_dev(x, out, layer.w, T=T, H=H, E=E, I=I, Is=Is, topk=k,
-                         mode="prefill", out_f32=False, logits=lg, workspace=ws,
+        qwen_forward_dev(x, out, wts, T=T, H=H, E=E, I=I, Is=Is, topk=k,
+                         mode="prefill", out_f32=False, workspace=ws,
                          debug=debug, stage_events=ev)
     cnt = DeviceBuffer(E * 4)
     call(debug={"counts_out": cnt})
@@ -570,10 +572,8 @@ def c5_result(args):
         f"{share_top:.3f}, empty experts {E - touched}")
     ms = _time_layer(call, args.steps, args.warmup)
     st = _stage_times(lambda ev: call(ev=ev), len(STAGES))
-    flops = 6 * H * I * T * k + 6 * H * Is * T
-    wbytes = touched * 3 * H * I + touched * 3 * (H // 128) * (I // 128) * 4
-    bytes_ = wbytes + 3 * H * Is + 2 * T * H * 2 + T * E * 4
-    res = {"metric": "C5 MoE layer tokens/s (prefill, skewed routing, logits given)",
+    flops, bytes_ = prefill_work(c, touched)
+    res = {"metric": "C5 MoE layer tokens/s (prefill, skewed routing, router GEMM included)",
            "value": round(T / (ms / 1e3), 1), "unit": "tokens/s",
            "ms_per_step": round(ms, 4), "steps": args.steps,
            "config": {"workload": "C5 Qwen-style FP8 MoE layer, Zipf-skewed prefill", **c,
@@ -582,6 +582,9 @@ def c5_result(args):
            "layer": {"flops": flops, "bytes": bytes_,
                      "mfma_frac": round(flops / (ms / 1e3) / (PEAK_FP8_TFLOPS * 1e12), 4),
                      "hbm_frac": round(bytes_ / (ms / 1e3) / (PEAK_HBM_GBPS * 1e9), 4),
+                     "attainable_frac": round(
+                         max(flops / (PEAK_FP8_TFLOPS * 1e12), bytes_ / (PEAK_HBM_GBPS * 1e9))
+                         / (ms / 1e3), 4),
                      "stage_ms": st, "touched_experts": touched,
                      "empty_experts": E - touched}}
     del layer
@@ -626,6 +629,20 @@ def decode_bytes(c, B, touched):
 # --------------------------------------------------------------------------
 # CPU baseline: numpy restatement of the quantized layer, bounded sample
 # --------------------------------------------------------------------------
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform's
+    processor string where that file is absent."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(layer, x_host):
     """The whole C2 layer on this host's cores: the numpy restatement of the
     quantized layer in expert-grouped form (oracle act_quant, fp32 BLAS),
@@ -684,7 +701,7 @@ def cpu_baseline(layer, x_host):
     sec = statistics.median(runs)
     return {
         "value": round(T / sec, 2), "unit": "tokens/s", "cores": cores,
-        "kind": "port",
+        "cpu_model": cpu_model(), "kind": "port",
         "sample": (f"the whole C2 layer ({T} tokens, all {E} experts, shared "
                    f"expert), numpy restatement of the quantized layer (oracle "
                    f"act_quant + fp32 BLAS on weights dequantized beforehand, "
@@ -723,7 +740,7 @@ def cpu_c1_literal_loop():
     ms = statistics.median(times) * 1e3
     return {"config": "C1 (64 tokens, H 1024, E 16, top-4, I 512, bf16 weights)",
             "ms": round(ms, 2), "tokens_per_s": round(T / (ms / 1e3), 1),
-            "cores": 1, "note": "median of 3 after a warm-up"}
+            "cores": 1, "cpu_model": cpu_model(), "note": "median of 3 after a warm-up"}
 
 
 # --------------------------------------------------------------------------
@@ -806,6 +823,9 @@ def main(argv=None) -> int:
     # idle (C2 calls: 0.475 ms in the first 10 ms, 0.41 ms from ~40 ms on);
     # 100 warm-up calls are ~45 ms at C2
     ap.add_argument("--warmup", type=int, default=100)
+    # clock settle, before (and not counted in) the warm-up calls: layer
+    # calls until this much wall time has passed, reported as its own key
+    ap.add_argument("--settle-ms", type=float, default=100.0)
     ap.add_argument("--decode-iters", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -881,6 +901,18 @@ def main(argv=None) -> int:
     counts = dbg["counts_out"].copy_host_raw(np.int32, (E,))
     touched = int((counts > 0).sum())
     log(f"setup {time.perf_counter() - t_setup:.1f}s; touched experts {touched}")
+
+    # ---- clock settle (reported as "settle"), then the warm-up calls -----
+    settle_calls, s0 = 0, time.perf_counter()
+    while (time.perf_counter() - s0) * 1e3 < args.settle_ms:
+        for _ in range(16):
+            layer_call(layer, x, out, ws, T, "prefill")
+        sync()
+        settle_calls += 16
+    settle = {"calls": settle_calls,
+              "ms": round((time.perf_counter() - s0) * 1e3, 1),
+              "note": "layer calls before the warm-up so the clocks ramp up; "
+                      "not counted in warmup"}
 
     # ---- headline: K steps of the full layer ---------------------------
     for _ in range(args.warmup):
@@ -975,6 +1007,7 @@ def main(argv=None) -> int:
     res = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "settle": settle,
         "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3",
         "data": "synthetic (seeded N(0,0.02) weights quantized on device, bf16 N(0,1) activations)",

@@ -231,11 +231,29 @@ int sllm_moe_pack_weights(int fp4, int up, const void* w0, const void* w1,
  * leaves them undone; sllm_moe_stream_status synchronizes `stream`, returns
  * -2 (and clears the mark) if any launch did so since the last call, else 0.
  * sllm_moe_tile_bound is the bound of sum_e ceil(n_e / bm) for N
- * assignments over E experts; sllm_moe_stream_grid is the grid used for an
- * item bound on num_cus CUs (host-only queries). */
+ * assignments over E experts; sllm_moe_stream_grid is the grid for an item
+ * bound on num_cus CUs when each XCD takes a contiguous eighth of the
+ * items, sllm_moe_stream_dec_grid when they are dealt to the XCDs in chunks
+ * of `chunk` consecutive items (the decode kernel's deal); host-only
+ * queries. */
 int sllm_moe_stream_status(void* stream);
 long sllm_moe_tile_bound(long N, int E, int bm);
 long sllm_moe_stream_grid(long upper_items, int num_cus);
+long sllm_moe_stream_dec_grid(long upper_items, int num_cus, long chunk);
+/* Host plan query (new: no reference counterpart; no device work): what the
+ * fused layer (deepseek = 0: sllm_moe_qwen_forward with packed FP8 weights,
+ * 1: sllm_moe_ds_forward) plans for a shape. Is = 0: no shared expert.
+ * out[0..9]: decode, bm (routed rows per tile), bm_sh, max_tiles, ks_r
+ * (router K slices), ks_up, ks_up_sh, ks_dn, ks_dn_sh (decode K chunks),
+ * #CUs used for planning; then, decode only, for the streamed launches
+ * j = 0 gate/up, 1 down (Qwen: routed + shared segment), 2 and 3 the
+ * DeepSeek shared expert's gate/up and down: out[10 + 3j] the launch's
+ * item bound, out[11 + 3j] its XCD deal chunk, out[12 + 3j] its grid
+ * (0 where a launch does not run). n_out >= SLLM_MOE_PLAN_FIELDS. */
+#define SLLM_MOE_PLAN_FIELDS 22
+int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,
+                        int topk, int mode, int logits_given, long* out,
+                        int n_out);
 /* Synthetic-weight quantizers (data preparation): FP8 128x128 block
  * (s = amax/448, optionally its power-of-two ceiling) and MXFP4 per 32. */
 int sllm_quantize_weight_fp8(const float* w, int N, int K, int pow2,
@@ -327,6 +345,12 @@ typedef struct sllm_moe_qwen_args {
    * one-expert top-1 call on the routed path (which writes them). */
   int* sorted_out;
   int* inv_pos_out;
+  /* Optional per-expert routing bias (E fp32 on the device, or NULL; new: no
+   * reference counterpart -- the skewed-load configuration adds it to the
+   * router logits of ref/qwen4_exp.py:173 before moe_route): every token
+   * routes on softmax top-k of logits + router_bias, so the bias moves both
+   * the selection and the weights. logits_out holds the logits without it. */
+  const float* router_bias;
 } sllm_moe_qwen_args;
 
 long sllm_moe_qwen_workspace_bytes(const sllm_moe_qwen_args* a);

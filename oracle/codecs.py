@@ -118,7 +118,8 @@ def decode_ue8m0(u8) -> np.ndarray:
     """E8M0 bytes -> float32: 2^(u-127); 0x00 -> 0.0, 0xFF -> NaN
     (loaders/fp8.py:145-156)."""
     u8 = np.asarray(u8, dtype=np.uint8)
-    out = np.exp2(u8.astype(np.float64) - 127.0).astype(np.float32)
+    # 0xFF (NaN below) is kept out of the exponent: 2^128 overflows float32
+    out = np.exp2(np.minimum(u8, 0xFE).astype(np.float64) - 127.0).astype(np.float32)
     out = np.where(u8 == 0x00, np.float32(0.0), out)
     out = np.where(u8 == 0xFF, np.float32(np.nan), out)
     return out.astype(np.float32)
@@ -197,4 +198,7 @@ def dequant_fp4_block(packed, scale_u8, block_w: int = 32) -> np.ndarray:
     if s.shape[-1] != (k + block_w - 1) // block_w or s.shape[-2] != w.shape[-2]:
         raise ValueError(f"fp4 scale shape {s.shape} does not fit {w.shape}")
     cols = np.arange(k) // block_w
-    return w * s[..., cols]
+    # a product past float32's range is inf, as in the loader's float32
+    # product (e.g. 6 * 2^127); no warning for it
+    with np.errstate(over="ignore"):
+        return w * s[..., cols]

@@ -38,7 +38,7 @@ class QwenArgs(Structure):
         ("ids_out", P), ("counts_out", P), ("workspace", P),
         ("workspace_bytes", c_long), ("stream", P), ("stage_events", P),
         ("wgu_packed", P), ("wd_packed", P), ("sgu_packed", P), ("sd_packed", P),
-        ("sorted_out", P), ("inv_pos_out", P),
+        ("sorted_out", P), ("inv_pos_out", P), ("router_bias", P),
     ]
 
 
@@ -133,6 +133,9 @@ SIGNATURES = {
     "sllm_moe_stream_status": (c_int, [P]),
     "sllm_moe_tile_bound": (c_long, [c_long, c_int, c_int]),
     "sllm_moe_stream_grid": (c_long, [c_long, c_int]),
+    "sllm_moe_stream_dec_grid": (c_long, [c_long, c_int, c_long]),
+    "sllm_moe_plan_query": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int,
+                                    c_int, c_int, c_int, c_void_p, c_int]),
     "sllm_quantize_weight_fp8": (c_int, [P, c_int, c_int, c_int, P, P, P]),
     "sllm_quantize_weight_mxfp4": (c_int, [P, c_int, c_int, P, P, P]),
     "sllm_moe_qwen_workspace_bytes": (c_long, [POINTER(QwenArgs)]),

@@ -18,10 +18,14 @@
 //   of the routed segment or of the shared expert's; operands of step s+3
 //   are in flight while step s computes, across item boundaries.
 // * XCD-aware item order. Workgroups are dealt to the eight XCDs round-robin
-//   (blockIdx % 8); each XCD owns a contiguous range of items and its
-//   workgroups take that range's items round-robin, so the column slabs of
-//   one row tile run at the same time on one XCD and gather the same
-//   activation rows through that XCD's L2.
+//   (blockIdx % 8). Launches that stream their weights deal the items to
+//   the XCDs in chunks of one row tile's items (chunk c to XCD c % 8), so
+//   the column slabs of one row tile run at the same time on one XCD and
+//   gather the same activation rows through that XCD's L2, and every XCD
+//   gets the same mix of routed and shared-expert items. Launches whose
+//   weights go through L2 (an expert's tiles share them) give each XCD a
+//   contiguous range instead, so that an expert's tiles meet in one L2.
+//   Each XCD's workgroups take its items round-robin.
 // * Item descriptors and gathered row indices of a workgroup's items are
 //   loaded into LDS once at the start.
 #include <algorithm>
@@ -800,7 +804,12 @@ __device__ __forceinline__ void dec_fused_finish(
     const SegDesc& S = seg ? S1 : S0;
     if (S.ksplit <= 1) continue;  // finished in the item's epilogue
     int* c = F.cnt + (seg ? F.cnt1 : 0) + (long)d.z * (S.N / 128) + nt;
-    if (atomicAdd(c, 1) == S.ksplit - 1) jobs[atomicAdd(&njob, 1)] = i;
+    // acquire-release at device scope: the chunk sums this workgroup
+    // stored before the barrier happen before the arrival, and the
+    // finisher's reads of every chunk's sums happen after it
+    if (__hip_atomic_fetch_add(c, 1, __ATOMIC_ACQ_REL,
+                               __HIP_MEMORY_SCOPE_AGENT) == S.ksplit - 1)
+      jobs[atomicAdd(&njob, 1)] = i;
   }
   __syncthreads();
   const int nj = njob;
@@ -865,7 +874,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   // slabs and K chunks), so that every XCD gets the same mix of routed and
   // shared-expert items (as in the prefill kernel; C3 B=32 163.1 / 164.2 ->
   // 161.6 / 160.6 us, B=1 and B=8 unchanged)
-  const int CB = max(1, (S0.N / NTW) * max(1, S0.ksplit));
+  // (the host sizes the grid for this deal: stream_dec_grid)
+  const int CB = dec_deal_chunk(S0, NTW);
   const int ncf = total / CB, crem = total % CB;
   const int xcount = (ncf > xcd ? (ncf - xcd + 7) / 8 : 0) * CB + (ncf % 8 == xcd ? crem : 0);
   const int nitems = xcount > jx ? (xcount - jx + nx - 1) / nx : 0;
@@ -1294,6 +1304,10 @@ int launch_split_finish(const SegDesc& s0, const SegDesc* s1, float limit,
   return 0;
 }
 
+long dec_launch_grid(long upper_items, long chunk) {
+  return stream_dec_grid(upper_items, num_cus(), chunk, ST_MAX_ITEMS);
+}
+
 // Down: the combine adds the slices, so a split costs no launch; it must
 // save a fifth of the steps (the bound overstates routed items).
 int dec_ksplit(long upper_items, int KB) {
@@ -1398,8 +1412,19 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                                     upper_items, "stream decode gemm");
     if (rc) return rc;
   }
-  const long grid = stream_grid(upper_items, num_cus(), ST_MAX_ITEMS);
+  // the kernel deals its items to the XCDs in chunks of one row tile's
+  // items of the first segment (column slabs x K chunks)
+  const long cb = dec_deal_chunk(s0, MODE == 0 ? 128 : 256);
+  const long grid = dec_launch_grid(upper_items, cb);
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
+  {
+    const long nx = grid / 8;
+    const long worst = (chunked_xcd_share(upper_items, cb) + nx - 1) / nx;
+    SLLM_CAPACITY(worst <= ST_MAX_ITEMS,
+                  "stream decode gemm: %ld items per workgroup above %d "
+                  "(upper_items %ld, chunk %ld, grid %ld)", worst,
+                  ST_MAX_ITEMS, upper_items, cb, grid);
+  }
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
       s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse);
@@ -1514,6 +1539,14 @@ long sllm_moe_stream_grid(long upper_items, int num_cus) {
     return -1;
   }
   return stream_grid(upper_items, num_cus, ST_MAX_ITEMS);
+}
+
+long sllm_moe_stream_dec_grid(long upper_items, int num_cus, long chunk) {
+  if (upper_items < 0 || num_cus <= 0 || chunk <= 0) {
+    set_error("sllm_moe_stream_dec_grid: bad args");
+    return -1;
+  }
+  return stream_dec_grid(upper_items, num_cus, chunk, ST_MAX_ITEMS);
 }
 
 // Size in bytes of the packed weight (and, for fp4, of the packed scales).

@@ -29,11 +29,14 @@ struct ActQuant {
   const uint16_t* gate_w;
   float* gate_out;
 };
+// bias (E floats, or null): routing takes softmax top-k of logit + bias
+// (the Qwen layer's per-expert routing bias); the logits stay as given.
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st,
                          int ks = 1, float* gate = nullptr,
                          int* chunk_hist = nullptr,
-                         const ActQuant* aq = nullptr);
+                         const ActQuant* aq = nullptr,
+                         const float* bias = nullptr);
 // Fused prefill router (softmax routing, router_topk_fits): per token t
 // and 128-expert tile y of the ny = ceil(E / 128) tiles, the tile's largest
 // logit m and sum of exp(l - m) at stat[2 (t ny + y)] (+1), and its topk
@@ -55,6 +58,10 @@ struct RouterPart {
   const uint16_t* gate_w;
   float* gate_out;
   int pow2;  // quantization scales rounded up to powers of two
+  // keys mode: per-expert routing bias (E floats, or null) added to the
+  // logits before the tiles' top-k and softmax partials (logits stays
+  // without it)
+  const float* bias;
 };
 bool router_topk_fits(int T, int E, int topk, int H);
 size_t router_part_bytes(int T, int E, int topk);
@@ -88,7 +95,7 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int* inv_pos, int* tile_info, int* num_tiles,
                                int max_tiles, hipStream_t st, int ks = 1,
                                float* gate = nullptr, int* zero = nullptr,
-                               int nzero = 0);
+                               int nzero = 0, const float* bias = nullptr);
 int launch_route_grouped(const float* logits, const float* bias, float* w,
                          int* ids, int T, int E, int topk, int n_group,
                          int topk_group, int scoring, float route_scale,
@@ -160,6 +167,30 @@ inline long stream_grid(long upper_items, int num_cus, int max_items) {
   if (need > nx) nx = need;
   return 8 * nx;
 }
+// Most items one XCD receives when `total` items are dealt to the XCDs in
+// chunks of `chunk` consecutive items (chunk c to XCD c % 8, the trailing
+// partial chunk to XCD (total / chunk) % 8), as the decode kernel deals
+// them: with ncf = total / chunk = 8a + r full chunks and a remainder
+// crem, XCDs below r hold a + 1 chunks and XCD r holds a chunks + crem, so
+// no XCD holds more than ceil(ceil(total / chunk) / 8) * chunk items. The
+// bound does not decrease as total grows, so its value at an item bound
+// covers every total up to that bound.
+inline long chunked_xcd_share(long total, long chunk) {
+  if (chunk < 1) chunk = 1;
+  return ((total + chunk - 1) / chunk + 7) / 8 * chunk;
+}
+// Persistent grid of a chunk-dealt launch (moe_stream_dec_kernel) with at
+// most upper_items items: #CUs rounded up to a multiple of 8, grown until
+// an XCD's largest share, dealt round-robin over its workgroups, gives no
+// workgroup more than max_items.
+inline long stream_dec_grid(long upper_items, int num_cus, long chunk,
+                            int max_items) {
+  const long per_xcd = chunked_xcd_share(upper_items, chunk);
+  long nx = (num_cus + 7) / 8;
+  const long need = (per_xcd + max_items - 1) / max_items;
+  if (need > nx) nx = need;
+  return 8 * nx;
+}
 
 struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   const uint8_t* a;        // A rows (row stride K bytes)
@@ -195,6 +226,13 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   // launch. Decode launches always stream.
   int wreuse;
 };
+// Items per XCD chunk of a decode launch: one row tile's items of its first
+// segment (column slabs of ntw columns x K chunks). The kernel deals with
+// this chunk and the host sizes the grid with it.
+__host__ __device__ inline int dec_deal_chunk(const SegDesc& s, int ntw) {
+  const int c = (s.N / ntw) * (s.ksplit > 1 ? s.ksplit : 1);
+  return c > 1 ? c : 1;
+}
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
                   hipStream_t st);
@@ -242,6 +280,9 @@ inline long dec_fuse_counters(long N, long T, int I, int Is) {
 // that would leave most CUs idle).
 int dec_ksplit(long upper_items, int KB);
 int dec_ksplit_up(long upper_items, int KB);
+// Grid of a decode streamed launch of at most upper_items items dealt in
+// chunks of `chunk` (dec_deal_chunk) on this device.
+long dec_launch_grid(long upper_items, long chunk);
 // h = silu(clamp(sum of gate slices)) * clamp(sum of up slices) for the
 // split mode-0 segments (limit > 0: the SwiGLU clamp of the DeepSeek path).
 int launch_split_finish(const SegDesc& s0, const SegDesc* s1, float limit,

@@ -37,6 +37,10 @@ struct Plan {
   int ks_up, ks_up_sh, ks_dn, ks_dn_sh, ks_r;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
+  // decode, streamed kernels: item bounds of the gate/up and down launches
+  // (Qwen: routed and shared segments in one launch each; DeepSeek: the
+  // shared expert's launches are the *_sh ones)
+  long up_items, dn_items, up_sh_items, dn_sh_items;
   size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters
   size_t rpart;  // Qwen prefill router partials (RouterPart), or 0
   size_t total;
@@ -126,6 +130,17 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
             dec_ksplit(rt * (H / 256) + sh_rt * (H / 256),
                        (has_shared ? std::min(I, Is) : I) / 128);
       }
+      p.up_items = rt * (I / 128) * p.ks_up;
+      p.dn_items = rt * (H / 256) * p.ks_dn;
+      const long sh_up = sh_rt * (Is / 128) * p.ks_up_sh;
+      const long sh_dn = sh_rt * (H / 256) * p.ks_dn_sh;
+      if (deepseek) {
+        p.up_sh_items = sh_up;
+        p.dn_sh_items = sh_dn;
+      } else {
+        p.up_items += sh_up;
+        p.dn_items += sh_dn;
+      }
     }
     p.hq = take(c, (size_t)p.N * I * 4);                      // h fp32
     p.hq_sh = has_shared ? take(c, (size_t)T * Is * 4) : 0;   // h_sh fp32
@@ -165,6 +180,15 @@ struct StageClock {
     return 0;
   }
 };
+
+// The code of two launch steps run in order, the second only after the
+// first succeeded: the first nonzero one, so that a -2 capacity code
+// reaches the entry point unchanged (an `a || b` of the two would be 1).
+template <typename F, typename G>
+static int first_rc(F f, G g) {
+  const int rc = f();
+  return rc ? rc : g();
+}
 
 // a failing stage's code (-1 error, -2 capacity) is the entry point's
 #define STAGE(clk, s, call)                                                   \
@@ -283,6 +307,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   // logits are not read, so a non-finite logit does not reach the output).
   const bool one_expert = p.decode && a->wgu_packed && E == 1 && k == 1 &&
                           a->logits_given && 1.0f + eps == 1.0f &&
+                          !a->router_bias &&
                           !a->logits_out && !a->w_out && !a->ids_out &&
                           !a->counts_out && !a->sorted_out && !a->inv_pos_out;
   // Decode-size routing: the router GEMM also computes the shared-expert
@@ -345,6 +370,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   RouterPart rp{};
   if (topk_router) {
     rp = router_part_at(ws + p.rpart, T, E, k);
+    rp.bias = a->router_bias;
     if (aq_fused) {
       rp.q = aq.q;
       rp.s = aq.s;
@@ -372,7 +398,8 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
                                      ntiles, p.max_tiles, st, p.ks_r,
-                                     gate_fin, fcnt, (int)nfcnt));
+                                     gate_fin, fcnt, (int)nfcnt,
+                                     a->router_bias));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE,
@@ -380,7 +407,8 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
               ? launch_route_merge(rp, T, E, eps, w, ids, st, chunk_hist)
               : launch_route_softmax(logits, w, ids, T, E, k, eps, st, p.ks_r,
                                      gate_fin, chunk_hist,
-                                     aq_fused ? &aq : nullptr));
+                                     aq_fused ? &aq : nullptr,
+                                     a->router_bias));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
           launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
                          tiles, ntiles, p.max_tiles, ws + p.pscr, st,
@@ -403,7 +431,6 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                    "sllm_moe_qwen_forward: packed weights incomplete");
       float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
       y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
-      const long sh_rt = sh ? (T + p.bm - 1) / p.bm : 0;
       SegDesc r1{}, s1{};
       r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
       r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
@@ -422,12 +449,18 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s1.pstride = (long)T * Is;
       const DecFuse f_up{fcnt, (long)p.N * (I / 128)};
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-            launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k, 0.f,
-                              (long)p.max_tiles * (I / 128) * p.ks_up +
-                                  sh_rt * (Is / 128) * p.ks_up_sh,
-                              st, p.bm, fused ? &f_up : nullptr) ||
-                (!fused && p.ks_up > 1 &&
-                 launch_split_finish(r1, sh ? &s1 : nullptr, 0.f, st)));
+            first_rc(
+                [&] {
+                  return launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k,
+                                           0.f, p.up_items, st, p.bm,
+                                           fused ? &f_up : nullptr);
+                },
+                [&] {
+                  return !fused && p.ks_up > 1
+                             ? launch_split_finish(r1, sh ? &s1 : nullptr,
+                                                   0.f, st)
+                             : 0;
+                }));
       SegDesc r2{}, s2{};
       r2.a = (const uint8_t*)h; r2.sorted_idx = sorted; r2.gather = 0;
       r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
@@ -445,9 +478,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
             launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
-                              (long)p.max_tiles * (H / 256) * p.ks_dn +
-                                  sh_rt * (H / 256) * p.ks_dn_sh,
-                              st, p.bm));
+                              p.dn_items, st, p.bm));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
       STAGE(clk, SLLM_MOE_STAGE_COMBINE,
@@ -520,11 +551,19 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       const bool sdense = rdense && sh && T > PREFILL_BM;
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             rdense && dense8_fits(0, r1)
-                ? launch_dense8(0, r1, 1, k, 0.f, 0, st, device_cus()) ||
-                      (sh && (sdense && dense8_fits(0, s1)
-                                  ? launch_dense8(0, s1, 1, k, 0.f, 0, st, device_cus())
-                                  : launch_stream(0, 0, s1, nullptr, k, 0.f, 0,
-                                                  sh_rt * (Is / 128), st)))
+                ? first_rc(
+                      [&] {
+                        return launch_dense8(0, r1, 1, k, 0.f, 0, st,
+                                             device_cus());
+                      },
+                      [&] {
+                        return !sh ? 0
+                               : sdense && dense8_fits(0, s1)
+                                   ? launch_dense8(0, s1, 1, k, 0.f, 0, st,
+                                                   device_cus())
+                                   : launch_stream(0, 0, s1, nullptr, k, 0.f, 0,
+                                                   sh_rt * (Is / 128), st);
+                      })
                 : launch_stream(0, 0, r1, sh ? &s1 : nullptr, k, 0.f, 0, up1, st));
       SegDesc r2{}, s2{};
       r2.wreuse = weights_reused(p.N, E, PREFILL_BM);
@@ -538,11 +577,19 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       const long up2 = (long)p.max_tiles * (H / 256) + sh_rt * (H / 256);
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
             rdense && dense8_fits(1, r2)
-                ? launch_dense8(1, r2, 1, k, 0.f, 0, st, device_cus()) ||
-                      (sh && (sdense && dense8_fits(1, s2)
-                                  ? launch_dense8(1, s2, 1, k, 0.f, 0, st, device_cus())
-                                  : launch_stream(0, 1, s2, nullptr, k, 0.f, 0,
-                                                  sh_rt * (H / 256), st)))
+                ? first_rc(
+                      [&] {
+                        return launch_dense8(1, r2, 1, k, 0.f, 0, st,
+                                             device_cus());
+                      },
+                      [&] {
+                        return !sh ? 0
+                               : sdense && dense8_fits(1, s2)
+                                   ? launch_dense8(1, s2, 1, k, 0.f, 0, st,
+                                                   device_cus())
+                                   : launch_stream(0, 1, s2, nullptr, k, 0.f, 0,
+                                                   sh_rt * (H / 256), st);
+                      })
                 : launch_stream(0, 1, r2, sh ? &s2 : nullptr, k, 0.f, 0, up2, st));
       // the shared expert ran inside the two launches above
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
@@ -717,6 +764,49 @@ long sllm_moe_ds_workspace_bytes(const sllm_moe_ds_args* a) {
       .total;
 }
 
+// Host plan query (no device work): the tiling and K splits the layer picks
+// for a shape, and for each streamed decode launch (gate/up, down, and the
+// DeepSeek shared expert's two) its item bound, XCD deal chunk and grid.
+int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,
+                        int topk, int mode, int logits_given, long* out,
+                        int n_out) {
+  SLLM_REQUIRE(out && n_out >= SLLM_MOE_PLAN_FIELDS && T > 0 && H > 0 &&
+                   E > 0 && I > 0 && Is >= 0 && topk > 0 && topk <= E &&
+                   H % 256 == 0 && I % 128 == 0 && Is % 128 == 0 &&
+                   mode >= 0 && mode <= 2,
+               "sllm_moe_plan_query: bad args (T=%d H=%d E=%d I=%d Is=%d "
+               "k=%d mode %d, %d outputs)", T, H, E, I, Is, topk, mode, n_out);
+  const Plan p = make_plan(T, H, E, I, Is, topk, mode, Is > 0, !logits_given,
+                           false, deepseek != 0);
+  for (int i = 0; i < SLLM_MOE_PLAN_FIELDS; ++i) out[i] = 0;
+  out[0] = p.decode;
+  out[1] = p.bm;
+  out[2] = p.bm_sh;
+  out[3] = p.max_tiles;
+  out[4] = p.ks_r;
+  out[5] = p.ks_up;
+  out[6] = p.ks_up_sh;
+  out[7] = p.ks_dn;
+  out[8] = p.ks_dn_sh;
+  out[9] = device_cus();
+  if (!p.decode) return 0;
+  // the first segment of each launch decides its deal chunk
+  const int segN[4] = {I, H, Is, H}, ntw[4] = {128, 256, 128, 256};
+  const int segks[4] = {p.ks_up, p.ks_dn, p.ks_up_sh, p.ks_dn_sh};
+  const long items[4] = {p.up_items, p.dn_items, p.up_sh_items, p.dn_sh_items};
+  for (int j = 0; j < 4; ++j) {
+    if (items[j] <= 0) continue;
+    SegDesc s{};
+    s.N = segN[j];
+    s.ksplit = segks[j];
+    const long cb = dec_deal_chunk(s, ntw[j]);
+    out[10 + 3 * j] = items[j];
+    out[11 + 3 * j] = cb;
+    out[12 + 3 * j] = dec_launch_grid(items[j], cb);
+  }
+  return 0;
+}
+
 }  // extern "C"
 
 namespace sllm {
@@ -836,7 +926,6 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     float* y = (float*)(ws + p.y);
     float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
     float* y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
-    const long sh_rt = (T + p.bm_sh - 1) / p.bm_sh;
     SegDesc r1{};
     r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
     r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
@@ -851,14 +940,17 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
-          launch_stream_dec(2, 0, r1, nullptr, k, L,
-                            (long)p.max_tiles * (I / 128) * p.ks_up, st,
-                            p.bm) ||
-              (p.ks_up > 1 && launch_split_finish(r1, nullptr, L, st)));
+          first_rc(
+              [&] {
+                return launch_stream_dec(2, 0, r1, nullptr, k, L, p.up_items,
+                                         st, p.bm);
+              },
+              [&] {
+                return p.ks_up > 1 ? launch_split_finish(r1, nullptr, L, st)
+                                   : 0;
+              }));
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-          launch_stream_dec(2, 1, r2, nullptr, k, 0.f,
-                            (long)p.max_tiles * (H / 256) * p.ks_dn, st,
-                            p.bm));
+          launch_stream_dec(2, 1, r2, nullptr, k, 0.f, p.dn_items, st, p.bm));
     if (sh) {
       SegDesc s1{};
       s1.a = (const uint8_t*)a->x; s1.total_rows = T;
@@ -872,13 +964,18 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
       s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
-            launch_stream_dec(1, 0, s1, nullptr, k, L,
-                              sh_rt * (Is / 128) * p.ks_up_sh, st,
-                              p.bm_sh) ||
-                (p.ks_up_sh > 1 && launch_split_finish(s1, nullptr, L, st)));
+            first_rc(
+                [&] {
+                  return launch_stream_dec(1, 0, s1, nullptr, k, L,
+                                           p.up_sh_items, st, p.bm_sh);
+                },
+                [&] {
+                  return p.ks_up_sh > 1
+                             ? launch_split_finish(s1, nullptr, L, st)
+                             : 0;
+                }));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN,
-            launch_stream_dec(1, 1, s2, nullptr, k, 0.f,
-                              sh_rt * (H / 256) * p.ks_dn_sh, st,
+            launch_stream_dec(1, 1, s2, nullptr, k, 0.f, p.dn_sh_items, st,
                               p.bm_sh));
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,

@@ -637,7 +637,10 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = wm * 32 + i * 16 + lg * 4 + v, c = we * 32 + j * 16 + lr;
-        lt[r * RG_LT + c] = acc[i][j][v];
+        // routing takes logit + bias (rp.bias: the per-expert routing
+        // bias); the caller's copy gets the logit itself
+        lt[r * RG_LT + c] = rp.bias && e0 + c < E ? acc[i][j][v] + rp.bias[e0 + c]
+                                                  : acc[i][j][v];
         if (logits && t0 + r < T && e0 + c < E)
           logits[(size_t)(t0 + r) * E + e0 + c] = acc[i][j][v];
       }
@@ -747,8 +750,10 @@ __device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
   }
 }
 
-// One token's softmax top-k on the calling wave: row = the token's E logits;
-// lanes j < topk write slot j of w_row / id_row (and of id_lds when given).
+// One token's softmax top-k on the calling wave: row = the token's E logits
+// (plus bias[e] when bias is given, after the slices are added; the row
+// keeps the logits without it); lanes j < topk write slot j of w_row /
+// id_row (and of id_lds when given).
 // The selection runs on the logits (softmax is monotone in them); pick j's
 // probability is exp(l - max) / sum recomputed from its key, and the
 // weights are those probabilities over their sum in pick order plus eps
@@ -756,10 +761,18 @@ __device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
 template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
 __device__ __forceinline__ void route_softmax_token(
     float* row, int ks, long kstride, int E, int topk, float eps,
-    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
+    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds,
+    const float* __restrict__ bias) {
   const int lane = threadIdx.x & 63;
   float v[EPL];
   logit_sums<EPL, G>(row, ks, kstride, E, true, -INFINITY, v);
+  if (bias) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) v[i] += bias[e];
+    }
+  }
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) m = fmaxf(m, v[i]);
@@ -790,7 +803,7 @@ template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
     float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
     int E, int topk, float eps, int ks, float* __restrict__ gate,
-    int* __restrict__ chunk_hist, ActQuant aq) {
+    int* __restrict__ chunk_hist, ActQuant aq, const float* __restrict__ bias) {
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (t >= T) return;
@@ -799,7 +812,7 @@ __global__ __launch_bounds__(256) void route_softmax_kernel(
   if (aq.x) act_quant_row(aq.x, t, aq.H, aq.pow2, aq.q, aq.s, aq.gate_w, aq.gate_out);
   route_softmax_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
                            w_out + (size_t)t * topk, id_out + (size_t)t * topk,
-                           nullptr);
+                           nullptr, bias);
   if (gate && lane == 0) route_gate_finish(gate, T, t, ks);
   if (chunk_hist && lane < topk) {  // lane reads back its own id
     const int a = t * topk + lane;
@@ -924,7 +937,8 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
     int* __restrict__ offsets, int* __restrict__ sorted_idx,
     int* __restrict__ inv_pos, int* __restrict__ tile_info,
     int* __restrict__ num_tiles, int max_tiles, int ks,
-    float* __restrict__ gate, int* __restrict__ zero, int nzero) {
+    float* __restrict__ gate, int* __restrict__ zero, int nzero,
+    const float* __restrict__ bias) {
   __shared__ int hist[PERM_FUSED_WAVES][PERM_FUSED_MAX_E];
   __shared__ int sh[1024];
   __shared__ int ids_lds[PERM_FUSED_MAX_N];
@@ -933,7 +947,8 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
     // fewer slice loads in flight: 16 waves share the register file
     route_softmax_token<EPL, (EPL >= 32 ? 1 : (32 / EPL < 8 ? 32 / EPL : 8))>(
         logits + (size_t)t * E, ks, (long)T * E, E, topk, eps,
-        w_out + (size_t)t * topk, id_out + (size_t)t * topk, ids_lds + t * topk);
+        w_out + (size_t)t * topk, id_out + (size_t)t * topk, ids_lds + t * topk,
+        bias);
     if (gate && (threadIdx.x & 63) == 0) route_gate_finish(gate, T, t, ks);
   }
   __syncthreads();
@@ -1296,7 +1311,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
                                int* counts, int* offsets, int* sorted_idx,
                                int* inv_pos, int* tile_info, int* num_tiles,
                                int max_tiles, hipStream_t st, int ks,
-                               float* gate, int* zero, int nzero) {
+                               float* gate, int* zero, int nzero,
+                               const float* bias) {
   SLLM_REQUIRE(ks >= 1 && (!gate || ks > 1),
                "route_permute_small: bad logit slices %d", ks);
   SLLM_REQUIRE(nzero == 0 || (zero && nzero > 0), "route_permute_small: bad zero range");
@@ -1311,7 +1327,7 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
     route_permute_small_kernel<n><<<1, 1024, 0, st>>>(                        \
         (float*)logits, w, ids, T, E, topk, eps, nbits, bm, counts, offsets,  \
         sorted_idx, inv_pos, tile_info, num_tiles, max_tiles, ks, gate,      \
-        zero, nzero);                                                         \
+        zero, nzero, bias);                                                   \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16)
 #undef CASE
@@ -1324,7 +1340,8 @@ int launch_route_permute_small(const float* logits, float* w, int* ids, int T,
 
 int launch_route_softmax(const float* logits, float* w, int* ids, int T,
                          int E, int topk, float eps, hipStream_t st, int ks,
-                         float* gate, int* chunk_hist, const ActQuant* aq_in) {
+                         float* gate, int* chunk_hist, const ActQuant* aq_in,
+                         const float* bias) {
   SLLM_REQUIRE(logits && w && ids && ks >= 1 && (!gate || ks > 1),
                "route_softmax: null pointer or bad logit slices");
   ActQuant aq{};
@@ -1344,7 +1361,8 @@ int launch_route_softmax(const float* logits, float* w, int* ids, int T,
 #define CASE(n)                                                               \
   case n:                                                                     \
     route_softmax_kernel<n><<<grid, 64 * tpb, 0, st>>>(                       \
-        (float*)logits, w, ids, T, E, topk, eps, ks, gate, chunk_hist, aq);   \
+        (float*)logits, w, ids, T, E, topk, eps, ks, gate, chunk_hist, aq,    \
+        bias);                                                                \
     break;
     CASE(1) CASE(2) CASE(4) CASE(8) CASE(16) CASE(32)
 #undef CASE

@@ -65,6 +65,7 @@ def _qwen_args(T, H, E, I, Is, topk, mode, out_f32, wdtype, eps, x, logits,
     a.logits = ptr(logits)
     w = weights
     a.router_w = ptr(w.get("router_w"))
+    a.router_bias = ptr(w.get("router_bias"))
     for k in ("wg", "wg_s", "wu", "wu_s", "wd", "wd_s", "sg", "sg_s", "su",
               "su_s", "sd", "sd_s", "sgl", "wgu_packed", "wd_packed",
               "sgu_packed", "sd_packed"):
@@ -302,6 +303,35 @@ class _Resident:
         return self.bufs.get(k)
 
 
+# Granularity of the fused layer's shapes (sllm_moe_qwen_forward): hidden a
+# multiple of 256 (the down projection's column slabs), intermediates of
+# 128 (the gate/up slabs and the 128-wide K steps).
+H_ALIGN, I_ALIGN = 256, 128
+
+
+def _round_up(n: int, m: int) -> int:
+    return -(-int(n) // m) * m
+
+
+def _bias_buffer(bias, E):
+    if bias is None:
+        return None
+    b = np.ascontiguousarray(bias, np.float32).reshape(-1)
+    if b.size != E:
+        raise ValueError(f"router_bias must hold E={E} values, got {b.size}")
+    return _up(b)
+
+
+def _pad_to(a, shape, fill=0):
+    """a zero-padded (or `fill`-padded) at the end of each axis to `shape`."""
+    a = np.asarray(a)
+    if tuple(a.shape) == tuple(shape):
+        return a
+    out = np.full(shape, fill, a.dtype)
+    out[tuple(slice(0, n) for n in a.shape)] = a
+    return out
+
+
 class QwenMoE:
     """Qwen-style layer with device-resident weights.
 
@@ -309,32 +339,59 @@ class QwenMoE:
     orientation (out, in): wg/wu (E, I, H), wd (E, H, I), scales
     (E, ceil(out/128), ceil(in/128)); shared sg/su (Is, H), sd (H, Is).
     bf16 weights (wdtype=1): float arrays (rounded to bf16), no scales.
-    router_w (E, H) and sgl (1, H) are rounded to bf16.
+    router_w (E, H) and sgl (1, H) are rounded to bf16. router_bias (E,)
+    fp32, optional: a per-expert bias added to the router logits before the
+    softmax top-k (the skewed-load configuration's routing bias).
+
+    Shapes whose hidden size is not a multiple of 256, or whose
+    intermediate sizes are not multiples of 128 (the reference's tiny dev
+    model: hidden 16, intermediate 8), are zero-padded up to them once, at
+    upload: padded columns of x and of the weights add exact zeros to every
+    dot product (the router's logits, the shared gate), padded intermediate
+    columns give gate = up = 0 and so h = silu(0) * 0 = 0, and padded output
+    columns are dropped. FP8 codes pad with code 0 (+0.0) and their block
+    scales with 1.0, which multiplies only those zero codes; the per-1x128
+    activation quantization of prefill sees the same maximum in every block
+    that holds real values. Outputs equal those of the unpadded arithmetic.
     """
 
     def __init__(self, router_w, wg, wu, wd, wg_s=None, wu_s=None, wd_s=None,
                  sg=None, su=None, sd=None, sg_s=None, su_s=None, sd_s=None,
-                 sgl=None, top_k=8, eps=1e-20, packed=True):
+                 sgl=None, top_k=8, eps=1e-20, packed=True, router_bias=None):
         wdtype = 0 if wg_s is not None else 1
         E, I, H = np.asarray(wg).shape
         Is = 0 if su is None else np.asarray(su).shape[0]
+        Hp, Ip = _round_up(H, H_ALIGN), _round_up(I, I_ALIGN)
+        Isp = _round_up(Is, I_ALIGN)
         self.wdtype = wdtype
-        cast = (lambda a: np.ascontiguousarray(a, np.uint8)) if self.wdtype == 0 \
-            else (lambda a: to_bf16(a))
-        b = {"router_w": _up(to_bf16(router_w)),
-             "wg": _up(cast(wg)), "wu": _up(cast(wu)), "wd": _up(cast(wd))}
         if self.wdtype == 0:
-            b.update(wg_s=_up(np.asarray(wg_s, np.float32)),
-                     wu_s=_up(np.asarray(wu_s, np.float32)),
-                     wd_s=_up(np.asarray(wd_s, np.float32)))
+            def cast(a, shape):
+                return _pad_to(np.ascontiguousarray(a, np.uint8), shape)
+        else:
+            def cast(a, shape):
+                return _pad_to(to_bf16(a), shape)
+
+        def scales(a, n, k):
+            return _pad_to(np.asarray(a, np.float32),
+                           (*np.shape(a)[:-2], -(-n // 128), -(-k // 128)), 1.0)
+        b = {"router_w": _up(_pad_to(to_bf16(router_w), (E, Hp))),
+             "router_bias": _bias_buffer(router_bias, E),
+             "wg": _up(cast(wg, (E, Ip, Hp))), "wu": _up(cast(wu, (E, Ip, Hp))),
+             "wd": _up(cast(wd, (E, Hp, Ip)))}
+        if self.wdtype == 0:
+            b.update(wg_s=_up(scales(wg_s, Ip, Hp)),
+                     wu_s=_up(scales(wu_s, Ip, Hp)),
+                     wd_s=_up(scales(wd_s, Hp, Ip)))
         if su is not None:
-            b.update(sg=_up(cast(sg)), su=_up(cast(su)), sd=_up(cast(sd)),
-                     sgl=_up(to_bf16(np.asarray(sgl).reshape(-1))))
+            b.update(sg=_up(cast(sg, (Isp, Hp))), su=_up(cast(su, (Isp, Hp))),
+                     sd=_up(cast(sd, (Hp, Isp))),
+                     sgl=_up(_pad_to(to_bf16(np.asarray(sgl).reshape(-1)), (Hp,))))
             if self.wdtype == 0:
-                b.update(sg_s=_up(np.asarray(sg_s, np.float32)),
-                         su_s=_up(np.asarray(su_s, np.float32)),
-                         sd_s=_up(np.asarray(sd_s, np.float32)))
-        self._finish(b, E, I, H, Is, top_k, eps, wdtype, packed)
+                b.update(sg_s=_up(scales(sg_s, Isp, Hp)),
+                         su_s=_up(scales(su_s, Isp, Hp)),
+                         sd_s=_up(scales(sd_s, Hp, Isp)))
+        self._finish(b, E, Ip, Hp, Isp, top_k, eps, wdtype, packed)
+        self.H_in = int(H)
 
     @classmethod
     def from_device(cls, bufs, *, E, I, H, Is, top_k=8, eps=1e-20, packed=True):
@@ -351,6 +408,7 @@ class QwenMoE:
     def _finish(self, b, E, I, H, Is, top_k, eps, wdtype, packed):
         self.wdtype = wdtype
         self.E, self.I, self.H, self.Is = int(E), int(I), int(H), int(Is)
+        self.H_in = self.H  # the caller's hidden size (H when not padded)
         self.top_k = int(top_k)
         self.eps = float(eps)
         if packed and wdtype == 0 and "wgu_packed" not in b:
@@ -372,8 +430,10 @@ class QwenMoE:
     def forward(self, x, logits=None, mode="auto", return_routing=False):
         """x (T, H) float (rounded to bf16) -> out (T, H) float32."""
         x = np.asarray(x, np.float32)
+        if x.ndim != 2 or x.shape[1] != self.H_in:
+            raise ValueError(f"x must be (T, {self.H_in}), got {x.shape}")
         T = x.shape[0]
-        xb = _up(to_bf16(x))
+        xb = _up(_pad_to(to_bf16(x), (T, self.H)))
         lg = _up(np.asarray(logits, np.float32)) if logits is not None else None
         out = DeviceBuffer(T * self.H * 4)
         dbg = {}
@@ -387,15 +447,15 @@ class QwenMoE:
                          Is=self.Is, topk=self.top_k, mode=mode, out_f32=True,
                          wdtype=self.wdtype, eps=self.eps, logits=lg,
                          workspace=ws, debug=dbg)
-        y = out.copy_host().reshape(T, self.H)
+        y = out.copy_host().reshape(T, self.H)[:, :self.H_in]
         stream_status()
         if not return_routing:
-            return y
+            return np.ascontiguousarray(y)
         r = {"logits": dbg["logits_out"].copy_host().reshape(T, self.E),
              "w": dbg["w_out"].copy_host().reshape(T, self.top_k),
              "ids": dbg["ids_out"].copy_host_raw(np.int32, (T, self.top_k)),
              "counts": dbg["counts_out"].copy_host_raw(np.int32, (self.E,))}
-        return y, r
+        return np.ascontiguousarray(y), r
 
 
 def check_tid2eid(table, E: int, top_k: int) -> np.ndarray:
@@ -522,15 +582,64 @@ class DeepseekMoE:
         return y, r
 
 
+# Device layers of moe_block_forward, most recently used last. An entry is
+# reused when the call passes the same router weight object (the caller's
+# checkpoint tensor: ref/qwen4_exp_pipeline.py:262-275 stacks the experts
+# anew on every call but passes the router tensor as stored) and weights
+# whose shapes, dtypes and strided samples match; it is dropped when that
+# router object is freed, or as the least recently used past BLOCK_CACHE_MAX.
+BLOCK_CACHE_MAX = 64
+_block_cache: "dict[tuple, tuple]" = {}
+
+
+def _sample_key(a):
+    if a is None:
+        return None
+    a = np.asarray(a)
+    flat = a.reshape(-1)
+    step = max(1, flat.size // 4096)
+    return (a.shape, a.dtype.str,
+            hash(np.ascontiguousarray(flat[::step][:4096]).tobytes()))
+
+
+def clear_block_cache() -> None:
+    """Frees every device layer moe_block_forward holds (call after editing
+    a weight array in place: such edits are not detected)."""
+    _block_cache.clear()
+
+
 def moe_block_forward(x, router_w, expert_gate, expert_up, expert_down,
                       shared_gate_w, shared_gate_linear_w, shared_up_w,
                       shared_down_w, top_k, eps=1e-20):
     """Device twin of ref/qwen4_exp.py:153-184 moe_block_forward with the
     same signature: weights are float arrays used at bf16 precision (the
-    bf16 GEMV path, fp32 activations). Returns (n, H) float32."""
-    layer = QwenMoE(router_w, expert_gate, expert_up, expert_down,
-                    sg=shared_gate_w if shared_up_w is not None else None,
-                    su=shared_up_w, sd=shared_down_w,
-                    sgl=shared_gate_linear_w if shared_up_w is not None else None,
-                    top_k=top_k, eps=eps)
-    return layer.forward(x)
+    bf16 GEMV path, fp32 activations). Returns (n, H) float32.
+
+    The device layer (weights uploaded once) is kept between calls with the
+    same weights (see BLOCK_CACHE_MAX); any hidden and intermediate sizes
+    are accepted (QwenMoE pads them exactly)."""
+    has_sh = shared_up_w is not None
+    key = (id(router_w), int(top_k), float(eps), _sample_key(router_w),
+           _sample_key(expert_gate), _sample_key(expert_up),
+           _sample_key(expert_down),
+           *((_sample_key(shared_gate_w), _sample_key(shared_gate_linear_w),
+              _sample_key(shared_up_w), _sample_key(shared_down_w))
+             if has_sh else ()))
+    hit = _block_cache.pop(key, None)
+    if hit is not None and hit[0]() is not router_w:
+        hit = None  # the router object died and its id was reused
+    if hit is None:
+        layer = QwenMoE(router_w, expert_gate, expert_up, expert_down,
+                        sg=shared_gate_w if has_sh else None,
+                        su=shared_up_w, sd=shared_down_w,
+                        sgl=shared_gate_linear_w if has_sh else None,
+                        top_k=top_k, eps=eps)
+        try:
+            ref = weakref.ref(router_w, lambda _r, k=key: _block_cache.pop(k, None))
+        except TypeError:  # not weak-referenceable: used for this call only
+            return layer.forward(x)
+        hit = (ref, layer)
+    _block_cache[key] = hit
+    while len(_block_cache) > BLOCK_CACHE_MAX:
+        _block_cache.pop(next(iter(_block_cache)))
+    return hit[1].forward(x)

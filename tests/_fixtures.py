@@ -204,6 +204,22 @@ def qwen_checkpoint(path, W, prefix, scale_tag="BF16"):
     write_safetensors(path, qwen_checkpoint_tensors(W, prefix, scale_tag))
 
 
+def check_router_logits(name, xh, rw, got):
+    """Device router logits against fp64 x . W_r^T of the same bf16 values
+    (ref/qwen4_exp.py:173, kernels/cuda/qwen4.cu:98-113,
+    ref/deepseek_v4.py:57-60): within 4 2^-24 sum_h |x_h| |w_h| per logit,
+    the bound of an fp32 accumulation of the exact bf16 products in any
+    order of chunks of at most 2^21 terms."""
+    x64, w64 = np.asarray(xh, np.float64), np.asarray(rw, np.float64)
+    want = x64 @ w64.T
+    mag = np.abs(x64) @ np.abs(w64).T
+    err = np.abs(np.asarray(got, np.float64) - want)
+    ratio = float((err / (mag + 1e-300)).max())
+    print(f"{name}: router logits vs fp64, max |err| / sum|x||w| = "
+          f"{ratio:.3e} (bound 4 * 2^-24 = {4 * 2.0 ** -24:.3e})", flush=True)
+    assert np.all(err <= 4 * 2.0 ** -24 * mag + 1e-30)
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

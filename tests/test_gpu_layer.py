@@ -2,8 +2,10 @@
 
 Routing (ids, per-expert counts) must be bit-exact at the logits boundary:
 the oracle routes the fp32 logits the device produced (the boundary the
-reference's sllm_q4_moe_router exposes); the router GEMM itself is checked
-separately against fp64 in test_gpu_kernels.py. Layer outputs must be
+reference's sllm_q4_moe_router exposes); the router GEMMs themselves are
+bounded against fp64 x . W_r^T (the fused prefill router here, the others in
+test_gpu_kernels.py, and at full size in test_gpu_fullsize.py). Layer
+outputs must be
 within the bf16-noise tolerance: relative L2 <= 1e-2 (asserted tighter where
 the arithmetic allows) and a max-abs bound, both printed.
 """
@@ -13,7 +15,7 @@ import pytest
 from oracle import deepseek_moe as dm
 from oracle import qwen_moe as qm
 
-from tests._fixtures import (check_qwen_routing, deepseek_layer,
+from tests._fixtures import (check_qwen_routing, check_router_logits, deepseek_layer,
                              deepseek_mxfp4, deepseek_mxfp4_gpu, qwen_checkpoint,
                              qwen_fp8, qwen_fp8_gpu, qwen_layer, rel_l2)
 
@@ -87,10 +89,12 @@ def test_qwen_fused_router_matches_full_row_routing(T, E, k):
     Cases: a partial last tile (E 200, 96), 80 candidate keys (E 1024),
     top-16 from one tile, top-1, ragged 64-token tiles, 160 candidates
     (E 2048: the merge's wave-per-token form), every expert picked (E 16,
-    top-16), a last tile of one expert (E 129)."""
+    top-16), a last tile of one expert (E 129). The fused router's logits
+    (its copy for the caller) are bounded against fp64 x . W_r^T."""
     x, W = qwen_fp8_gpu(seed=T + E, T=T, H=512, E=E, I=128, Is=128)
     layer = qwen_layer(W, k)
     y_f, r_f = layer.forward(x, mode="prefill", return_routing=True)
+    check_router_logits(f"fused router T={T} E={E}", x, W.router_w, r_f["logits"])
     assert _check_routing(r_f, E, k) == 0
     y_g, r_g = layer.forward(x, logits=r_f["logits"], mode="prefill",
                              return_routing=True)
@@ -161,6 +165,94 @@ def test_c1_bf16_literal_oracle():
     want = qm.moe_block_forward(x, rw, eg, eu, ed, None, None, None, None, k)
     rel, mabs, scale = _report("C1 bf16", got, want)
     assert rel < 1e-4
+
+
+@pytest.mark.parametrize("T,E,k,S,inter", [(5, 4, 2, 8, 8), (64, 4, 2, 8, 8),
+                                           (3, 6, 3, 20, 12)])
+def test_dev_model_shapes_through_drop_in(T, E, k, S, inter):
+    """The reference's tiny dev model (serving/dev_model.py:244-257: hidden
+    16, 4 experts, top-2, moe_inter = shared_inter = 8) through the drop-in
+    moe_block_forward (ref/qwen4_exp_pipeline.py:278-284 calls it with these
+    shapes), against the reference's literal per-token loop; hidden 20 /
+    intermediate 12 as a ragged case. The layer pads the shapes to the
+    kernels' granularity with zeros, which adds nothing. A second call with
+    the same weights reuses the device layer (no upload) and gives the same
+    bits; another router weight object gets a layer of its own."""
+    from oracle.codecs import round_bf16 as bf
+    from sllm_amd import moe
+    rng = np.random.default_rng(T + S)
+    H, I, Is = (16 if S == 8 else 20), inter, inter
+    x = bf(rng.standard_normal((T, H)).astype(np.float32))
+    rw = bf((rng.standard_normal((E, H)) * 0.5).astype(np.float32))
+    eg = bf((rng.standard_normal((E, I, H)) * 0.3).astype(np.float32))
+    eu = bf((rng.standard_normal((E, I, H)) * 0.3).astype(np.float32))
+    ed = bf((rng.standard_normal((E, H, I)) * 0.3).astype(np.float32))
+    sg = bf((rng.standard_normal((Is, H)) * 0.3).astype(np.float32))
+    su = bf((rng.standard_normal((Is, H)) * 0.3).astype(np.float32))
+    sd = bf((rng.standard_normal((H, Is)) * 0.3).astype(np.float32))
+    sgl = bf((rng.standard_normal((1, H)) * 0.3).astype(np.float32))
+    moe.clear_block_cache()
+    got = moe.moe_block_forward(x, rw, eg, eu, ed, sg, sgl, su, sd, k)
+    assert got.shape == (T, H) and got.dtype == np.float32
+    want = qm.moe_block_forward(x, rw, eg, eu, ed, sg, sgl, su, sd, k)
+    rel, mabs, scale = _report(f"dev-model shapes T={T} H={H} I={I}", got, want)
+    assert rel < 1e-4
+    assert len(moe._block_cache) == 1
+    layer = next(iter(moe._block_cache.values()))[1]
+    # the pipeline's _moe_w stacks the experts anew on each call
+    again = moe.moe_block_forward(x, rw, eg.copy(), eu.copy(), ed.copy(), sg, sgl,
+                                  su, sd, k)
+    np.testing.assert_array_equal(again, got)
+    assert len(moe._block_cache) == 1
+    assert next(iter(moe._block_cache.values()))[1] is layer
+    rw2 = rw.copy()
+    moe.moe_block_forward(x, rw2, eg, eu, ed, sg, sgl, su, sd, k)
+    assert len(moe._block_cache) == 2
+    moe.clear_block_cache()
+
+
+@pytest.mark.parametrize("T,mode", [(300, "prefill"), (300, "prefill-logits"),
+                                    (40, "decode"), (8, "decode")])
+def test_qwen_router_bias_every_routing_path(T, mode):
+    """The per-expert routing bias (router_bias; the skewed-load
+    configuration's) on each routing path: the fused prefill router (bias
+    before the tiles' top-k and softmax partials), the full-row softmax
+    routing with the logits given, the multi-workgroup decode routing (40
+    tokens, split router slices) and the one-workgroup route + permute
+    (8 tokens). Ids bit-exact against the oracle's moe_route of logits +
+    bias (one fp32 addition), weights rtol 1e-5, the layer output against
+    the oracle layer on those routes; logits_out holds the logits without
+    the bias (bounded against fp64 x . W_r^T)."""
+    from sllm_amd.moe import QwenMoE
+    E, k, H, I = 64, 6, 512, 256
+    x, W = qwen_fp8(seed=31 + T, T=T, H=H, E=E, I=I, Is=256)
+    rng = np.random.default_rng(31)
+    ranks = rng.permutation(E) + 1
+    bias = (-2.0 * np.log(ranks)).astype(np.float32)
+    bias[ranks > 50] = -40.0
+    layer = QwenMoE(W.router_w, W.wg_q, W.wu_q, W.wd_q, W.wg_s, W.wu_s, W.wd_s,
+                    sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
+                    sd_s=W.sd_s, sgl=W.sgl, top_k=k, router_bias=bias)
+    given = mode == "prefill-logits"
+    lg_in = (x @ W.router_w.T).astype(np.float32) if given else None
+    m = "prefill" if mode.startswith("prefill") else "decode"
+    y, r = layer.forward(x, logits=lg_in, mode=m, return_routing=True)
+    if given:
+        np.testing.assert_array_equal(r["logits"], lg_in)
+    else:
+        check_router_logits(f"biased router {mode}", x, W.router_w, r["logits"])
+    lg = (r["logits"] + bias[None, :]).astype(np.float32)
+    assert check_qwen_routing(lg, r["ids"], r["w"], k, name=f"bias {mode}").size == 0
+    np.testing.assert_array_equal(r["counts"], np.bincount(r["ids"].ravel(), minlength=E))
+    assert r["counts"][ranks > 50].sum() == 0
+    if m == "prefill":
+        want = qm.moe_layer_fp8(x, lg, W, k)
+        rel, mabs, scale = _report(f"bias {mode}", y, want)
+        assert rel < 3e-3 and mabs < 0.05 * scale
+    else:
+        want = qm.moe_layer_fp8_dequant(x, lg, W, k)
+        rel, mabs, scale = _report(f"bias {mode}", y, want)
+        assert rel < 1e-4
 
 
 def test_qwen_skewed_with_empty_experts():

@@ -97,7 +97,8 @@ def test_fp4_table_and_nibble_order():
         for j in range(K // 2):
             b = int(packed[i, j])
             for nib in (b & 0x0F, (b >> 4) & 0x0F):
-                want[i, k] = codecs.FP4_TABLE[nib] * 2.0 ** (int(s[i, k // 32]) - 127)
+                with np.errstate(over="ignore"):  # 6 * 2^127 is inf in float32
+                    want[i, k] = codecs.FP4_TABLE[nib] * 2.0 ** (int(s[i, k // 32]) - 127)
                 k += 1
     np.testing.assert_array_equal(got, want)
 

@@ -1,19 +1,33 @@
 """CPU checks of the streamed GEMMs' work-item sizing (no GPU needed).
 
-The persistent launches hold at most 32 work items per workgroup; the host
-sizes the grid from a bound of the ragged tile count. These tests take
-C5-sized routings (T=16384, top-10, E=512, 128-row tiles) including the
-adversarial ones, count tiles by brute force, and deal the items over the
-grid the library picks exactly as the kernels do (XCD x = workgroup % 8
-owns items [total x / 8, total (x + 1) / 8), dealt round-robin over its
-workgroups), asserting no workgroup gets more than 32.
+The decode kernel (moe_stream_dec_kernel) holds at most 32 work items per
+workgroup; the prefill kernel (moe_stream_kernel) takes its items 32 at a
+time and so has no limit, but must still take every item exactly once. The
+host sizes each persistent grid from a bound of the ragged tile count. These
+tests port the kernels' dealing exactly:
+
+* prefill, weights through L2 (ranges): XCD x = workgroup % 8 owns items
+  [total x / 8, total (x + 1) / 8), dealt round-robin over its workgroups;
+* prefill, streamed weights, and every decode launch: items go to the XCDs
+  in chunks of CB consecutive items (chunk c to XCD c % 8, the partial last
+  chunk to XCD (total / CB) % 8), then round-robin over each XCD's
+  workgroups; CB is one row tile's items of the first segment (column slabs,
+  times K chunks in decode).
+
+They take the library's own plans (sllm_moe_plan_query: tile rows, K
+splits, item bounds, deal chunks and grids) for decode batches of the
+bench's shapes and of others, and assert that every tile count up to the
+plan's bound deals no workgroup more than 32 items.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
 from sllm_amd import _lib
 
 ST_MAX_ITEMS = 32
+PLAN_FIELDS = 22
 
 
 def _need_lib():
@@ -22,15 +36,48 @@ def _need_lib():
     return _lib.lib()
 
 
-def _max_items_per_workgroup(total: int, grid: int) -> int:
+def _xcd_count(total, xcd, cb, ranges):
+    """Items XCD `xcd` owns (the kernels' xcount)."""
+    if ranges:
+        return total * (xcd + 1) // 8 - total * xcd // 8
+    ncf, crem = divmod(total, cb)
+    full = (ncf - xcd + 7) // 8 if ncf > xcd else 0
+    return full * cb + (crem if ncf % 8 == xcd else 0)
+
+
+def _item_at(total, xcd, q, cb, ranges):
+    """Flat item index of the XCD's q-th item (the kernels' item_at)."""
+    if ranges:
+        return total * xcd // 8 + q
+    return (xcd + 8 * (q // cb)) * cb + q % cb
+
+
+def _deal(total, grid, cb, ranges):
+    """Items of every workgroup, as lists of flat item indices."""
     nx = grid // 8
-    worst = 0
-    for x in range(8):
-        beg, end = total * x // 8, total * (x + 1) // 8
-        n = end - beg
-        # workgroup j of this XCD takes items beg + j, beg + j + nx, ...
-        worst = max(worst, -(-n // nx) if n else 0)
-    return worst
+    out = []
+    for b in range(grid):
+        xcd, jx = b % 8, b // 8
+        xc = _xcd_count(total, xcd, cb, ranges)
+        n = (xc - jx + nx - 1) // nx if xc > jx else 0
+        out.append([_item_at(total, xcd, jx + m * nx, cb, ranges) for m in range(n)])
+    return out
+
+
+def _max_items(total, grid, cb, ranges=False):
+    """Most items one workgroup receives (workgroup jx = 0 of each XCD)."""
+    nx = grid // 8
+    return max(-(-_xcd_count(total, x, cb, ranges) // nx) for x in range(8))
+
+
+@pytest.mark.parametrize("ranges", [False, True])
+@pytest.mark.parametrize("cb", [1, 4, 8, 12, 96])
+def test_deal_takes_every_item_once(ranges, cb):
+    """The ported deal is a partition of [0, total) for every total."""
+    for grid in (8, 64, 256):
+        for total in list(range(0, 200)) + [1023, 4097]:
+            items = sorted(i for w in _deal(total, grid, cb, ranges) for i in w)
+            assert items == list(range(total)), (grid, total, cb, ranges)
 
 
 def _counts_cases(N, E, k, rng):
@@ -71,21 +118,108 @@ def test_tile_bound_covers_worst_routings(bm):
 
 
 @pytest.mark.parametrize("ncu", [256, 304, 80, 8])
-def test_stream_grid_deals_at_most_32_items(ncu):
+def test_stream_dec_grid_deals_at_most_32_items(ncu):
+    """The chunk-dealt grid bound holds for every total up to the bound,
+    for chunk sizes of one tile's slabs (x K chunks)."""
+    lib = _need_lib()
+    for upper in (1, 31, 257, 4000, 9408, 20000):
+        for cb in (1, 2, 4, 8, 12, 14, 28, 96, 160):
+            grid = lib.sllm_moe_stream_dec_grid(upper, ncu, cb)
+            assert grid % 8 == 0 and grid >= ncu
+            worst = max(_max_items(t, grid, cb) for t in
+                        range(max(0, upper - 3 * cb * 8), upper + 1))
+            assert worst <= ST_MAX_ITEMS, (upper, cb, grid, worst)
+
+
+def _plan(lib, ds, T, H, E, I, Is, k, mode=2, logits_given=0):
+    out = (ctypes.c_long * PLAN_FIELDS)()
+    rc = lib.sllm_moe_plan_query(ds, T, H, E, I, Is, k, mode, logits_given,
+                                 ctypes.addressof(out), PLAN_FIELDS)
+    assert rc == 0, _lib.last_error()
+    return list(out)
+
+
+# (deepseek, H, E, k, I, Is): the bench's C3 shape, the DeepSeek C4 shape,
+# and shapes whose decode plans split the down projection finely
+SHAPES = [
+    (0, 2048, 512, 10, 512, 512),      # C2 / C3
+    (0, 4096, 128, 8, 1536, 1536),     # a Qwen3-style layer
+    (0, 3584, 64, 8, 2560, 20480),     # a wide shared expert
+    (0, 2048, 64, 6, 1408, 5632),
+    (0, 5120, 1, 1, 17408, 0),         # a dense MLP run as the layer
+    (1, 7168, 256, 8, 2048, 2048),     # C4
+    (1, 4096, 64, 6, 1536, 1536),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_decode_plans_deal_at_most_32_items(shape):
+    """Every decode launch of the library's plans, at every batch size and
+    every routed tile count up to the plan's bound, deals no workgroup more
+    than 32 items."""
+    lib = _need_lib()
+    ds, H, E, k, I, Is = shape
+    for T in range(1, 65):
+        p = _plan(lib, ds, T, H, E, I, Is, k)
+        assert p[0] == 1
+        bm, bm_sh, max_tiles = p[1], p[2], p[3]
+        ks_up, ks_up_sh, ks_dn, ks_dn_sh = p[5], p[6], p[7], p[8]
+        sh_rt = -(-T // bm_sh) if Is else 0
+        # per launch: (routed tiles -> items, shared items)
+        launches = [
+            (I // 128 * ks_up, (0 if ds else sh_rt * (Is // 128) * ks_up_sh)),
+            (H // 256 * ks_dn, (0 if ds else sh_rt * (H // 256) * ks_dn_sh)),
+        ]
+        for j, (per_tile, shared) in enumerate(launches):
+            upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
+            assert upper == max_tiles * per_tile + shared, (T, j)
+            assert cb == per_tile and grid % 8 == 0, (T, j)
+            worst = max(_max_items(rt * per_tile + shared, grid, cb)
+                        for rt in range(1, max_tiles + 1))
+            assert worst <= ST_MAX_ITEMS, (T, j, upper, cb, grid, worst)
+        if ds and Is:
+            for j, per_tile in ((2, Is // 128 * ks_up_sh), (3, H // 256 * ks_dn_sh)):
+                upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
+                assert upper == sh_rt * per_tile and cb == per_tile
+                assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS, (T, j)
+
+
+def test_old_contiguous_sizing_would_overflow():
+    """Regression: sizing the decode grid as if each XCD held a contiguous
+    eighth of the items (sllm_moe_stream_grid) deals 37 items to a
+    workgroup of the H 4096, E 128, top-8, I 1536 layer at 6 tokens, and
+    36 to the H 3584, E 64, I 2560, Is 20480 layer at 7 tokens; the
+    chunk-aware grid the library now launches keeps them at 32."""
+    lib = _need_lib()
+    for (ds, H, E, k, I, Is), T, old_worst in (
+            ((0, 4096, 128, 8, 1536, 1536), 6, 37),
+            ((0, 3584, 64, 8, 2560, 20480), 7, 36)):
+        p = _plan(lib, ds, T, H, E, I, Is, k)
+        bad = None
+        for j in (0, 1):
+            upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
+            old = lib.sllm_moe_stream_grid(upper, p[9])
+            w_old = _max_items(upper, old, cb)
+            if w_old > ST_MAX_ITEMS:
+                bad = w_old
+            assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS
+        assert bad == old_worst, (H, T, bad)
+
+
+@pytest.mark.parametrize("ncu", [256, 304, 80, 8])
+def test_prefill_grid_deals_every_item(ncu):
+    """Prefill launches run one workgroup per CU (items taken 32 at a time):
+    the ported deal covers every item once at C5-sized item counts."""
     lib = _need_lib()
     rng = np.random.default_rng(1)
     T, k, E, H, I = 16384, 10, 512, 2048, 512
     N = T * k
-    bound = lib.sllm_moe_tile_bound(N, E, 128)
     sh_tiles = -(-T // 128)
+    grid = 8 * (-(-ncu // 8))
     for slabs in (I // 128, H // 256):  # gate/up, then down
-        upper = bound * slabs + sh_tiles * slabs
-        grid = lib.sllm_moe_stream_grid(upper, ncu)
-        assert grid % 8 == 0 and grid >= ncu
         for name, counts in _counts_cases(N, E, k, rng):
             total = (int(np.sum(-(-counts // 128))) + sh_tiles) * slabs
-            assert _max_items_per_workgroup(total, grid) <= ST_MAX_ITEMS, (name, total)
-        # the bound itself, and a decode-style split of it
-        assert _max_items_per_workgroup(upper, grid) <= ST_MAX_ITEMS
-        g3 = lib.sllm_moe_stream_grid(upper * 3, ncu)
-        assert _max_items_per_workgroup(upper * 3, g3) <= ST_MAX_ITEMS
+            for ranges in (False, True):
+                dealt = _deal(total, grid, slabs, ranges)
+                assert sum(len(w) for w in dealt) == total, name
+                assert len({i for w in dealt for i in w}) == total, name
