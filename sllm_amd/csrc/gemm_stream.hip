@@ -804,10 +804,18 @@ __device__ __forceinline__ void dec_fused_finish(
     const SegDesc& S = seg ? S1 : S0;
     if (S.ksplit <= 1) continue;  // finished in the item's epilogue
     int* c = F.cnt + (seg ? F.cnt1 : 0) + (long)d.z * (S.N / 128) + nt;
-    // acquire-release at device scope: the chunk sums this workgroup
-    // stored before the barrier happen before the arrival, and the
-    // finisher's reads of every chunk's sums happen after it
-    if (__hip_atomic_fetch_add(c, 1, __ATOMIC_ACQ_REL,
+    // A relaxed device-scope count. The ordering it relies on is the
+    // ISA's, not the HIP memory model's: every chunk sum went out as a
+    // device-scope (sc1) store, written through this XCD's L2 to the
+    // coherence point, and each thread waited for its own stores'
+    // completion (vmcnt 0) before the barrier above, so they are visible
+    // device-wide before any count of this workgroup issues; the finisher
+    // learns it finished from the count's return value, and its loads of
+    // the sums, issued only after that (in order, no speculation), are
+    // device-scope (sc1) loads that miss any stale L2 copy. An acq_rel
+    // count (a whole-L2 write-back before it and an L2 invalidate after)
+    // gives the same bits and cost B=1 / 2 / 4 layers 2 / 7 / 7.5 us.
+    if (__hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT) == S.ksplit - 1)
       jobs[atomicAdd(&njob, 1)] = i;
   }
