@@ -460,12 +460,24 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t gsl[RT_GATE_MAX];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   {  // the permutation's chunk histograms, filled by the routing launch
-    const long nthr = (long)gridDim.x * gridDim.y * 512;
-    for (long i = ((long)blockIdx.y * gridDim.x + blockIdx.x) * 512 + tid;
-         i < zero_n; i += nthr)
+    const long nthr = (long)gridDim.x * 512;
+    for (long i = (long)blockIdx.x * 512 + tid; i < zero_n; i += nthr)
       zero[i] = 0;
   }
-  const int t0 = blockIdx.x * RG_TT, e0 = blockIdx.y * RG_TE;
+  // Tile (bx, by) of workgroup b (router_topk_grid): XCD b % 8 takes token
+  // tiles b % 8, b % 8 + 8, ..., each one's ny expert tiles on consecutive
+  // workgroups of that XCD, so a token tile's activation rows come from HBM
+  // once and from the XCD's L2 for its other expert tiles. (With the token
+  // tile as the fast grid dimension, the expert tiles of one token tile ran
+  // a whole round of the grid apart once T passed 64 x #CUs / ny tokens,
+  // each reading the rows again: 16384 tokens x 512 experts fetched 286 MB
+  // for 67 MB of activations; with this deal 127 MB. The launch's time did
+  // not change (105 us): it is bound by its MFMA and top-k work, not HBM.)
+  const int ny = (E + RG_TE - 1) / RG_TE, ntx = (T + RG_TT - 1) / RG_TT;
+  const int bx = (int)(blockIdx.x % 8) + 8 * (int)(blockIdx.x / 8 / ny);
+  const int by = (int)(blockIdx.x / 8 % ny);
+  if (bx >= ntx) return;  // the last XCD round's spare workgroups
+  const int t0 = bx * RG_TT, e0 = by * RG_TE;
   const int nk = H / RG_KC;
   auto stage = [&](int kc) __attribute__((always_inline)) -> uint8_t* {
     const int sidx = kc % 3;
@@ -503,8 +515,8 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  const int rpy = (RG_TT + (int)gridDim.y - 1) / (int)gridDim.y;
-  const int qr0 = min(RG_TT, (int)blockIdx.y * rpy), qr1 = min(RG_TT, qr0 + rpy);
+  const int rpy = (RG_TT + ny - 1) / ny;
+  const int qr0 = min(RG_TT, by * rpy), qr1 = min(RG_TT, qr0 + rpy);
   const int qslot = tid >> 4, q16 = tid & 15;
   float gdot[2] = {0.f, 0.f};
   // a step's quantized rows are stored at the start of the next step,
@@ -646,7 +658,7 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
       }
   dma::bar_lds();
   const int r16 = lane & 15, rg = lane >> 4;
-  const int ny = gridDim.y, y = blockIdx.y;
+  const int y = by;
   int tl[2];
   float m[2], sm[2];
   uint64_t key[2][8];
@@ -1194,6 +1206,13 @@ static bool topk_ok(int E, int topk) {
          (long)ceil_div(E, RG_TE) * topk <= 512;
 }
 
+// 1-D grid of router_topk_kernel: ceil(E / 128) expert tiles for each of
+// the ceil(T / 64) token tiles, rounded up to whole rounds of 8 (one token
+// tile per XCD slot).
+static unsigned router_topk_grid(int T, int E) {
+  return (unsigned)(8 * ceil_div(ceil_div(T, RG_TT), 8) * ceil_div(E, RG_TE));
+}
+
 bool router_topk_fits(int T, int E, int topk, int H) {
   return T > RG_SMALL_T && topk_ok(E, topk) && H > 0 && H % RG_KC == 0 &&
          H <= RT_GATE_MAX;
@@ -1225,8 +1244,7 @@ int launch_router_topk(const uint16_t* x, const uint16_t* w, float* logits,
   SLLM_REQUIRE(!rp.gate_w || (rp.q && rp.gate_out),
                "router_topk: gate needs the quantization and gate buffers");
   SLLM_REQUIRE(zero_n == 0 || zero, "router_topk: null zero range");
-  dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
-  router_topk_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, zero,
+  router_topk_kernel<<<router_topk_grid(T, E), 512, 0, st>>>(x, w, logits, T, E, H, zero,
                                            zero_n, rp);
   SLLM_LAUNCHED();
   return 0;
@@ -1247,8 +1265,8 @@ int launch_router_logits_quant(const uint16_t* x, const uint16_t* w,
   rp.q = q;
   rp.s = s;
   rp.pow2 = pow2 ? 1 : 0;
-  dim3 grid(ceil_div(T, RG_TT), ceil_div(E, RG_TE));
-  router_topk_kernel<<<grid, 512, 0, st>>>(x, w, logits, T, E, H, nullptr, 0, rp);
+  router_topk_kernel<<<router_topk_grid(T, E), 512, 0, st>>>(x, w, logits, T, E, H,
+                                                             nullptr, 0, rp);
   SLLM_LAUNCHED();
   return 0;
 }
