@@ -32,6 +32,8 @@
 #include <type_traits>
 
 #include "launch.h"
+#include "permute_fused.h"
+#include "route_token.h"
 
 namespace sllm {
 
@@ -855,7 +857,8 @@ __device__ __forceinline__ void dec_fused_finish(
 
 template <int BF, int MODE, bool WNT, int BM>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
-    SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F) {
+    SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F,
+    RouteInline RI) {
   constexpr int RB = BM / 16;
   static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
@@ -863,18 +866,69 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   __shared__ float rwl[ST_MAX_ITEMS][BM];
   __shared__ __attribute__((aligned(16))) uint16_t a_hi[2][BM * SD_LS];
   __shared__ __attribute__((aligned(16))) uint16_t a_lo[MODE == 1 ? 2 : 1][MODE == 1 ? BM * SD_LS : 8];
+  // the batch's routing when the launch routes it (gate/up only): per-wave
+  // expert histograms, the picked ids, the sorted assignment indices, the
+  // tile table, and the scan scratch with the tile count after it
+  constexpr bool RTE = MODE == 0;
+  static_assert(RI_MAX_ROUTE_T <= ST_WAVES, "one routed token per wave");
+  __shared__ int ri_hist[RTE ? ST_WAVES : 1][RTE ? RI_MAX_E : 1];
+  __shared__ int ri_ids[RTE ? RI_MAX_N : 1];
+  __shared__ int ri_sorted[RTE ? RI_MAX_N : 1];
+  __shared__ __attribute__((aligned(16))) int ri_tiles[RTE ? 4 * RI_MAX_TILES : 4];
+  __shared__ int ri_sh[ST_WAVES + 1];
 
   constexpr int NTW = MODE == 0 ? 128 : 256;
   constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, lc = lane & 15;
 
-  auto seg_items_dec = [&](const SegDesc& S) {
-    const int rt = S.tile_info ? *S.num_tiles : (S.total_rows + BM - 1) / BM;
+  // ---- the batch's routing and permutation (RouteInline): every
+  // workgroup computes the same tables in LDS; workgroup 0 also writes
+  // them out ---------------------------------------------------------------
+  bool inl = false;
+  if constexpr (RTE) {
+    if (RI.logits || RI.ids_in) {
+      inl = true;
+      const bool lead = blockIdx.x == 0;
+      const int k = RI.topk;
+      if (RI.logits) {
+        // wave w routes token w; other workgroups read the rows meanwhile:
+        // no write-back of the summed slices (store false)
+        if (wave < RI.T) {
+          route_softmax_token<8, 2>(RI.logits + (size_t)wave * RI.E, RI.ks,
+                                    (long)RI.T * RI.E, RI.E, k, RI.eps,
+                                    lead ? RI.w + (size_t)wave * k : nullptr,
+                                    lead ? RI.ids + (size_t)wave * k : nullptr,
+                                    ri_ids + wave * k, RI.bias, false);
+          if (lead && RI.gate && lane == 0) route_gate_finish(RI.gate, RI.T, wave, RI.ks);
+        }
+      } else {
+        for (int i = tid; i < RI.T * k; i += ST_THREADS) ri_ids[i] = RI.ids_in[i];
+      }
+      __syncthreads();
+      const PermDst out = lead ? PermDst{RI.counts, RI.offsets, RI.sorted,
+                                         RI.inv, RI.tiles, RI.ntiles}
+                               : PermDst{};
+      const PermDst mine{nullptr, nullptr, ri_sorted, nullptr, ri_tiles,
+                         &ri_sh[ST_WAVES]};
+      permute_block<ST_WAVES, RI_G, RI_MAX_E>(ri_ids, RI.T * k, RI.E, RI.nbits,
+                                               RI.bm, RI.max_tiles, out, mine,
+                                               ri_hist, ri_sh);
+      __syncthreads();
+    }
+  }
+  // the routed segment's tile table and sorted rows: this launch's own or
+  // the permutation launch's
+  const int* tiles0 = inl ? ri_tiles : S0.tile_info;
+  const int* sorted0 = inl ? ri_sorted : S0.sorted_idx;
+
+  auto seg_items_dec = [&](const SegDesc& S, bool own) {
+    const int rt = own ? ri_sh[ST_WAVES]
+                 : S.tile_info ? *S.num_tiles : (S.total_rows + BM - 1) / BM;
     return rt * (S.N / NTW) * S.ksplit;
   };
-  const int n0 = seg_items_dec(S0);
-  const int n1 = nseg > 1 ? seg_items_dec(S1) : 0;
+  const int n0 = seg_items_dec(S0, inl);
+  const int n1 = nseg > 1 ? seg_items_dec(S1, false) : 0;
   const int total = n0 + n1;
   const int nx = gridDim.x / 8;
   const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
@@ -903,8 +957,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     const int q = li / S.ksplit, kc = li % S.ksplit;
     const int rt = q / ntn, nt = q % ntn;
     int e = 0, rb, rows;
-    if (S.tile_info) {
-      const int4 d = *(const int4*)(S.tile_info + 4 * rt);
+    const int* ti = seg ? S.tile_info : tiles0;
+    if (ti) {
+      const int4 d = *(const int4*)(ti + 4 * rt);
       e = d.x;
       rb = d.y;
       rows = min(BM, d.z);
@@ -924,8 +979,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     float rw = 1.f;
     if (r < d.w) {
       const int p = d.z + r;
-      src = S.gather ? S.sorted_idx[p] / topk : p;
-      if (S.row_w) rw = S.row_w[S.row_w_by_idx ? S.sorted_idx[p] : p];
+      const int* si = (d.x & 1) ? S.sorted_idx : sorted0;
+      src = S.gather ? si[p] / topk : p;
+      if (S.row_w) rw = S.row_w[S.row_w_by_idx ? si[p] : p];
     }
     rsrc[i][r] = src;
     rwl[i][r] = rw;
@@ -1414,7 +1470,7 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 template <int BF, int MODE, int BM>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st,
-                         const DecFuse& fuse) {
+                         const DecFuse& fuse, const RouteInline& route) {
   {
     const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, BM,
                                     upper_items, "stream decode gemm");
@@ -1435,7 +1491,7 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   }
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse);
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route);
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1443,7 +1499,7 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
 int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
                       long upper_items, hipStream_t st, int bm,
-                      const DecFuse* fuse_in) {
+                      const DecFuse* fuse_in, const RouteInline* route_in) {
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
                    (bm == 16 || bm == 32),
                "stream decode gemm: bad format or tile rows %d", bm);
@@ -1484,9 +1540,30 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                    "stream decode gemm: a fused finish needs h, chunk slices "
                    "under 2 GiB, and tile rows for the routed segment");
   }
+  RouteInline route{};
+  if (route_in && (route_in->logits || route_in->ids_in)) {
+    route = *route_in;
+    SLLM_REQUIRE(!route.logits || (route.T <= RI_MAX_ROUTE_T && route.ks >= 1 &&
+                                   (!route.gate || route.ks > 1) && route.w &&
+                                   route.ids && !route.ids_in),
+                 "stream decode gemm: bad in-launch routing (T=%d ks=%d)",
+                 route.T, route.ks);
+    SLLM_REQUIRE(mode == 0 && s0.gather && s0.tile_info && s0.sorted_idx &&
+                     route.topk == topk && route.bm == bm &&
+                     route.max_tiles == s0.max_tiles &&
+                     route_inline_fits(route.T, route.E, topk, route.max_tiles) &&
+                     route.counts && route.offsets &&
+                     route.sorted == s0.sorted_idx && route.inv &&
+                     route.tiles == s0.tile_info &&
+                     route.ntiles == s0.num_tiles,
+                 "stream decode gemm: bad in-launch routing (T=%d E=%d k=%d "
+                 "tiles %d)", route.T, route.E, route.topk, route.max_tiles);
+    route.nbits = 0;
+    while ((1 << route.nbits) < route.E) ++route.nbits;
+  }
 #define GO(B, M)                                                         \
-  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse) \
-                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse)
+  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse, route) \
+                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse, route)
   if (mode == 0) {
     if (bf == SF_FP4) GO(SF_FP4, 0);
     GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales

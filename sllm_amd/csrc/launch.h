@@ -82,10 +82,13 @@ int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
 // Decode-size helpers (router.hip): router GEMM for T <= 64 with an optional
 // shared-expert gate tile, and softmax top-k fused with the permutation in
 // one workgroup (when route_permute_small_fits).
+// zero / nzero: ints cleared by the launch (the counters of a later
+// launch on the stream), or none.
 int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
                              float* logits, int T, int E, int H,
                              const uint16_t* sgl, float* gate_out,
-                             hipStream_t st, int ks = 1);
+                             hipStream_t st, int ks = 1, int* zero = nullptr,
+                             long nzero = 0);
 bool route_permute_small_fits(int T, int E, int topk);
 // zero / nzero (both permutation launches, one-workgroup path only): ints
 // to clear on the way, the counters of the fused decode launches after it.
@@ -266,10 +269,47 @@ struct DecFuse {
   int* cnt;
   long cnt1;
 };
+// A mode-0 decode launch may also build its batch's permutation itself,
+// from the ids of the routing launch (RouteInline.ids_in non-null), or
+// route the batch too (RouteInline.logits non-null, Qwen softmax top-k, at
+// most RI_MAX_ROUTE_T tokens: one per wave). Every workgroup computes the
+// expert-major permutation (and before it the tokens' softmax top-k from
+// the router's logits: ks K-chunk slices, plus bias) in LDS, before its
+// items -- the arithmetic of the routing and permutation launches, so
+// every workgroup holds the same tables, equal to theirs bit for bit.
+// Workgroup 0 also writes them (w, ids when routing; counts, offsets,
+// sorted, inv, tiles, ntiles) for the later launches, and finishes the
+// split router's shared gate (gate non-null). The routed segment's
+// tile_info / num_tiles / sorted_idx are then not read. Limits: E <=
+// RI_MAX_E, T topk <= RI_MAX_N, max_tiles <= RI_MAX_TILES
+// (route_inline_fits).
+constexpr int RI_MAX_E = 512;
+constexpr int RI_G = 4;                      // 64-assignment groups per wave
+constexpr int RI_MAX_N = 8 * RI_G * 64;      // eight waves
+constexpr int RI_MAX_TILES = 640;
+constexpr int RI_MAX_ROUTE_T = 8;            // tokens routed in the launch
+struct RouteInline {
+  float* logits;
+  const int* ids_in;
+  const float* bias;
+  float* gate;
+  float* w;
+  int* ids;
+  int* counts;
+  int* offsets;
+  int* sorted;
+  int* inv;
+  int* tiles;
+  int* ntiles;
+  int T, E, topk, ks, nbits, bm, max_tiles;
+  float eps;
+};
+bool route_inline_fits(int T, int E, int topk, long max_tiles);
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
                       hipStream_t st, int bm = 16,
-                      const DecFuse* fuse = nullptr);
+                      const DecFuse* fuse = nullptr,
+                      const RouteInline* route = nullptr);
 // Counter ints of a fused gate/up launch: N routed rows, T shared rows.
 inline long dec_fuse_counters(long N, long T, int I, int Is) {
   return N * (I / 128) + T * (Is / 128);

@@ -57,6 +57,7 @@ static int weights_reused(long rows, long experts, int bm) {
 }
 
 static int dense8_mode();
+static bool route_inline_on();
 static int device_cus();
 
 static size_t take(size_t& cur, size_t bytes) {
@@ -327,6 +328,22 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   SLLM_REQUIRE(nfcnt < (1L << 31), "sllm_moe_qwen_forward: too many counters");
   const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool small_route = p.decode && route_permute_small_fits(T, E, k);
+  // Streamed decode of a routed layer: the gate/up launch builds the
+  // permutation in every workgroup (the tables written out by workgroup 0)
+  // in place of the permutation launch (perm_inl, after the multi-workgroup
+  // routing launch), and up to 8 tokens it routes them too (route_inl, one
+  // token per wave) in place of the routing launch; the router launch then
+  // clears the fused finish's counters. Routing in the launch needs the
+  // router launch (not the caller's logits) and leaves a split router's
+  // slices unsummed (not when the caller copies the logits). Between 9 and
+  // 16 tokens the one-workgroup route + permute launch is faster than
+  // either (a wave's second token costs as much as the launch).
+  const bool inl_ok = p.decode && a->wgu_packed && !one_expert &&
+                      route_inline_fits(T, E, k, p.max_tiles) &&
+                      route_inline_on();
+  const bool route_inl = inl_ok && small_router && T <= RI_MAX_ROUTE_T &&
+                         (!a->logits_out || p.ks_r == 1);
+  const bool perm_inl = inl_ok && !route_inl && !small_route && !fused;
   // Prefill: the softmax routing launch also quantizes each token's row
   // (and forms the shared-expert gate), in place of the activation-quant
   // launch (one wave per token in both; C2: 11.8 + 11.3 -> 19.8 us).
@@ -346,7 +363,9 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
           launch_router_small_gate((const uint16_t*)a->x,
                                    (const uint16_t*)a->router_w, logits, T, E,
                                    H, sh ? (const uint16_t*)a->sgl : nullptr,
-                                   sh ? gate : nullptr, st, p.ks_r));
+                                   sh ? gate : nullptr, st, p.ks_r,
+                                   route_inl ? fcnt : nullptr,
+                                   route_inl ? nfcnt : 0));
     gate_done = sh;
   }
   // split router: the routing launch finishes the gate from its partials
@@ -390,7 +409,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                                    (const uint16_t*)a->router_w, logits, T, E,
                                    H, st, 1, chunk_hist, hist_n));
   }
-  if (one_expert) {
+  if (one_expert || route_inl) {
     STAGE(clk, SLLM_MOE_STAGE_ROUTE, 0);
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else if (small_route) {
@@ -410,9 +429,11 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                                      aq_fused ? &aq : nullptr,
                                      a->router_bias));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
-          launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
-                         tiles, ntiles, p.max_tiles, ws + p.pscr, st,
-                         route_hist, fcnt, (int)nfcnt));
+          perm_inl ? 0
+                   : launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted,
+                                    inv, tiles, ntiles, p.max_tiles,
+                                    ws + p.pscr, st, route_hist, fcnt,
+                                    (int)nfcnt));
   }
 
   if (p.decode) {
@@ -448,12 +469,23 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
       s1.pstride = (long)T * Is;
       const DecFuse f_up{fcnt, (long)p.N * (I / 128)};
+      RouteInline ri{};
+      if (route_inl || perm_inl) {
+        ri.logits = route_inl ? logits : nullptr;
+        ri.ids_in = perm_inl ? ids : nullptr;
+        ri.bias = a->router_bias; ri.gate = route_inl ? gate_fin : nullptr;
+        ri.w = w; ri.ids = ids; ri.counts = counts; ri.offsets = offsets;
+        ri.sorted = sorted; ri.inv = inv; ri.tiles = tiles; ri.ntiles = ntiles;
+        ri.T = T; ri.E = E; ri.topk = k; ri.ks = p.ks_r; ri.bm = p.bm;
+        ri.max_tiles = p.max_tiles; ri.eps = eps;
+      }
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             first_rc(
                 [&] {
                   return launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k,
                                            0.f, p.up_items, st, p.bm,
-                                           fused ? &f_up : nullptr);
+                                           fused ? &f_up : nullptr,
+                                           route_inl || perm_inl ? &ri : nullptr);
                 },
                 [&] {
                   return !fused && p.ks_up > 1
@@ -839,6 +871,13 @@ static int device_cus() {
 static int dense8_mode() {
   const char* v = std::getenv("SLLM_MOE_DENSE8");
   return v && v[0] == '0' ? 0 : (v && v[0] == '2' ? 2 : 1);
+}
+
+// SLLM_MOE_ROUTE_INLINE=0: decode routes in its own launches (the same
+// tables, bit for bit).
+static bool route_inline_on() {
+  const char* v = std::getenv("SLLM_MOE_ROUTE_INLINE");
+  return !(v && v[0] == '0');
 }
 
 static bool dense_layer(const sllm_moe_ds_args* a) {

@@ -26,9 +26,10 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x;
 }
 
-// Block-wide exclusive scan of one value per thread (1024 threads, 16
-// waves): a DPP scan inside each wave, the 16 wave totals through LDS,
-// two barriers in all. sh needs 16 ints.
+// Block-wide exclusive scan of one value per thread (NW waves, 1024
+// threads by default): a DPP scan inside each wave, the NW wave totals
+// through LDS, two barriers in all. sh needs NW ints.
+template <int NW = 16>
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int x = wave_incl_scan(v);
@@ -36,7 +37,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
   __syncthreads();
   int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < 16; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int t = sh[w];
     base += w < wave ? t : 0;
     tot += t;
@@ -46,45 +47,55 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
   return base + x - v;
 }
 
-// One workgroup of 16 waves (1024 threads) permutes N <= PERM_FUSED_MAX_N
-// assignments over E <= PERM_FUSED_MAX_E experts. Wave w owns the contiguous
-// assignment range [w R, (w + 1) R) and keeps its ids in registers;
-// histogram per wave in LDS, one scan over (expert, wave) for counts,
-// offsets, the tile table and each wave's per-expert base, then every wave
-// scatters its range in order: lanes holding the same expert are matched
-// with one ballot per id bit, so the rank among equal ids is the popcount
-// of lower matching lanes (stable, atomic-free). `ids` may point to global
-// memory or LDS; hist / sh are the workgroup's LDS scratch.
+// One workgroup permutes N assignments over E experts: NW waves (1024
+// threads in the permutation launches, 512 in the decode gate/up launch
+// that routes its own batch), N <= NW G 64, E <= min(HE, NW 64). Wave w
+// owns the contiguous assignment range [w R, (w + 1) R) and keeps its ids
+// in registers; histogram per wave in LDS, one scan over (expert, wave)
+// for counts, offsets, the tile table and each wave's per-expert base,
+// then every wave scatters its range in order: lanes holding the same
+// expert are matched with one ballot per id bit, so the rank among equal
+// ids is the popcount of lower matching lanes (stable, atomic-free). `ids`
+// may point to global memory or LDS; hist / sh are the workgroup's LDS
+// scratch. The results go to d0 and to d1 (global arrays or LDS copies);
+// a null pointer in either is not written.
 constexpr int PERM_FUSED_MAX_E = 1024;
 constexpr int PERM_FUSED_WAVES = 16;
 constexpr int PERM_FUSED_G = 4;  // 64-assignment groups per wave
 constexpr int PERM_FUSED_MAX_N = PERM_FUSED_WAVES * PERM_FUSED_G * 64;
 
-__device__ __forceinline__ void permute_fused_body(
-    const int* ids, int N, int E, int nbits, int bm, int* __restrict__ counts,
-    int* __restrict__ offsets, int* __restrict__ sorted_idx,
-    int* __restrict__ inv_pos, int* __restrict__ tile_info,
-    int* __restrict__ num_tiles, int max_tiles,
-    int (*hist)[PERM_FUSED_MAX_E], int* sh, int* __restrict__ zero = nullptr,
-    int nzero = 0) {
+struct PermDst {
+  int* counts;      // E
+  int* offsets;     // E + 1
+  int* sorted_idx;  // N
+  int* inv_pos;     // N
+  int* tile_info;   // 4 max_tiles
+  int* num_tiles;   // 1
+};
+
+template <int NW, int G, int HE>
+__device__ __forceinline__ void permute_block(
+    const int* ids, int N, int E, int nbits, int bm, int max_tiles,
+    const PermDst& d0, const PermDst& d1, int (*hist)[HE], int* sh,
+    int* __restrict__ zero = nullptr, int nzero = 0) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < nzero; i += 1024) zero[i] = 0;
-  const int R = ((N + PERM_FUSED_WAVES - 1) / PERM_FUSED_WAVES + 63) & ~63;
+  for (int i = tid; i < nzero; i += NW * 64) zero[i] = 0;
+  const int R = ((N + NW - 1) / NW + 63) & ~63;
   const int a0 = min(N, wave * R), a1 = min(N, a0 + R);
-  int idv[PERM_FUSED_G];
+  int idv[G];
 #pragma unroll
-  for (int g = 0; g < PERM_FUSED_G; ++g) {
+  for (int g = 0; g < G; ++g) {
     const int a = a0 + g * 64 + lane;
     const int v = ids[min(a, N - 1)];
     idv[g] = a < a1 ? v : -1;
   }
   if (tid < E) {
 #pragma unroll
-    for (int w = 0; w < PERM_FUSED_WAVES; ++w) hist[w][tid] = 0;
+    for (int w = 0; w < NW; ++w) hist[w][tid] = 0;
   }
   __syncthreads();
 #pragma unroll
-  for (int g = 0; g < PERM_FUSED_G; ++g) {
+  for (int g = 0; g < G; ++g) {
     const int e = idv[g];
     if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
   }
@@ -92,7 +103,7 @@ __device__ __forceinline__ void permute_fused_body(
   int cnt = 0;
   if (tid < E) {
 #pragma unroll
-    for (int w = 0; w < PERM_FUSED_WAVES; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const int v = hist[w][tid];
       hist[w][tid] = cnt;
       cnt += v;
@@ -100,22 +111,27 @@ __device__ __forceinline__ void permute_fused_body(
   }
   const int ntile = (tid < E && cnt > 0) ? (cnt + bm - 1) / bm : 0;
   int tot_rows, tot_tiles;
-  const int off = block_excl_scan(cnt, sh, tot_rows);
-  const int toff = block_excl_scan(ntile, sh, tot_tiles);
+  const int off = block_excl_scan<NW>(cnt, sh, tot_rows);
+  const int toff = block_excl_scan<NW>(ntile, sh, tot_tiles);
   if (tid < E) {
-    counts[tid] = cnt;
-    offsets[tid] = off;
+    if (d0.counts) d0.counts[tid] = cnt;
+    if (d1.counts) d1.counts[tid] = cnt;
+    if (d0.offsets) d0.offsets[tid] = off;
+    if (d1.offsets) d1.offsets[tid] = off;
 #pragma unroll
-    for (int w = 0; w < PERM_FUSED_WAVES; ++w) hist[w][tid] += off;
+    for (int w = 0; w < NW; ++w) hist[w][tid] += off;
     for (int i = 0; i < ntile && toff + i < max_tiles; ++i) {
       const int r0 = i * bm;
-      *(int4*)(tile_info + 4 * (toff + i)) =
-          make_int4(tid, off + r0, min(bm, cnt - r0), 0);
+      const int4 t4 = make_int4(tid, off + r0, min(bm, cnt - r0), 0);
+      if (d0.tile_info) *(int4*)(d0.tile_info + 4 * (toff + i)) = t4;
+      if (d1.tile_info) *(int4*)(d1.tile_info + 4 * (toff + i)) = t4;
     }
   }
   if (tid == 0) {
-    offsets[E] = tot_rows;
-    *num_tiles = min(tot_tiles, max_tiles);
+    if (d0.offsets) d0.offsets[E] = tot_rows;
+    if (d1.offsets) d1.offsets[E] = tot_rows;
+    if (d0.num_tiles) *d0.num_tiles = min(tot_tiles, max_tiles);
+    if (d1.num_tiles) *d1.num_tiles = min(tot_tiles, max_tiles);
   }
   __syncthreads();
   // each wave walks its own range with its own base row: program order
@@ -123,12 +139,15 @@ __device__ __forceinline__ void permute_fused_body(
   int* run = hist[wave];
   const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int g = 0; g < PERM_FUSED_G; ++g) {
+  for (int g = 0; g < G; ++g) {
     const int a = a0 + g * 64 + lane;
     const int raw = idv[g];
     const bool valid = raw >= 0 && raw < E;
     const int e = valid ? raw : 0;
-    if (!valid && a < a1) inv_pos[a] = -1;  // dropped: the combine skips it
+    if (!valid && a < a1) {  // dropped: the combine skips it
+      if (d0.inv_pos) d0.inv_pos[a] = -1;
+      if (d1.inv_pos) d1.inv_pos[a] = -1;
+    }
     uint64_t peers = __ballot(valid);
     if (peers == 0) continue;  // an empty group (uniform across the wave)
     for (int b = 0; b < nbits; ++b) {
@@ -140,12 +159,27 @@ __device__ __forceinline__ void permute_fused_body(
     __builtin_amdgcn_wave_barrier();
     if (valid) {
       const int pos = start + __popcll(peers & lt);
-      sorted_idx[pos] = a;
-      inv_pos[a] = pos;
+      if (d0.sorted_idx) d0.sorted_idx[pos] = a;
+      if (d1.sorted_idx) d1.sorted_idx[pos] = a;
+      if (d0.inv_pos) d0.inv_pos[a] = pos;
+      if (d1.inv_pos) d1.inv_pos[a] = pos;
       if ((peers >> lane) == 1ull) run[e] = start + __popcll(peers);
     }
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+// The permutation launches' form: 16 waves, results to global memory.
+__device__ __forceinline__ void permute_fused_body(
+    const int* ids, int N, int E, int nbits, int bm, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted_idx,
+    int* __restrict__ inv_pos, int* __restrict__ tile_info,
+    int* __restrict__ num_tiles, int max_tiles,
+    int (*hist)[PERM_FUSED_MAX_E], int* sh, int* __restrict__ zero = nullptr,
+    int nzero = 0) {
+  const PermDst d{counts, offsets, sorted_idx, inv_pos, tile_info, num_tiles};
+  permute_block<PERM_FUSED_WAVES, PERM_FUSED_G, PERM_FUSED_MAX_E>(
+      ids, N, E, nbits, bm, max_tiles, d, PermDst{}, hist, sh, zero, nzero);
 }
 
 }  // namespace sllm

@@ -22,6 +22,7 @@
 #include "launch.h"
 #include "lds_dma.h"
 #include "permute_fused.h"
+#include "route_token.h"
 
 namespace sllm {
 
@@ -179,14 +180,19 @@ constexpr int RG_SMALL_T = 64;
 // all read sgl; column 0 is kept): unsplit it writes sigmoid(logit) to
 // gate_out[t], split it writes chunk q's partial to gate_out[T + q T + t]
 // and the routing kernel adds the partials in order and applies the
-// sigmoid (route_gate_finish).
+// sigmoid (route_gate_finish). zero[0, nzero) is cleared (a later
+// launch's counters).
 template <int NTI>
 __global__ __launch_bounds__(512) void router_gemm_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     float* __restrict__ logits, int T, int E, int H,
-    const uint16_t* __restrict__ sgl, float* __restrict__ gate_out) {
+    const uint16_t* __restrict__ sgl, float* __restrict__ gate_out,
+    int* __restrict__ zero, long nzero) {
   __shared__ float part[8][NTI * 16][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (long i = ((long)blockIdx.y * gridDim.x + blockIdx.x) * 512 + threadIdx.x;
+       i < nzero; i += (long)gridDim.x * gridDim.y * 512)
+    zero[i] = 0;
   const int lr = lane & 15, lg = lane >> 4;
   const int e0 = blockIdx.x * 16;
   const bool gate_tile = e0 >= E;
@@ -241,100 +247,6 @@ __global__ __launch_bounds__(512) void router_gemm_small_kernel(
       out[(size_t)r * E + e0 + c] = s;
     }
   }
-}
-
-// --------------------------------------------------------------------------
-// softmax top-k with renormalisation (ref/qwen4_exp.py:118-140)
-// --------------------------------------------------------------------------
-// Top-k keys: the order key of the value (f32_order_key) in the high half,
-// ~e in the low half, so that a larger key is a larger value and, among
-// equal values, the lower expert id e; 0 = no candidate. -0 is keyed as +0:
-// the two are equal values (and give equal probabilities), so they tie.
-__device__ __forceinline__ uint64_t topk_key(float v, int e) {
-  v = v == 0.f ? 0.f : v;
-  return ((uint64_t)f32_order_key(v) << 32) |
-         (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-}
-
-__device__ __forceinline__ float topk_key_value(uint64_t key) {
-  const uint32_t k = (uint32_t)(key >> 32);
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-__device__ __forceinline__ int topk_key_id(uint64_t key) {
-  return (int)(0xFFFFFFFFu - (uint32_t)key);
-}
-
-// Descending sorting networks (2, 4, 8 inputs: 1, 5, 19 comparators).
-template <int N>
-__device__ __forceinline__ void sort_desc(uint64_t (&k)[N]) {
-  auto ce = [&](int i, int j) {
-    const uint64_t a = k[i], b = k[j];
-    const bool sw = b > a;
-    k[i] = sw ? b : a;
-    k[j] = sw ? a : b;
-  };
-  if constexpr (N == 2) {
-    ce(0, 1);
-  } else if constexpr (N == 4) {
-    ce(0, 1); ce(2, 3); ce(0, 2); ce(1, 3); ce(1, 2);
-  } else if constexpr (N == 8) {
-    ce(0, 2); ce(1, 3); ce(4, 6); ce(5, 7);
-    ce(0, 4); ce(1, 5); ce(2, 6); ce(3, 7);
-    ce(0, 1); ce(2, 3); ce(4, 5); ce(6, 7);
-    ce(2, 4); ce(3, 5);
-    ce(1, 4); ce(3, 6);
-    ce(1, 2); ce(3, 4); ce(5, 6);
-  }
-}
-
-// Descending top-k of the wave's candidate keys (key[i] of each lane, 0 =
-// none; keys are distinct, as each carries its expert id); lane j < topk
-// returns pick j's key (0 past the candidates).
-// Up to 8 keys per lane: each lane sorts its keys once, then every pick
-// is one wave maximum of the lanes' heads and a pop on the owning lane.
-// More keys per lane: every pick takes the lane maxima afresh.
-template <int EPL>
-__device__ __forceinline__ uint64_t wave_topk_keys(uint64_t (&key)[EPL],
-                                                   int topk) {
-  const int lane = threadIdx.x & 63;
-  uint64_t mine = 0;
-  if constexpr (EPL <= 8) {
-    sort_desc<EPL>(key);
-    for (int kk = 0; kk < topk; ++kk) {
-      // the maximum of the value halves; the full 64-bit keys only decide
-      // between lanes that share it
-      const uint32_t hi = (uint32_t)(key[0] >> 32);
-      const uint32_t mhi = wave_max_u32(hi);
-      const uint64_t bal = __ballot(hi == mhi);
-      uint64_t best;
-      if (__popcll(bal) == 1) {
-        const int owner = (int)__builtin_ctzll(bal);
-        best = ((uint64_t)mhi << 32) |
-               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], owner);
-      } else {
-        best = wave_max_u64(hi == mhi ? key[0] : 0ull);
-      }
-      if (lane == kk) mine = best;
-      if (best != 0 && key[0] == best) {  // the one lane whose head it is
-#pragma unroll
-        for (int i = 0; i + 1 < EPL; ++i) key[i] = key[i + 1];
-        key[EPL - 1] = 0;
-      }
-    }
-  } else {
-    for (int kk = 0; kk < topk; ++kk) {
-      uint64_t best = 0;
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-      best = wave_max_u64(best);
-      if (lane == kk) mine = best;
-#pragma unroll
-      for (int i = 0; i < EPL; ++i)
-        if (best != 0 && key[i] == best) key[i] = 0;
-    }
-  }
-  return mine;
 }
 
 // --------------------------------------------------------------------------
@@ -699,118 +611,6 @@ __global__ __launch_bounds__(512, 1) void router_topk_kernel(
   }
 }
 
-// The calling wave's logits of one row (lane holds experts lane + 64 i;
-// fill past E) when the row is held as ks K-chunk slices kstride floats
-// apart (the split decode router GEMM): slices are added in order, the
-// loads of G slices in flight together. With several slices
-// the owning wave (store) writes the sums back into slice 0, which then
-// holds the logits the routing used (the debug copy reads slice 0).
-// G: slices whose loads are in flight together (registers: G * EPL).
-template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
-__device__ __forceinline__ void logit_sums(float* row, int ks, long kstride,
-                                           int E, bool store, float fill,
-                                           float (&v)[EPL]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < E ? row[e] : fill;
-  }
-  if (ks <= 1) return;
-  for (int q0 = 1; q0 < ks; q0 += G) {
-    float t[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        const int e = lane + 64 * i;
-        t[g][i] = q0 + g < ks && e < E ? row[(q0 + g) * kstride + e] : 0.f;
-      }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) v[i] += t[g][i];
-  }
-  if (store) {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E) row[e] = v[i];
-    }
-  }
-}
-
-// Lane j < topk holds pick j; m and s are the row's largest logit and sum
-// of exp(l - m): pick j's probability is exp(l - m) / s, and the weights
-// are those probabilities over their sum in pick order plus eps
-// (ref/qwen4_exp.py:118-140).
-__device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
-                                             int topk, float eps,
-                                             float* __restrict__ w_row,
-                                             int* __restrict__ id_row,
-                                             int* id_lds) {
-  const int lane = threadIdx.x & 63;
-  const float pn = expf(topk_key_value(pick) - m) / s;  // lane j: pick j
-  float wsum = 0.f;
-  for (int j = 0; j < topk; ++j)
-    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pn), j));
-  if (lane < topk) {
-    const int myid = topk_key_id(pick);
-    w_row[lane] = pn / (wsum + eps);
-    id_row[lane] = myid;
-    if (id_lds) id_lds[lane] = myid;
-  }
-}
-
-// One token's softmax top-k on the calling wave: row = the token's E logits
-// (plus bias[e] when bias is given, after the slices are added; the row
-// keeps the logits without it); lanes j < topk write slot j of w_row /
-// id_row (and of id_lds when given).
-// The selection runs on the logits (softmax is monotone in them); pick j's
-// probability is exp(l - max) / sum recomputed from its key, and the
-// weights are those probabilities over their sum in pick order plus eps
-// (ref/qwen4_exp.py:118-140).
-template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
-__device__ __forceinline__ void route_softmax_token(
-    float* row, int ks, long kstride, int E, int topk, float eps,
-    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds,
-    const float* __restrict__ bias) {
-  const int lane = threadIdx.x & 63;
-  float v[EPL];
-  logit_sums<EPL, G>(row, ks, kstride, E, true, -INFINITY, v);
-  if (bias) {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E) v[i] += bias[e];
-    }
-  }
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) m = fmaxf(m, v[i]);
-  m = wave_max(m);
-  float s = 0.f;
-  uint64_t key[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + 64 * i;
-    s += e < E ? expf(v[i] - m) : 0.f;
-    key[i] = e < E ? topk_key(v[i], e) : 0ull;
-  }
-  s = wave_sum(s);
-  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
-  softmax_emit(pick, m, s, topk, eps, w_row, id_row, id_lds);
-}
-
-// Token t's shared-expert gate from the split router GEMM's ks partial
-// logits (gate[T + q T + t]): added in chunk order, sigmoid into gate[t].
-__device__ __forceinline__ void route_gate_finish(float* gate, int T, int t,
-                                                  int ks) {
-  float g = gate[T + t];
-  for (int q = 1; q < ks; ++q) g += gate[T + q * T + t];
-  gate[t] = sigmoid_f32(g);
-}
-
 template <int EPL>
 __global__ __launch_bounds__(256) void route_softmax_kernel(
     float* logits, float* __restrict__ w_out, int* __restrict__ id_out, int T,
@@ -1166,15 +966,21 @@ int router_ksplit(int T, int H) {
 static int launch_router_small(const uint16_t* x, const uint16_t* w,
                                float* logits, int T, int E, int H,
                                const uint16_t* sgl, float* gate_out, int ks,
-                               hipStream_t st) {
+                               hipStream_t st, int* zero = nullptr,
+                               long nzero = 0) {
   SLLM_REQUIRE(ks >= 1 && ks <= H / 32, "router_small: bad K split %d", ks);
+  SLLM_REQUIRE(nzero >= 0 && (nzero == 0 || zero), "router_small: bad zero range");
   const dim3 grid(ceil_div(E, 16) + (gate_out ? 1 : 0), ks);
+#define CASE(n)                                                              \
+  router_gemm_small_kernel<n><<<grid, 512, 0, st>>>(x, w, logits, T, E, H,   \
+                                                    sgl, gate_out, zero, nzero)
   switch (ceil_div(T, 16)) {
-    case 1: router_gemm_small_kernel<1><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
-    case 2: router_gemm_small_kernel<2><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
-    case 3: router_gemm_small_kernel<3><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
-    default: router_gemm_small_kernel<4><<<grid, 512, 0, st>>>(x, w, logits, T, E, H, sgl, gate_out); break;
+    case 1: CASE(1); break;
+    case 2: CASE(2); break;
+    case 3: CASE(3); break;
+    default: CASE(4); break;
   }
+#undef CASE
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1309,16 +1115,23 @@ int launch_route_merge(const RouterPart& rp, int T, int E, float eps,
 int launch_router_small_gate(const uint16_t* x, const uint16_t* w,
                              float* logits, int T, int E, int H,
                              const uint16_t* sgl, float* gate_out,
-                             hipStream_t st, int ks) {
+                             hipStream_t st, int ks, int* zero, long nzero) {
   SLLM_REQUIRE(x && w && logits && T > 0 && T <= RG_SMALL_T && E > 0 &&
                    H % 32 == 0 && (!gate_out || sgl),
                "router_small_gate: bad args (T=%d E=%d H=%d)", T, E, H);
-  return launch_router_small(x, w, logits, T, E, H, sgl, gate_out, ks, st);
+  return launch_router_small(x, w, logits, T, E, H, sgl, gate_out, ks, st,
+                             zero, nzero);
 }
 
 // One workgroup routes every token (a wave per token): worth it only while
 // the tokens fit one pass of the 16 waves; larger batches route with the
 // multi-workgroup kernel.
+bool route_inline_fits(int T, int E, int topk, long max_tiles) {
+  return T > 0 && T <= RG_SMALL_T && E >= topk && E <= RI_MAX_E &&
+         topk > 0 && topk <= 64 && (long)T * topk <= RI_MAX_N &&
+         max_tiles <= RI_MAX_TILES;
+}
+
 bool route_permute_small_fits(int T, int E, int topk) {
   return T <= PERM_FUSED_WAVES && (long)T * topk <= PERM_FUSED_MAX_N &&
          E <= PERM_FUSED_MAX_E;

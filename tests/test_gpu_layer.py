@@ -137,6 +137,71 @@ def test_qwen_decode_32_row_tiles(B, E, k):
     assert rel < 1e-4
 
 
+@pytest.mark.parametrize("B,E,k,biased", [(1, 512, 10, False), (3, 64, 6, True),
+                                          (4, 512, 10, True), (8, 512, 10, False),
+                                          (16, 64, 6, False), (17, 64, 6, True),
+                                          (32, 512, 10, True), (40, 4, 2, False),
+                                          (64, 512, 10, False)])
+def test_decode_inline_routing_matches_launches(B, E, k, biased, monkeypatch):
+    """Streamed decode builds the expert-major permutation inside the
+    gate/up launch (every workgroup in LDS, workgroup 0 writing the tables
+    for the later launches): up to 8 tokens after routing them there too
+    (one token per wave), above 16 tokens from the routing launch's ids;
+    9-16 tokens keep the one-workgroup route + permute launch (B=16 here).
+    SLLM_MOE_ROUTE_INLINE=0 routes and permutes in their own launches. The
+    output, route weights, ids, counts, sorted rows and inverse positions
+    agree bit for bit, on repeated calls. Covered: with and without a
+    router bias, the fused gate/up finish (B <= 4), the split router's
+    logit slices and shared-gate partials (B > 16), and 32-row tiles
+    (E = 4). The output also matches the oracle layer on the launch path's
+    logits."""
+    from sllm_amd.moe import QwenMoE, _up, qwen_forward_dev
+    from sllm_amd.runtime import DeviceBuffer, to_bf16
+    H, I = 512, 256
+    make = qwen_fp8_gpu if E >= 256 else qwen_fp8
+    x, W = make(seed=700 + B + E, T=B, H=H, E=E, I=I, Is=I)
+    rng = np.random.default_rng(B + E)
+    bias = (-rng.random(E) * 2.0).astype(np.float32) if biased else None
+    layer = QwenMoE(W.router_w, W.wg_q, W.wu_q, W.wd_q, W.wg_s, W.wu_s, W.wd_s,
+                    sg=W.sg_q, su=W.su_q, sd=W.sd_q, sg_s=W.sg_s, su_s=W.su_s,
+                    sd_s=W.sd_s, sgl=W.sgl, top_k=k, router_bias=bias)
+    N = B * k
+    shapes = {"w_out": (np.float32, (B, k)), "ids_out": (np.int32, (B, k)),
+              "counts_out": (np.int32, (E,)), "sorted_out": (np.int32, (N,)),
+              "inv_pos_out": (np.int32, (N,))}
+
+    def run():
+        dbg = {n: DeviceBuffer(int(np.prod(s)) * 4) for n, (_, s) in shapes.items()}
+        out = DeviceBuffer(B * H * 4)
+        qwen_forward_dev(_up(to_bf16(x)), out, layer._w, T=B, H=H, E=E, I=I,
+                         Is=I, topk=k, mode="decode", out_f32=True,
+                         eps=layer.eps, workspace=layer._workspace(B, "decode", False),
+                         debug=dbg)
+        res = {"y": out.copy_host().reshape(B, H)}
+        for n, (dt, s) in shapes.items():
+            res[n] = dbg[n].copy_host_raw(dt, s)
+        return res
+
+    def same(a, b, what):
+        for n in a:
+            np.testing.assert_array_equal(a[n].view(np.uint32), b[n].view(np.uint32),
+                                          err_msg=f"{what}: {n}")
+
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "1")
+    inl = run()
+    same(inl, run(), "inline, second call")
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "0")
+    same(inl, run(), "inline vs launches")
+    y, r = layer.forward(x, mode="decode", return_routing=True)
+    np.testing.assert_array_equal(y, inl["y"])
+    lg = r["logits"] + (bias[None, :] if biased else 0.0)
+    assert check_qwen_routing(lg.astype(np.float32), inl["ids_out"], inl["w_out"], k,
+                              name=f"inline B={B}").size == 0
+    want = qm.moe_layer_fp8_dequant(x, lg.astype(np.float32), W, k)
+    rel, _, _ = _report(f"inline routing B={B} E={E}", inl["y"], want)
+    assert rel < 1e-4
+
+
 def test_qwen_logits_given_and_auto_mode():
     x, W = qwen_fp8(seed=5, T=96, H=512, E=8, I=256, Is=256)
     layer = qwen_layer(W, 3)
