@@ -83,9 +83,14 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.decode = force_gemv || pick_decode(mode, T);
   // The Qwen layer routes decode batches that fit one workgroup in one
   // fused launch (route_permute_small_fits), which would read every logit
-  // slice through one CU: its router stays unsplit there.
-  const bool fused_route =
-      !deepseek && p.decode && route_permute_small_fits(T, E, topk);
+  // slice through one CU: its router stays unsplit there. Up to
+  // RI_MAX_ROUTE_T tokens the streamed layer routes inside the gate/up
+  // launch instead, whose workgroups each read the slices: split there.
+  const bool inl_route = !deepseek && p.decode && !force_gemv &&
+                         T <= RI_MAX_ROUTE_T && route_inline_fits(T, E, topk, 0) &&
+                         route_inline_on();
+  const bool fused_route = !deepseek && p.decode && !inl_route &&
+                           route_permute_small_fits(T, E, topk);
   p.ks_r = p.decode && need_logits && !fused_route ? router_ksplit(T, H) : 1;
   p.N = T * topk;
   if (p.decode) {

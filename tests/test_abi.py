@@ -101,21 +101,27 @@ def test_host_bf16_rounding_matches_python():
     np.testing.assert_array_equal(got, to_bf16(x))
 
 
-def test_decode_workspace_holds_split_router_slices():
+@pytest.mark.parametrize("inline", ["1", "0"])
+def test_decode_workspace_holds_split_router_slices(inline, monkeypatch):
     """Host plan, no GPU: a decode call that computes its own logits splits
-    the router GEMM's K over 2 workgroups when its batch is routed by the
-    multi-workgroup kernels (17 <= T <= 64 here), so its workspace holds 2
-    partial-logit slices of T * E floats and 2 partial gate slices of T
-    floats beyond a call given the logits. Batches routed in one fused
-    workgroup (T <= 16) and prefill keep one slice; prefill also holds the
-    fused router's partials: per token and 128-expert tile, a (max, sum)
-    pair and k top-k keys of 8 bytes."""
+    the router GEMM's K over 2 workgroups when its batch is routed by
+    many workgroups: by the multi-workgroup routing kernel (17 <= T <= 64
+    here), or up to 8 tokens inside the gate/up launch, whose workgroups
+    each read the slices. Its workspace then holds 2 partial-logit slices
+    of T * E floats and 2 partial gate slices of T floats beyond a call
+    given the logits. Batches routed in one fused workgroup (9 <= T <= 16,
+    and T <= 8 with SLLM_MOE_ROUTE_INLINE=0) and prefill keep one slice;
+    prefill also holds the fused router's partials: per token and
+    128-expert tile, a (max, sum) pair and k top-k keys of 8 bytes."""
     from sllm_amd.moe import qwen_workspace_bytes as wsb
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", inline)
 
     def up256(n):
         return -(-n // 256) * 256
     H, E, I, Is, k = 2048, 512, 512, 512, 10
-    for T, mode, split in ((1, "decode", False), (16, "decode", False),
+    for T, mode, split in ((1, "decode", inline == "1"),
+                           (8, "decode", inline == "1"), (9, "decode", False),
+                           (16, "decode", False),
                            (17, "decode", True), (32, "decode", True),
                            (64, "decode", True), (128, "prefill", False)):
         own = wsb(T, H, E, I, Is, k, mode)
