@@ -586,7 +586,8 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_kernel(
     // 16-row groups holding tile rows (wave-uniform): the e8m0-scaled
     // MFMAs of the padding groups past them are skipped (C4: gate/up 2.37 ->
     // 2.32 ms, down 1.32 -> 1.24). The fp32-scale path keeps its
-    // branch-free group loop: skipping there made C2's gate/up 6% slower.
+    // branch-free group loop: skipping there made C2's gate/up 10% slower
+    // and C5's (whose cold experts leave half-empty second tiles) 25%.
     const int ngrp = __builtin_amdgcn_readfirstlane((crows + 15) >> 4);
     auto sx_of = [&](int row) -> float {  // activation scale of a tile row
       if constexpr (PERSTEP) return sa_lds[buf][row][0];
