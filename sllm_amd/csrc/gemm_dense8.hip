@@ -18,7 +18,8 @@
 //   ahead: the step's 128 gathered activation rows (XOR-swizzled by row),
 //   its 32 KB packed weight block verbatim (already in MFMA fragment order)
 //   and the rows' activation scales. Waves 0-3 issue them (thirteen loads
-//   per wave per stage), spread over their first groups' MFMAs; the next
+//   per wave per stage), spread over their first groups' MFMAs (on an
+//   item's last step too, before its epilogue); the next
 //   stage is made ready (vmcnt, then a fence-free barrier) before a step's
 //   last group, whose MFMA issue covers the barrier and the next step's
 //   first fragment reads.
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(D8_THREADS, 1) void moe_dense8_kernel(
       uint8_t* const nst = j == 0 ? stg1 : (j == 1 ? stg2 : stg0);
       uint8_t* const nxt = j == 0 ? stg2 : (j == 1 ? stg0 : stg1);
       const bool last = ckb + 1 == KB;
-      const bool spread = loader && !last && s + 2 < total_steps;
+      const bool spread = loader && s + 2 < total_steps;
       Frag cur_f = nf;
       const WFrag g = ng;
       // weight scale of subtile q: gate / up of the slab, or the wave's
@@ -381,7 +382,6 @@ __global__ __launch_bounds__(D8_THREADS, 1) void moe_dense8_kernel(
       if (spread) advance();
       if (last) {
         epilogue(ci);
-        if (s + 2 < total_steps) issue(nxt);
         if (s + 1 < total_steps) ng = wfrag_at(nst);
       }
     };
