@@ -856,10 +856,105 @@ __device__ __forceinline__ void dec_fused_finish(
   }
 }
 
+// Fused combine of a decode down launch (DecCombine, launch.h), run by
+// every workgroup after its last item, with the ordering argument of
+// dec_fused_finish: the y slices went out as device-scope (sc1) stores,
+// each thread waits for its own (vmcnt 0) before the barrier, and the
+// finisher reads the slices with device-scope loads once the count's
+// return value says its arrival was the unit's last. A unit (token t,
+// 256-column slab) expects one arrival per K slice of each kept slot of t
+// and per shared-expert slice. Its sum is launch_combine_split's: a group
+// of four waves takes the slices (slot-major, then K slice, then shared)
+// w, w + 4, ... in batches of CF_BATCH loads, and the four partial sums
+// are added in wave order; the two wave groups take a unit each.
+constexpr int DC_BATCH = 8;  // combine_f32_kernel's batch of slice loads
+
+template <int BM>
+__device__ __forceinline__ void dec_fused_combine(
+    const SegDesc& S0, const SegDesc& S1, const DecCombine& C,
+    const int4* desc, int nitems, int* jobs, int& njob, int (*pos)[64],
+    float4 (*part)[4][64]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nslab = C.H / 256;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores done
+  if (tid == 0) njob = 0;
+  __syncthreads();
+  for (int q = tid; q < nitems * BM; q += ST_THREADS) {
+    const int i = q / BM, r = q % BM;
+    const int4 d = desc[i];
+    if (r >= d.w) continue;
+    const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF;
+    // a routed tile's rows are one expert's assignments: distinct tokens
+    const int t = seg ? d.z + r : C.sorted[d.z + r] / C.topk;
+    int kept = 0;
+    for (int j = 0; j < C.topk; ++j) kept += C.inv[t * C.topk + j] >= 0;
+    const int want = kept * C.ks + (C.y_sh ? C.ks_sh : 0);
+    // relaxed device-scope count: see dec_fused_finish
+    if (__hip_atomic_fetch_add(C.cnt + t * nslab + nt, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) == want - 1)
+      jobs[atomicAdd(&njob, 1)] = t * nslab + nt;
+  }
+  __syncthreads();
+  const int nj = njob;
+  const int g = wave >> 2, wq = wave & 3;
+  const __amdgpu_buffer_rsrc_t ry = dev_rsrc(C.y);
+  const __amdgpu_buffer_rsrc_t rs = dev_rsrc(C.y_sh ? C.y_sh : C.y);
+  const int nr = C.topk * C.ks, nsl = nr + (C.y_sh ? C.ks_sh : 0);
+  for (int u0 = 0; u0 < nj; u0 += 2) {
+    const bool live = u0 + g < nj;
+    const int u = live ? jobs[u0 + g] : jobs[u0];
+    const int t = u / nslab, c = (u % nslab) * 256 + lane * 4;
+    if (wq == 0 && lane < C.topk) pos[g][lane] = C.inv[t * C.topk + lane];
+    __syncthreads();
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int b = wq; b < nsl; b += 4 * DC_BATCH) {
+      float4 v[DC_BATCH];
+#pragma unroll
+      for (int k = 0; k < DC_BATCH; ++k) {
+        const int sl = min(b + k * 4, nsl - 1);
+        // a dropped assignment (position -1) reads row 0 and is not added
+        v[k] = sl < nr
+                   ? ld_dev4(ry, (sl % C.ks) * C.kstride +
+                                     (long)max(pos[g][sl / C.ks], 0) * C.H + c)
+                   : ld_dev4(rs, (sl - nr) * C.kstride_sh + (long)t * C.H + c);
+      }
+#pragma unroll
+      for (int k = 0; k < DC_BATCH; ++k) {
+        const int sl = b + k * 4;
+        if (sl < nsl && (sl >= nr || pos[g][sl / C.ks] >= 0)) {
+          acc.x += v[k].x;
+          acc.y += v[k].y;
+          acc.z += v[k].z;
+          acc.w += v[k].w;
+        }
+      }
+    }
+    part[g][wq][lane] = acc;
+    __syncthreads();
+    if (wq == 0 && live) {
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float4 p = part[g][w][lane];
+        acc.x += p.x;
+        acc.y += p.y;
+        acc.z += p.z;
+        acc.w += p.w;
+      }
+      if (C.out_f32) {
+        *(float4*)((float*)C.out + (size_t)t * C.H + c) = acc;
+      } else {
+        *(uint2*)((uint16_t*)C.out + (size_t)t * C.H + c) =
+            make_uint2(pk_bf16(acc.x, acc.y), pk_bf16(acc.z, acc.w));
+      }
+    }
+    __syncthreads();  // pos and part are the next pair's
+  }
+}
+
 template <int BF, int MODE, bool WNT, int BM>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F,
-    RouteInline RI) {
+    RouteInline RI, DecCombine C) {
   constexpr int RB = BM / 16;
   static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
@@ -1142,10 +1237,15 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       } else {
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
-          float* out = (float*)S.y + kc * S.pstride + (size_t)(d.z + row) * S.N +
-                       nt * 256 + wave * 32 + sb * 16 + lg * 4;
-          *(float4*)out = make_float4(acc[r][sb][0] * rw, acc[r][sb][1] * rw,
-                                      acc[r][sb][2] * rw, acc[r][sb][3] * rw);
+          const long o = kc * S.pstride + (long)(d.z + row) * S.N + nt * 256 +
+                         wave * 32 + sb * 16 + lg * 4;
+          if (C.cnt)  // read by the fused combine's finisher: device scope
+            st_dev4(dev_rsrc((const float*)S.y), o, acc[r][sb][0] * rw,
+                    acc[r][sb][1] * rw, acc[r][sb][2] * rw, acc[r][sb][3] * rw);
+          else
+            *(float4*)((float*)S.y + o) =
+                make_float4(acc[r][sb][0] * rw, acc[r][sb][1] * rw,
+                            acc[r][sb][2] * rw, acc[r][sb][3] * rw);
         }
       }
     }
@@ -1246,6 +1346,14 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       __shared__ int jobs[ST_MAX_ITEMS];
       __shared__ int njob;
       dec_fused_finish<BM>(S0, S1, limit, F, desc, nitems, jobs, njob);
+    }
+  } else {
+    if (C.cnt) {
+      __shared__ int cjobs[ST_MAX_ITEMS * BM];
+      __shared__ int ncj;
+      __shared__ int cpos[2][64];
+      __shared__ float4 cpart[2][4][64];
+      dec_fused_combine<BM>(S0, S1, C, desc, nitems, cjobs, ncj, cpos, cpart);
     }
   }
 }
@@ -1471,7 +1579,8 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 template <int BF, int MODE, int BM>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st,
-                         const DecFuse& fuse, const RouteInline& route) {
+                         const DecFuse& fuse, const RouteInline& route,
+                         const DecCombine& comb) {
   {
     const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, BM,
                                     upper_items, "stream decode gemm");
@@ -1492,7 +1601,7 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
   }
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route);
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route, comb);
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1500,7 +1609,8 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
 int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
                       long upper_items, hipStream_t st, int bm,
-                      const DecFuse* fuse_in, const RouteInline* route_in) {
+                      const DecFuse* fuse_in, const RouteInline* route_in,
+                      const DecCombine* comb_in) {
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
                    (bm == 16 || bm == 32),
                "stream decode gemm: bad format or tile rows %d", bm);
@@ -1562,9 +1672,29 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
     route.nbits = 0;
     while ((1 << route.nbits) < route.E) ++route.nbits;
   }
+  DecCombine comb{};
+  if (comb_in && comb_in->cnt) {
+    comb = *comb_in;
+    const long sh_rows = s1 ? s1->total_rows : 0;
+    SLLM_REQUIRE(mode == 1 && comb.inv && comb.sorted && comb.out &&
+                     comb.y == (const float*)s0.y && comb.ks == s0.ksplit &&
+                     comb.kstride == s0.pstride && comb.topk == topk &&
+                     comb.topk > 0 && comb.topk <= 64 && comb.H == s0.N &&
+                     comb.H % 256 == 0 && s0.tile_info && s0.sorted_idx &&
+                     comb.T > 0 && (long)comb.T * comb.topk <= (1L << 24) &&
+                     (s1 ? (comb.y_sh == (const float*)s1->y &&
+                            comb.ks_sh == s1->ksplit &&
+                            comb.kstride_sh == s1->pstride &&
+                            sh_rows == comb.T && !s1->tile_info)
+                         : comb.y_sh == nullptr) &&
+                     4L * comb.ks * comb.kstride < (1L << 31) &&
+                     4L * comb.ks_sh * comb.kstride_sh < (1L << 31),
+                 "stream decode gemm: bad fused combine (T=%d H=%d k=%d)",
+                 comb.T, comb.H, comb.topk);
+  }
 #define GO(B, M)                                                         \
-  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse, route) \
-                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse, route)
+  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse, route, comb) \
+                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse, route, comb)
   if (mode == 0) {
     if (bf == SF_FP4) GO(SF_FP4, 0);
     GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales

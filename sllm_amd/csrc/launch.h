@@ -305,11 +305,33 @@ struct RouteInline {
   float eps;
 };
 bool route_inline_fits(int T, int E, int topk, long max_tiles);
+// A mode-1 decode launch may also do the weighted combine (DecCombine.cnt
+// non-null): its y slices go out as device-scope stores, every workgroup
+// counts, after its last item, each of its item rows' arrival at
+// cnt[t (H / 256) + slab] (zeroed earlier on the same stream), and the
+// workgroup whose arrival completes a (token, 256-column slab) unit adds
+// the unit's slices as launch_combine_split does -- the same partial sums
+// in the same order, so out equals that launch's bit for bit.
+struct DecCombine {
+  int* cnt;
+  const int* inv;     // inv_pos: permuted row of assignment t topk + j, or -1
+  const int* sorted;  // sorted_idx: assignment of permuted row p
+  const float* y;     // ks routed slices of N x H, kstride floats apart
+  long kstride;
+  int ks;
+  const float* y_sh;  // ks_sh shared-expert slices of T x H, or null
+  long kstride_sh;
+  int ks_sh;
+  int T, H, topk, out_f32;
+  void* out;
+};
+inline long dec_combine_counters(long T, int H) { return T * (H / 256); }
 int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       int topk, float limit, long upper_items,
                       hipStream_t st, int bm = 16,
                       const DecFuse* fuse = nullptr,
-                      const RouteInline* route = nullptr);
+                      const RouteInline* route = nullptr,
+                      const DecCombine* comb = nullptr);
 // Counter ints of a fused gate/up launch: N routed rows, T shared rows.
 inline long dec_fuse_counters(long N, long T, int I, int Is) {
   return N * (I / 128) + T * (Is / 128);

@@ -41,7 +41,9 @@ struct Plan {
   // (Qwen: routed and shared segments in one launch each; DeepSeek: the
   // shared expert's launches are the *_sh ones)
   long up_items, dn_items, up_sh_items, dn_sh_items;
-  size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters
+  size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters,
+                // then the fused combine's (fcnt_on)
+  bool fcnt_on;
   size_t rpart;  // Qwen prefill router partials (RouterPart), or 0
   size_t total;
 };
@@ -155,8 +157,11 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.gu = p.ks_up > 1 ? take(c, (size_t)2 * p.ks_up * p.N * I * 4) : 0;
     p.gu_sh = has_shared && p.ks_up_sh > 1
                   ? take(c, (size_t)2 * p.ks_up_sh * T * Is * 4) : 0;
-    if (!deepseek && !force_gemv && T <= DEC_FUSE_MAX_T)
-      p.fcnt = take(c, (size_t)dec_fuse_counters(p.N, T, I, has_shared ? Is : 0) * 4);
+    if (!deepseek && !force_gemv && T <= DEC_FUSE_MAX_T) {
+      p.fcnt_on = true;
+      p.fcnt = take(c, (size_t)(dec_fuse_counters(p.N, T, I, has_shared ? Is : 0) +
+                                dec_combine_counters(T, H)) * 4);
+    }
   } else {
     p.xq = take(c, (size_t)T * H);
     p.sx = take(c, (size_t)T * (H / 128) * 4);
@@ -323,9 +328,9 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   // Streamed decode of a routed layer at a few tokens: the gate/up launch
   // finishes its K-split items itself (DecFuse) on counters the
   // permutation launch clears, which saves the finish launch (B=1: 44 ->
-  // 42 us). From B=8 on the separate finish launch is as fast, and a fused
-  // combine in the down launch was slower at every batch size (its units
-  // complete together at the launch's end).
+  // 42 us); with the routing in the gate/up launch the router launch
+  // clears them. From 5 tokens on the finish launch is as fast or faster
+  // (B=8: 76.5 vs 76.9 us with the fused finish).
   const bool fused = p.decode && a->wgu_packed && !one_expert && !bf16w &&
                      T <= DEC_FUSE_MAX_T && (p.ks_up > 1 || p.ks_up_sh > 1);
   int* fcnt = fused ? (int*)(ws + p.fcnt) : nullptr;
@@ -349,6 +354,19 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   const bool route_inl = inl_ok && small_router && T <= RI_MAX_ROUTE_T &&
                          (!a->logits_out || p.ks_r == 1);
   const bool perm_inl = inl_ok && !route_inl && !small_route && !fused;
+  // One token: the down launch also does the combine (DecCombine: a
+  // counter per 256-column slab), which leaves three launches (router,
+  // gate/up, down; B=1 39.2 -> 39.0 us). From two tokens on the units'
+  // finishing queues on the last workgroups of the launch (every unit
+  // completes at its end): B=2 / 4 / 8 +2.6 / +3.8 / +5.8 us, and at
+  // 32-64 tokens +11-12 us, so the combine keeps its launch there.
+  const bool comb_inl = route_inl && p.fcnt_on && T == 1;
+  const long nccnt = comb_inl ? dec_combine_counters(T, H) : 0;
+  int* ccnt = comb_inl ? (int*)(ws + p.fcnt) + dec_fuse_counters(p.N, T, I, sh ? Is : 0)
+                       : nullptr;
+  // the counters the router launch clears (both sets, whichever run)
+  int* rzero = route_inl && p.fcnt_on ? (int*)(ws + p.fcnt) : nullptr;
+  const long nrzero = rzero ? dec_fuse_counters(p.N, T, I, sh ? Is : 0) + nccnt : 0;
   // Prefill: the softmax routing launch also quantizes each token's row
   // (and forms the shared-expert gate), in place of the activation-quant
   // launch (one wave per token in both; C2: 11.8 + 11.3 -> 19.8 us).
@@ -369,8 +387,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                                    (const uint16_t*)a->router_w, logits, T, E,
                                    H, sh ? (const uint16_t*)a->sgl : nullptr,
                                    sh ? gate : nullptr, st, p.ks_r,
-                                   route_inl ? fcnt : nullptr,
-                                   route_inl ? nfcnt : 0));
+                                   rzero, nrzero));
     gate_done = sh;
   }
   // split router: the routing launch finishes the gate from its partials
@@ -513,16 +530,27 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       s2.wp = (const uint8_t*)a->sd_packed; s2.s0 = a->sd_s; s2.N = H;
       s2.K = Is; s2.row_w = gate; s2.y = (uint16_t*)y_sh;
       s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
+      DecCombine dc{};
+      if (comb_inl) {
+        dc.cnt = ccnt; dc.inv = inv; dc.sorted = sorted;
+        dc.y = y; dc.kstride = (long)p.N * H; dc.ks = p.ks_dn;
+        dc.y_sh = sh ? y_sh : nullptr; dc.kstride_sh = (long)T * H;
+        dc.ks_sh = sh ? p.ks_dn_sh : 0;
+        dc.T = T; dc.H = H; dc.topk = k; dc.out_f32 = a->out_f32;
+        dc.out = a->out;
+      }
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
             launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
-                              p.dn_items, st, p.bm));
+                              p.dn_items, st, p.bm, nullptr, nullptr,
+                              comb_inl ? &dc : nullptr));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
       STAGE(clk, SLLM_MOE_STAGE_COMBINE,
-            launch_combine_split(y, one_expert ? nullptr : inv, k, y_sh, T, H,
-                                 a->out_f32, a->out,
-                                 p.ks_dn, (long)p.N * H, p.ks_dn_sh,
-                                 (long)T * H, st));
+            comb_inl ? 0
+                     : launch_combine_split(y, one_expert ? nullptr : inv, k,
+                                            y_sh, T, H, a->out_f32, a->out,
+                                            p.ks_dn, (long)p.N * H, p.ks_dn_sh,
+                                            (long)T * H, st));
     } else {
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           launch_gemv(wf, 1, a->x, 1, 1, sorted, k, p.N, tiles, ntiles,
