@@ -229,7 +229,8 @@ def _stage_times(call_with_events, nstages, reps=10):
     per = {s: [] for s in STAGES}
     for _ in range(reps):
         call_with_events(evs)
-        evs[-1].synchronize()
+        for e in evs:  # stages a call skips are recorded at its end
+            e.synchronize()
         for i, s in enumerate(STAGES):
             per[s].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]))
     return {s: round(statistics.median(v), 4) for s, v in per.items()}
@@ -793,7 +794,8 @@ def decode_leg(layer, batches, iters, flush):
             for it in range(10):
                 memset(flush, it & 0xFF, flush.nbytes)
                 layer_call(layer, xb, ob, wsb, B, "decode", stage_events=evs)
-                evs[-1].synchronize()
+                for e in evs:
+                    e.synchronize()
                 for i, s_ in enumerate(STAGES):
                     per[s_].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3)
             decode[str(B)]["stage_us"] = {s_: round(statistics.median(v), 2)
@@ -936,7 +938,8 @@ def main(argv=None) -> int:
     per_stage = {s: [] for s in STAGES}
     for _ in range(max(5, min(args.steps, 20))):
         layer_call(layer, x, out, ws, T, "prefill", stage_events=evs)
-        evs[-1].synchronize()
+        for e in evs:
+            e.synchronize()
         for i, s in enumerate(STAGES):
             per_stage[s].append(evs[2 * i].elapsed_ms(evs[2 * i + 1]))
     stage_ms = {s: statistics.median(v) for s, v in per_stage.items()}

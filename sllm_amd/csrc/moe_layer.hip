@@ -182,12 +182,21 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
 struct StageClock {
   void** ev;
   hipStream_t st;
+  mutable unsigned done = 0;  // stages whose events are recorded
   int begin(int s) const {
     if (ev) SLLM_HIP(hipEventRecord((hipEvent_t)ev[2 * s], st));
     return 0;
   }
   int end(int s) const {
     if (ev) SLLM_HIP(hipEventRecord((hipEvent_t)ev[2 * s + 1], st));
+    done |= 1u << s;
+    return 0;
+  }
+  // Stages the call did not reach: recorded with zero length at the end,
+  // so that every stage's events exist on every call.
+  int finish() const {
+    for (int s = 0; s < SLLM_MOE_STAGES; ++s)
+      if (!(done & (1u << s)) && (begin(s) || end(s))) return -1;
     return 0;
   }
 };
@@ -684,6 +693,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
+  if (clk.finish()) return -1;
   return copy_debug(logits, w, ids, counts, sorted, inv, T, E, p.N,
                     a->logits_out, a->w_out, a->ids_out, a->counts_out,
                     a->sorted_out, a->inv_pos_out, st);
@@ -984,9 +994,17 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
             : launch_route_grouped(logits, a->bias, w, ids, T, E, k,
                                    a->n_group, a->topk_group, a->scoring,
                                    a->route_scale, st, p.ks_r));
+  // Streamed decode: the routed gate/up launch builds the permutation from
+  // the routing launch's ids in every workgroup (RouteInline.ids_in), in
+  // place of the permutation launch, as in the Qwen layer.
+  const bool perm_inl = p.decode && a->w13_packed &&
+                        route_inline_fits(T, E, k, p.max_tiles) &&
+                        route_inline_on();
   STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
-        launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv, tiles,
-                       ntiles, p.max_tiles, ws + p.pscr, st));
+        perm_inl ? 0
+                 : launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted,
+                                  inv, tiles, ntiles, p.max_tiles, ws + p.pscr,
+                                  st));
 
   if (p.decode && a->w13_packed) {
     // streamed packed weights, unquantized activations; the route weight
@@ -1011,11 +1029,20 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.wp = (const uint8_t*)a->w2_packed; r2.s0 = a->w2_s_packed;
     r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
+    RouteInline ri{};
+    if (perm_inl) {
+      ri.ids_in = ids;
+      ri.counts = counts; ri.offsets = offsets; ri.sorted = sorted;
+      ri.inv = inv; ri.tiles = tiles; ri.ntiles = ntiles;
+      ri.T = T; ri.E = E; ri.topk = k; ri.ks = 1; ri.bm = p.bm;
+      ri.max_tiles = p.max_tiles;
+    }
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           first_rc(
               [&] {
                 return launch_stream_dec(2, 0, r1, nullptr, k, L, p.up_items,
-                                         st, p.bm);
+                                         st, p.bm, nullptr,
+                                         perm_inl ? &ri : nullptr);
               },
               [&] {
                 return p.ks_up > 1 ? launch_split_finish(r1, nullptr, L, st)
@@ -1176,6 +1203,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
           launch_combine(y, 0, inv, k, y_sh, T, H, a->out_f32, a->out, st));
   }
+  if (clk.finish()) return -1;
   return copy_debug(logits, w, ids, counts, sorted, inv, T, E, p.N,
                     a->logits_out, a->w_out, a->ids_out, a->counts_out,
                     a->sorted_out, a->inv_pos_out, st);

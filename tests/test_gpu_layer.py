@@ -592,6 +592,35 @@ def test_deepseek_decode(B):
     assert rel < 1e-4
 
 
+@pytest.mark.parametrize("B,hashed", [(1, False), (8, False), (24, False),
+                                      (64, False), (13, True)])
+def test_deepseek_decode_inline_permutation_matches_launch(B, hashed, monkeypatch):
+    """Streamed DeepSeek decode builds the expert-major permutation in the
+    routed gate/up launch (every workgroup in LDS, workgroup 0 writing the
+    tables for the down and combine launches) from the grouped or hash
+    routing launch's ids; SLLM_MOE_ROUTE_INLINE=0 runs the permutation
+    launch instead. The output and the routing agree bit for bit."""
+    x, W = deepseek_mxfp4(seed=90 + B, T=B, H=1024, E=16, I=512, Is=512)
+    kw = dict(n_group=4, topk_group=2, scoring="sigmoid", route_scale=2.5,
+              swiglu_limit=10.0)
+    fwd = {}
+    if hashed:
+        rng = np.random.default_rng(B)
+        tid2eid = np.stack([rng.permutation(16)[:4] for _ in range(40)]).astype(np.int32)
+        kw = dict(scoring="sigmoid", route_scale=2.5, tid2eid=tid2eid)
+        fwd = dict(token_ids=rng.integers(0, 40, B).astype(np.int32))
+    layer = deepseek_layer(W, 4, **kw)
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "1")
+    y1, r1 = layer.forward(x, mode="decode", return_routing=True, **fwd)
+    np.testing.assert_array_equal(layer.forward(x, mode="decode", **fwd), y1)
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "0")
+    y0, r0 = layer.forward(x, mode="decode", return_routing=True, **fwd)
+    np.testing.assert_array_equal(y1.view(np.uint32), y0.view(np.uint32))
+    for n in ("logits", "w", "ids", "counts"):
+        np.testing.assert_array_equal(np.asarray(r1[n]).view(np.uint32),
+                                      np.asarray(r0[n]).view(np.uint32), err_msg=n)
+
+
 @pytest.mark.parametrize("T", [1, 13, 32, 64])
 def test_decode_router_split_logits(T):
     """Decode-size router GEMM with its K split over workgroups: the
