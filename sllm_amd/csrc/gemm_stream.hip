@@ -727,28 +727,26 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// e2m1 nibble -> fp32 (exact)
-__device__ __forceinline__ float e2m1_f32(uint32_t n) {
-  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
-  const uint32_t bits = e ? ((e + 126u) << 23) | (m << 22) : (m ? 0x3F000000u : 0u);
-  return __uint_as_float(bits | ((n & 8u) << 28));
-}
-
-// 8 e2m1 values (one dword, low nibble first) times scale -> 8 bf16
-__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t d, float scale) {
-  float f[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) f[j] = e2m1_f32((d >> (4 * j)) & 15u) * scale;
-  const v4uv r = {pack_bf16_hi(f[0], f[1]), pack_bf16_hi(f[2], f[3]),
-                    pack_bf16_hi(f[4], f[5]), pack_bf16_hi(f[6], f[7])};
+// 8 e2m1 values (one dword, low nibble first) times the e8m0 scale byte sb
+// -> 8 bf16, exact: v_cvt_scalef32_pk_bf16_fp4 converts the two nibbles of
+// byte j (low nibble first) times 2^(exponent of its f32 scale operand - 127)
+// in one instruction. Checked on gfx950 against e2m1 * 2^(sb - 127) in fp32
+// for every data byte and scale byte: bit-identical, denormals included, for
+// sb 1..254, and NaN for sb 255, as the loader convention has it
+// (loaders/fp8.py:145-156). The instruction reads sb 0 as 2^-127, where the
+// convention has a zero scale: the data word is zeroed instead (+0 for -0
+// products, which leaves every sum unchanged).
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t d, uint32_t sb) {
+  d = sb ? d : 0u;
+  const float s = __uint_as_float(sb << 23);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 0);
+  const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 1);
+  const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 2);
+  const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, s, 3);
+  const v4uv r = {__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                  __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
   return __builtin_bit_cast(bf16x8, r);
-}
-
-// e8m0 byte -> fp32 scale, loader convention (loaders/fp8.py:145-156):
-// 0x00 -> 0, 0xFF -> NaN
-__device__ __forceinline__ float e8m0_f32(uint32_t b) {
-  return b == 0 ? 0.f : (b == 255 ? __uint_as_float(0x7FC00000u)
-                                  : __uint_as_float(b << 23));
 }
 
 // BM: rows per tile, 16 or 32 (RB = BM / 16 row blocks; each weight
@@ -1295,7 +1293,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       for (int sb = 0; sb < 2; ++sb) {
         bf16x8 wv;
         if constexpr (BF == SF_FP4) {
-          wv = fp4x8_to_bf16((uint32_t)bcur.v[sb][mm], e8m0_f32((bcur.sc >> (8 * sb)) & 0xFF));
+          wv = fp4x8_to_bf16((uint32_t)bcur.v[sb][mm], (bcur.sc >> (8 * sb)) & 0xFFu);
         } else {
           wv = fp8x8_to_bf16((uint32_t)bcur.v[sb][2 * mm], (uint32_t)bcur.v[sb][2 * mm + 1]);
         }

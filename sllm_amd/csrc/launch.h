@@ -229,12 +229,22 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   // launch. Decode launches always stream.
   int wreuse;
 };
-// Items per XCD chunk of a decode launch: one row tile's items of its first
-// segment (column slabs of ntw columns x K chunks). The kernel deals with
-// this chunk and the host sizes the grid with it.
-__host__ __device__ inline int dec_deal_chunk(const SegDesc& s, int ntw) {
-  const int c = (s.N / ntw) * (s.ksplit > 1 ? s.ksplit : 1);
+// Items per XCD chunk of a decode launch, from its first segment: one row
+// tile's items (column slabs of ntw columns x K chunks) for routed rows, so
+// that the items of a tile, which read the same A rows, meet in one L2; an
+// eighth of that for identity rows (the DeepSeek shared expert's launches,
+// one row tile up to 16 or 32 tokens, whose A rows are a few KB per token),
+// so that a one-tile launch still reaches all 8 XCDs (one-tile chunks left
+// 7 of them idle: C4 B=1 shared gate/up 36.1 us, down 27.2 us). The kernel
+// deals with this chunk and the host sizes the grid with it.
+__host__ __device__ inline int dec_deal_chunk(int N, int ntw, int ksplit,
+                                              bool routed) {
+  const int tile = (N / ntw) * (ksplit > 1 ? ksplit : 1);
+  const int c = routed ? tile : (tile + 7) / 8;
   return c > 1 ? c : 1;
+}
+__host__ __device__ inline int dec_deal_chunk(const SegDesc& s, int ntw) {
+  return dec_deal_chunk(s.N, ntw, s.ksplit, s.tile_info != nullptr);
 }
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,

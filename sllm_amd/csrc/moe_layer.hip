@@ -871,10 +871,11 @@ int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,
   const long items[4] = {p.up_items, p.dn_items, p.up_sh_items, p.dn_sh_items};
   for (int j = 0; j < 4; ++j) {
     if (items[j] <= 0) continue;
-    SegDesc s{};
-    s.N = segN[j];
-    s.ksplit = segks[j];
-    const long cb = dec_deal_chunk(s, ntw[j]);
+    // the routed launches' rows come from the tile table (identity rows for
+    // a one-expert Qwen layer, run as a dense MLP), the DeepSeek shared
+    // expert's are identity rows
+    const bool routed = j < 2 && (deepseek || E > 1 || topk > 1);
+    const long cb = dec_deal_chunk(segN[j], ntw[j], segks[j], routed);
     out[10 + 3 * j] = items[j];
     out[11 + 3 * j] = cb;
     out[12 + 3 * j] = dec_launch_grid(items[j], cb);

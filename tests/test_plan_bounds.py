@@ -12,7 +12,9 @@ tests port the kernels' dealing exactly:
   in chunks of CB consecutive items (chunk c to XCD c % 8, the partial last
   chunk to XCD (total / CB) % 8), then round-robin over each XCD's
   workgroups; CB is one row tile's items of the first segment (column slabs,
-  times K chunks in decode).
+  times K chunks in decode), an eighth of that (rounded up) in decode
+  launches whose first segment has identity rows (the DeepSeek shared
+  expert, a one-expert layer).
 
 They take the library's own plans (sllm_moe_plan_query: tile rows, K
 splits, item bounds, deal chunks and grids) for decode batches of the
@@ -173,14 +175,16 @@ def test_decode_plans_deal_at_most_32_items(shape):
         for j, (per_tile, shared) in enumerate(launches):
             upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
             assert upper == max_tiles * per_tile + shared, (T, j)
-            assert cb == per_tile and grid % 8 == 0, (T, j)
+            # identity rows (a one-expert layer): an eighth of a tile
+            want_cb = per_tile if (ds or E > 1 or k > 1) else max(1, -(-per_tile // 8))
+            assert cb == want_cb and grid % 8 == 0, (T, j)
             worst = max(_max_items(rt * per_tile + shared, grid, cb)
                         for rt in range(1, max_tiles + 1))
             assert worst <= ST_MAX_ITEMS, (T, j, upper, cb, grid, worst)
         if ds and Is:
             for j, per_tile in ((2, Is // 128 * ks_up_sh), (3, H // 256 * ks_dn_sh)):
                 upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
-                assert upper == sh_rt * per_tile and cb == per_tile
+                assert upper == sh_rt * per_tile and cb == max(1, -(-per_tile // 8))
                 assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS, (T, j)
 
 
