@@ -25,13 +25,6 @@ enum WFmt { WF_FP8_BLOCK = 0, WF_MXFP4 = 1, WF_BF16 = 2, WF_F32 = 3 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// E2M1 nibble -> fp32 (exact): e = bits 1-2, m = bit 0, sign = bit 3.
-__device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
-  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
-  uint32_t bits = e ? ((e + 126u) << 23) | (m << 22) : (m ? 0x3F000000u : 0u);
-  return __uint_as_float(bits | ((n & 8u) << 28));
-}
-
 template <int WF>
 struct ChunkK {  // K values in one 16-byte chunk of a weight row
   static constexpr int value =
@@ -56,13 +49,27 @@ __device__ __forceinline__ void load_w_chunk(const uint8_t* row, int k0,
       w[4 * i + 3] = hi.y * scale;
     }
   } else if constexpr (WF == WF_MXFP4) {
+    // e2m1 * 2^(b - 127) is exact in bf16: v_cvt_scalef32_pk_bf16_fp4 makes
+    // two values per instruction (it reads only the exponent of its scale
+    // operand, so a zero scale zeroes the data instead; a NaN scale gives
+    // NaN), then they are widened to fp32
     const uint4 r = *(const uint4*)(row + k0 / 2);
     const uint32_t d[4] = {r.x, r.y, r.z, r.w};
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t di = scale == 0.f ? 0u : d[i];
+      const uint32_t p[4] = {
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(di, scale, 0)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(di, scale, 1)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(di, scale, 2)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(di, scale, 3))};
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        w[8 * i + j] = e2m1_to_f32((d[i] >> (4 * j)) & 15u) * scale;
+      for (int j = 0; j < 4; ++j) {
+        w[8 * i + 2 * j] = __uint_as_float(p[j] << 16);
+        w[8 * i + 2 * j + 1] = __uint_as_float(p[j] & 0xFFFF0000u);
+      }
+    }
   } else if constexpr (WF == WF_F32) {
     (void)scale;
     const float4 r = *(const float4*)(row + 4 * k0);

@@ -40,8 +40,6 @@ namespace sllm {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum { SF_FP8_F32S = 0, SF_FP8_POW2 = 1, SF_FP4 = 2 };
-
 constexpr int ST_BM = 128;
 constexpr int ST_LDS = 144;          // A row stride in LDS (128 + 16 pad)
 constexpr int ST_MAX_ITEMS = 32;     // work items per workgroup
@@ -949,11 +947,18 @@ __device__ __forceinline__ void dec_fused_combine(
   }
 }
 
-template <int BF, int MODE, bool WNT, int BM>
+template <int BF, int MODE, bool WNT, int BM, int BF1 = BF>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F,
-    RouteInline RI, DecCombine C) {
+    RouteInline RI, DecCombine C, int CB) {
   constexpr int RB = BM / 16;
+  // BF1 != BF: the first segment's weights are MXFP4 and the second's FP8
+  // with fp32 block scales (a DeepSeek layer's routed and shared experts in
+  // one launch); a workgroup streams its MXFP4 items, then its FP8 items
+  constexpr bool MIX = BF1 != BF;
+  static_assert(!MIX || (BF == SF_FP4 && BF1 == SF_FP8_F32S),
+                "mixed formats: MXFP4 first segment, FP8 second");
+  __shared__ int mix_nf4;  // mixed: the workgroup's MXFP4 items
   static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
   __shared__ int rsrc[ST_MAX_ITEMS][BM];
@@ -972,7 +977,6 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   __shared__ int ri_sh[ST_WAVES + 1];
 
   constexpr int NTW = MODE == 0 ? 128 : 256;
-  constexpr int BLK = BF == SF_FP4 ? 16384 : 32768;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, lc = lane & 15;
 
@@ -1026,12 +1030,11 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   const int total = n0 + n1;
   const int nx = gridDim.x / 8;
   const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
-  // XCD x takes chunks x, x + 8, ... of one row tile's items (its column
-  // slabs and K chunks), so that every XCD gets the same mix of routed and
-  // shared-expert items (as in the prefill kernel; C3 B=32 163.1 / 164.2 ->
-  // 161.6 / 160.6 us, B=1 and B=8 unchanged)
-  // (the host sizes the grid for this deal: stream_dec_grid)
-  const int CB = dec_deal_chunk(S0, NTW);
+  // XCD x takes chunks x, x + 8, ... of CB items (a row tile's items, its
+  // column slabs and K chunks, at most: dec_deal_chunk), so that every XCD
+  // gets the same mix of routed and shared-expert items (as in the prefill
+  // kernel; C3 B=32 163.1 / 164.2 -> 161.6 / 160.6 us, B=1 and B=8
+  // unchanged) (the host sizes the grid for this deal: stream_dec_grid)
   const int ncf = total / CB, crem = total % CB;
   const int xcount = (ncf > xcd ? (ncf - xcd + 7) / 8 : 0) * CB + (ncf % 8 == xcd ? crem : 0);
   const int nitems = xcount > jx ? (xcount - jx + nx - 1) / nx : 0;
@@ -1061,8 +1064,17 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       rb = rt * BM;
       rows = min(BM, S.total_rows - rb);
     }
+    int slot = tid;
+    if constexpr (MIX) {  // MXFP4 (first-segment) items first, in deal order
+      static_assert(ST_MAX_ITEMS <= 64, "a workgroup's items are one wave's lanes");
+      const uint64_t fp8 = __ballot(seg);  // lanes tid < nitems <= 32 of wave 0
+      const int nf8_below = __popcll(fp8 & ((1ull << tid) - 1));
+      const int nf4 = nitems - __popcll(fp8);
+      slot = seg ? nf4 + nf8_below : tid - nf8_below;
+      if (tid == 0) mix_nf4 = nf4;
+    }
     // x: segment (bit 0), column slab (bits 1-15), K chunk (bits 16-30)
-    desc[tid] = make_int4(seg | (nt << 1) | (kc << 16), e, rb, rows);
+    desc[slot] = make_int4(seg | (nt << 1) | (kc << 16), e, rb, rows);
   }
   __syncthreads();
   for (int q = tid; q < nitems * BM; q += ST_THREADS) {
@@ -1090,12 +1102,6 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     kb0 = kc * KB / S.ksplit;
     nkb = (kc + 1) * KB / S.ksplit - kb0;
   };
-  int total_steps = 0;
-  for (int i = 0; i < nitems; ++i) {
-    int kb0, nkb;
-    kchunk(i, kb0, nkb);
-    total_steps += nkb;
-  }
 
   // activation tile of a K step: BM rows x 128 values; thread tid takes
   // rows tid / 32 + 16 r and values [4 (tid % 32), +4)
@@ -1110,87 +1116,12 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     float sb0, sb1;
   };
 
-  int pi = 0, pkb = 0, pKB = 1;
-  const uint8_t* pa[RB];
-  const uint8_t* pb = nullptr;
-  const float *ps0 = nullptr, *ps1 = nullptr;
-  const uint16_t* ps4 = nullptr;
-  auto p_enter = [&](int i) {
-    const int4 d = desc[i];
-    const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF;
-    const SegDesc& S = seg ? S1 : S0;
-    const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
-    int kb0;
-    kchunk(i, kb0, pKB);
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-      pa[r] = S.a + ((size_t)rsrc[i][a_row + 16 * r] * K + kb0 * 128 + a_col) *
-                        (MODE == 0 ? 2 : 4);
-    const size_t blk0 = ((size_t)d.y * NT + nt) * KB + kb0;
-    if constexpr (BF == SF_FP4) {
-      pb = S.wp + blk0 * BLK + (wave * 2) * 1024 + lane * 16;
-      ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
-    } else {
-      pb = S.wp + blk0 * BLK + (wave * 4) * 1024 + lane * 16;
-      if constexpr (MODE == 0) {
-        ps0 = (const float*)S.s0 + blk0;
-        ps1 = (const float*)S.s1 + blk0;
-      } else {
-        const int nblk = nt * 2 + wave / 4;
-        ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB + kb0;
-      }
-    }
-  };
-  auto p_advance = [&]() {
-    if (pkb + 1 < pKB) {
-      ++pkb;
-    } else if (pi + 1 < nitems) {
-      ++pi;
-      pkb = 0;
-      p_enter(pi);
-    }
-  };
-  auto prefetch = [&](ASet& af, BSetD& b) {
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-      af.v[r] = *(const AVec*)(pa[r] + (size_t)pkb * 128 * (MODE == 0 ? 2 : 4));
-    const uint8_t* base = pb + (size_t)pkb * BLK;
-    if constexpr (BF == SF_FP4) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const uint4 v = ld_stream<WNT>(base + s * 1024);
-        b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-      }
-      b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
-      b.sb0 = b.sb1 = 1.f;
-    } else {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const uint4 lo4 = ld_stream<WNT>(base + (2 * s) * 1024);
-        const uint4 hi4 = ld_stream<WNT>(base + (2 * s + 1) * 1024);
-        b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
-                       (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
-      }
-      b.sc = 0;
-      b.sb0 = ps0[pkb];
-      b.sb1 = MODE == 0 ? ps1[pkb] : b.sb0;
-    }
-    p_advance();
-  };
-
   f32x4 acc[RB][2];
   auto clear_acc = [&]() {
 #pragma unroll
     for (int r = 0; r < RB; ++r) acc[r][0] = acc[r][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
   };
   clear_acc();
-
-  int ci = 0, ckb = 0, cKB = 1, crows = 0;
-  auto c_enter = [&](int i) {
-    int kb0;
-    kchunk(i, kb0, cKB);
-    crows = desc[i].w;
-  };
 
   // acc[r][s][v]: row 16 r + lc of the tile, output column 4 lg + v of
   // subtile s
@@ -1250,95 +1181,198 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     clear_acc();
   };
 
-  auto step = [&](int st, ASet& acur, ASet& aload, BSetD& bcur, BSetD& bload) {
-    const int buf = st & 1;
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {  // activations -> LDS as bf16 (mode 1: hi
-                                    // and lo halves), rows past the tile zeroed
-      const int row = a_row + 16 * r;
-      const uint32_t m = row < crows ? ~0u : 0u;
-      if constexpr (MODE == 0) {
-        *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
-            (u32x2){acur.v[r].x & m, acur.v[r].y & m};
-      } else {
-        float f[4] = {__uint_as_float(acur.v[r].x & m), __uint_as_float(acur.v[r].y & m),
-                      __uint_as_float(acur.v[r].z & m), __uint_as_float(acur.v[r].w & m)};
-        uint32_t hb[4], lb[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          hb[j] = f32_to_bf16(f[j]);
-          lb[j] = f32_to_bf16(f[j] - __uint_as_float(hb[j] << 16));
-        }
-        *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
-            (u32x2){hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-        *(u32x2*)(a_lo[buf] + row * SD_LS + a_col) =
-            (u32x2){lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-      }
+  // The streamed K steps of items [i0, i1), whose weights are all MXFP4
+  // (F4: 16 KB weight blocks, e8m0 scales applied in the conversion) or all
+  // FP8 (32 KB blocks, the step's partial times its fp32 block scale): one
+  // format per pipeline, so that its loads keep three steps in flight (a
+  // per-step format branch left the compiler waiting on all but a few
+  // loads at every step)
+  auto pipeline = [&](auto f4c, const int i0, const int i1) {
+    constexpr bool F4 = decltype(f4c)::value;
+    int total_steps = 0;
+    for (int i = i0; i < i1; ++i) {
+      int kb0, nkb;
+      kchunk(i, kb0, nkb);
+      total_steps += nkb;
     }
-    __syncthreads();
-    prefetch(aload, bload);
-    f32x4 part[RB][2];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) part[r][0] = part[r][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int mm = 0; mm < 4; ++mm) {
-      const int ko = lg * 32 + mm * 8;
-      bf16x8 xh[RB], xl[RB];
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        xh[r] = *(const bf16x8*)(a_hi[buf] + (16 * r + lc) * SD_LS + ko);
-        if constexpr (MODE == 1) xl[r] = *(const bf16x8*)(a_lo[buf] + (16 * r + lc) * SD_LS + ko);
-      }
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        bf16x8 wv;
-        if constexpr (BF == SF_FP4) {
-          wv = fp4x8_to_bf16((uint32_t)bcur.v[sb][mm], (bcur.sc >> (8 * sb)) & 0xFFu);
-        } else {
-          wv = fp8x8_to_bf16((uint32_t)bcur.v[sb][2 * mm], (uint32_t)bcur.v[sb][2 * mm + 1]);
-        }
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          f32x4& tgt = BF == SF_FP4 ? acc[r][sb] : part[r][sb];
-          tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xh[r], tgt, 0, 0, 0);
-          if constexpr (MODE == 1)
-            tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xl[r], tgt, 0, 0, 0);
-        }
-      }
-    }
-    if constexpr (BF != SF_FP4) {
+
+    int pi = i0, pkb = 0, pKB = 1;
+    const uint8_t* pa[RB];
+    const uint8_t* pb = nullptr;
+    const float *ps0 = nullptr, *ps1 = nullptr;
+    const uint16_t* ps4 = nullptr;
+    auto p_enter = [&](int i) {
+      const int4 d = desc[i];
+      const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF;
+      const SegDesc& S = seg ? S1 : S0;
+      const int K = S.K, KB = K / 128, N = S.N, NT = N / NTW;
+      int kb0;
+      kchunk(i, kb0, pKB);
 #pragma unroll
       for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          acc[r][0][v] = fmaf(part[r][0][v], bcur.sb0, acc[r][0][v]);
-          acc[r][1][v] = fmaf(part[r][1][v], bcur.sb1, acc[r][1][v]);
+        pa[r] = S.a + ((size_t)rsrc[i][a_row + 16 * r] * K + kb0 * 128 + a_col) *
+                          (MODE == 0 ? 2 : 4);
+      const size_t blk0 = ((size_t)d.y * NT + nt) * KB + kb0;
+      if constexpr (F4) {
+        pb = S.wp + blk0 * 16384 + (wave * 2) * 1024 + lane * 16;
+        ps4 = (const uint16_t*)S.s0 + blk0 * 512 + wave * 64 + lane;
+      } else {
+        pb = S.wp + blk0 * 32768 + (wave * 4) * 1024 + lane * 16;
+        if constexpr (MODE == 0) {
+          ps0 = (const float*)S.s0 + blk0;
+          ps1 = (const float*)S.s1 + blk0;
+        } else {
+          const int nblk = nt * 2 + wave / 4;
+          ps0 = ps1 = (const float*)S.s0 + ((size_t)d.y * (N / 128) + nblk) * KB + kb0;
         }
-    }
-    if (++ckb == cKB) {
-      epilogue(ci);
-      ckb = 0;
-      if (ci + 1 < nitems) c_enter(++ci);
-    }
-  };
+      }
+    };
+    auto p_advance = [&]() {
+      if (pkb + 1 < pKB) {
+        ++pkb;
+      } else if (pi + 1 < i1) {
+        ++pi;
+        pkb = 0;
+        p_enter(pi);
+      }
+    };
+    auto prefetch = [&](ASet& af, BSetD& b) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        af.v[r] = *(const AVec*)(pa[r] + (size_t)pkb * 128 * (MODE == 0 ? 2 : 4));
+      const uint8_t* base = pb + (size_t)pkb * (F4 ? 16384 : 32768);
+      if constexpr (F4) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const uint4 v = ld_stream<WNT>(base + s * 1024);
+          b.v[s] = (v8i){(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+        }
+        b.sc = __builtin_nontemporal_load(ps4 + (size_t)pkb * 512);
+        b.sb0 = b.sb1 = 1.f;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const uint4 lo4 = ld_stream<WNT>(base + (2 * s) * 1024);
+          const uint4 hi4 = ld_stream<WNT>(base + (2 * s + 1) * 1024);
+          b.v[s] = (v8i){(int)lo4.x, (int)lo4.y, (int)lo4.z, (int)lo4.w,
+                         (int)hi4.x, (int)hi4.y, (int)hi4.z, (int)hi4.w};
+        }
+        b.sc = 0;
+        b.sb0 = ps0[pkb];
+        b.sb1 = MODE == 0 ? ps1[pkb] : b.sb0;
+      }
+      p_advance();
+    };
 
-  BSetD b0, b1, b2, b3;
-  ASet a0, a1, a2, a3;
-  p_enter(0);
-  c_enter(0);
-  prefetch(a0, b0);
-  prefetch(a1, b1);
-  prefetch(a2, b2);
-  int st = 0;
-  for (; st + 4 <= total_steps; st += 4) {
-    step(st, a0, a3, b0, b3);
-    step(st + 1, a1, a0, b1, b0);
-    step(st + 2, a2, a1, b2, b1);
-    step(st + 3, a3, a2, b3, b2);
+    int ci = i0, ckb = 0, cKB = 1, crows = 0;
+    auto c_enter = [&](int i) {
+      int kb0;
+      kchunk(i, kb0, cKB);
+      crows = desc[i].w;
+    };
+
+    auto step = [&](int st, ASet& acur, ASet& aload, BSetD& bcur, BSetD& bload) {
+      const int buf = st & 1;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {  // activations -> LDS as bf16 (mode 1: hi
+                                      // and lo halves), rows past the tile zeroed
+        const int row = a_row + 16 * r;
+        const uint32_t m = row < crows ? ~0u : 0u;
+        if constexpr (MODE == 0) {
+          *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
+              (u32x2){acur.v[r].x & m, acur.v[r].y & m};
+        } else {
+          float f[4] = {__uint_as_float(acur.v[r].x & m), __uint_as_float(acur.v[r].y & m),
+                        __uint_as_float(acur.v[r].z & m), __uint_as_float(acur.v[r].w & m)};
+          uint32_t hb[4], lb[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            hb[j] = f32_to_bf16(f[j]);
+            lb[j] = f32_to_bf16(f[j] - __uint_as_float(hb[j] << 16));
+          }
+          *(u32x2*)(a_hi[buf] + row * SD_LS + a_col) =
+              (u32x2){hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+          *(u32x2*)(a_lo[buf] + row * SD_LS + a_col) =
+              (u32x2){lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+        }
+      }
+      __syncthreads();
+      prefetch(aload, bload);
+      f32x4 part[RB][2];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) part[r][0] = part[r][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        const int ko = lg * 32 + mm * 8;
+        bf16x8 xh[RB], xl[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          xh[r] = *(const bf16x8*)(a_hi[buf] + (16 * r + lc) * SD_LS + ko);
+          if constexpr (MODE == 1) xl[r] = *(const bf16x8*)(a_lo[buf] + (16 * r + lc) * SD_LS + ko);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          bf16x8 wv;
+          if constexpr (F4) {
+            wv = fp4x8_to_bf16((uint32_t)bcur.v[sb][mm], (bcur.sc >> (8 * sb)) & 0xFFu);
+          } else {
+            wv = fp8x8_to_bf16((uint32_t)bcur.v[sb][2 * mm], (uint32_t)bcur.v[sb][2 * mm + 1]);
+          }
+#pragma unroll
+          for (int r = 0; r < RB; ++r) {
+            f32x4& tgt = F4 ? acc[r][sb] : part[r][sb];
+            tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xh[r], tgt, 0, 0, 0);
+            if constexpr (MODE == 1)
+              tgt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, xl[r], tgt, 0, 0, 0);
+          }
+        }
+      }
+      if constexpr (!F4) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc[r][0][v] = fmaf(part[r][0][v], bcur.sb0, acc[r][0][v]);
+            acc[r][1][v] = fmaf(part[r][1][v], bcur.sb1, acc[r][1][v]);
+          }
+      }
+      if (++ckb == cKB) {
+        epilogue(ci);
+        ckb = 0;
+        if (ci + 1 < i1) c_enter(++ci);
+      }
+    };
+
+    BSetD b0, b1, b2, b3;
+    ASet a0, a1, a2, a3;
+    p_enter(i0);
+    c_enter(i0);
+    prefetch(a0, b0);
+    prefetch(a1, b1);
+    prefetch(a2, b2);
+    int st = 0;
+    for (; st + 4 <= total_steps; st += 4) {
+      step(st, a0, a3, b0, b3);
+      step(st + 1, a1, a0, b1, b0);
+      step(st + 2, a2, a1, b2, b1);
+      step(st + 3, a3, a2, b3, b2);
+    }
+    if (st < total_steps) step(st, a0, a3, b0, b3);
+    if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
+    if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+  };
+  if constexpr (MIX) {
+    // the MXFP4 items were placed first; the barrier hands the LDS
+    // activation buffers from the last MXFP4 step to the first FP8 one
+    const int nf4 = mix_nf4;
+    if (nf4 > 0) pipeline(std::true_type{}, 0, nf4);
+    if (nf4 < nitems) {
+      if (nf4 > 0) __syncthreads();
+      pipeline(std::false_type{}, nf4, nitems);
+    }
+  } else {
+    pipeline(std::integral_constant<bool, BF == SF_FP4>{}, 0, nitems);
   }
-  if (st < total_steps) step(st, a0, a3, b0, b3);
-  if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
-  if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
   if constexpr (MODE == 0) {
     if (F.cnt) {
       __shared__ int jobs[ST_MAX_ITEMS];
@@ -1574,7 +1608,7 @@ int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
 #undef GO
 }
 
-template <int BF, int MODE, int BM>
+template <int BF, int MODE, int BM, int BF1 = BF>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st,
                          const DecFuse& fuse, const RouteInline& route,
@@ -1584,9 +1618,9 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                                     upper_items, "stream decode gemm");
     if (rc) return rc;
   }
-  // the kernel deals its items to the XCDs in chunks of one row tile's
-  // items of the first segment (column slabs x K chunks)
-  const long cb = dec_deal_chunk(s0, MODE == 0 ? 128 : 256);
+  // the kernel deals its items to the XCDs in chunks of (at most) one row
+  // tile's items of the first segment (column slabs x K chunks)
+  const long cb = dec_deal_chunk(s0, MODE == 0 ? 128 : 256, upper_items);
   const long grid = dec_launch_grid(upper_items, cb);
   SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   {
@@ -1598,8 +1632,9 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                   ST_MAX_ITEMS, upper_items, cb, grid);
   }
   SegDesc dummy = s0;
-  moe_stream_dec_kernel<BF, MODE, true, BM><<<(unsigned)grid, ST_THREADS, 0, st>>>(
-      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route, comb);
+  moe_stream_dec_kernel<BF, MODE, true, BM, BF1><<<(unsigned)grid, ST_THREADS, 0, st>>>(
+      s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route, comb,
+      (int)cb);
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1608,10 +1643,14 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
                       long upper_items, hipStream_t st, int bm,
                       const DecFuse* fuse_in, const RouteInline* route_in,
-                      const DecCombine* comb_in) {
+                      const DecCombine* comb_in, int bf1) {
+  if (bf1 < 0 || !s1_in) bf1 = bf;
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
-                   (bm == 16 || bm == 32),
-               "stream decode gemm: bad format or tile rows %d", bm);
+                   (bm == 16 || bm == 32) &&
+                   (bf1 == bf || (bf == SF_FP4 && bf1 != SF_FP4 && bf1 >= 0 &&
+                                  bf1 <= 2)),
+               "stream decode gemm: bad format (%d, %d) or tile rows %d", bf,
+               bf1, bm);
   const int ntw = mode == 0 ? 128 : 256;
   SegDesc seg[2] = {s0_in, s1_in ? *s1_in : s0_in};
   for (int i = 0; i < (s1_in ? 2 : 1); ++i) {
@@ -1622,7 +1661,7 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                  "stream decode gemm: bad segment (N=%d K=%d)", s->N, s->K);
     SLLM_REQUIRE(mode == 1 ? s->y != nullptr : s->hq != nullptr,
                  "stream decode gemm: missing outputs");
-    SLLM_REQUIRE(bf == SF_FP4 || mode == 1 || s->s1,
+    SLLM_REQUIRE((i ? bf1 : bf) == SF_FP4 || mode == 1 || s->s1,
                  "stream decode gemm: missing W3 scales");
     SLLM_REQUIRE((!s->gather && !s->row_w_by_idx) || s->sorted_idx,
                  "stream decode gemm: gather / row_w_by_idx need sorted_idx");
@@ -1690,15 +1729,18 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                  "stream decode gemm: bad fused combine (T=%d H=%d k=%d)",
                  comb.T, comb.H, comb.topk);
   }
-#define GO(B, M)                                                         \
-  return bm == 32 ? go_stream_dec<B, M, 32>(s0, s1, topk, limit, upper_items, st, fuse, route, comb) \
-                  : go_stream_dec<B, M, 16>(s0, s1, topk, limit, upper_items, st, fuse, route, comb)
+  // fp32 scale arithmetic covers power-of-two fp8 scales (bf 1)
+#define GO(B, M, B1)                                                     \
+  return bm == 32 ? go_stream_dec<B, M, 32, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb) \
+                  : go_stream_dec<B, M, 16, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb)
   if (mode == 0) {
-    if (bf == SF_FP4) GO(SF_FP4, 0);
-    GO(SF_FP8_F32S, 0);  // fp32 scale arithmetic covers power-of-two scales
+    if (bf == SF_FP4 && bf1 != SF_FP4) GO(SF_FP4, 0, SF_FP8_F32S);
+    if (bf == SF_FP4) GO(SF_FP4, 0, SF_FP4);
+    GO(SF_FP8_F32S, 0, SF_FP8_F32S);
   } else {
-    if (bf == SF_FP4) GO(SF_FP4, 1);
-    GO(SF_FP8_F32S, 1);
+    if (bf == SF_FP4 && bf1 != SF_FP4) GO(SF_FP4, 1, SF_FP8_F32S);
+    if (bf == SF_FP4) GO(SF_FP4, 1, SF_FP4);
+    GO(SF_FP8_F32S, 1, SF_FP8_F32S);
   }
 #undef GO
 }

@@ -229,22 +229,29 @@ struct SegDesc {  // one segment (routed or shared expert) of a streamed launch
   // launch. Decode launches always stream.
   int wreuse;
 };
-// Items per XCD chunk of a decode launch, from its first segment: one row
-// tile's items (column slabs of ntw columns x K chunks) for routed rows, so
-// that the items of a tile, which read the same A rows, meet in one L2; an
-// eighth of that for identity rows (the DeepSeek shared expert's launches,
-// one row tile up to 16 or 32 tokens, whose A rows are a few KB per token),
-// so that a one-tile launch still reaches all 8 XCDs (one-tile chunks left
-// 7 of them idle: C4 B=1 shared gate/up 36.1 us, down 27.2 us). The kernel
-// deals with this chunk and the host sizes the grid with it.
-__host__ __device__ inline int dec_deal_chunk(int N, int ntw, int ksplit,
-                                              bool routed) {
+// Items per XCD chunk of a decode launch of at most upper_items items, from
+// its first segment: one row tile's items (column slabs of ntw columns x K
+// chunks) for routed rows, so that the items of a tile, which read the same
+// A rows, meet in one L2; an eighth of that for identity rows (the DeepSeek
+// shared expert's launches, one row tile up to 16 or 32 tokens, whose A
+// rows are a few KB per token), so that a one-tile launch still reaches all
+// 8 XCDs (one-tile chunks left 7 of them idle: C4 B=1 shared gate/up 36.1
+// us, down 27.2 us). Either way at most a 64th of the items, so that every
+// XCD takes about 8 chunks: with few tiles of many items (a K-split launch
+// at one token) whole-tile chunks gave one XCD twice the others' share (C4
+// B=1 gate/up with the shared expert as a 9th tile: 56 K steps per
+// workgroup against 32). The host passes it to the kernel and sizes the
+// grid with it.
+inline int dec_deal_chunk(int N, int ntw, int ksplit, bool routed,
+                          long upper_items) {
   const int tile = (N / ntw) * (ksplit > 1 ? ksplit : 1);
-  const int c = routed ? tile : (tile + 7) / 8;
-  return c > 1 ? c : 1;
+  long c = routed ? tile : (tile + 7) / 8;
+  c = std::min(c, upper_items / 64);
+  return c > 1 ? (int)c : 1;
 }
-__host__ __device__ inline int dec_deal_chunk(const SegDesc& s, int ntw) {
-  return dec_deal_chunk(s.N, ntw, s.ksplit, s.tile_info != nullptr);
+inline int dec_deal_chunk(const SegDesc& s, int ntw, long upper_items) {
+  return dec_deal_chunk(s.N, ntw, s.ksplit, s.tile_info != nullptr,
+                        upper_items);
 }
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
@@ -261,12 +268,17 @@ int launch_dense8(int mode, const SegDesc& s0, int f32s, int topk, float limit,
                   int pow2, hipStream_t st, int num_cus);
 int launch_dense(int mode, const SegDesc& s0, int topk, float limit, int pow2,
                  hipStream_t st, int num_cus);
+// Packed weight formats of the streamed launches (their bf argument): fp8
+// with fp32 block scales, fp8 with power-of-two block scales, MXFP4.
+enum { SF_FP8_F32S = 0, SF_FP8_POW2 = 1, SF_FP4 = 2 };
 // Decode variant over the same packed weights: bm-row tiles (16 or 32; the
 // tile_info rows must fit), weights converted to bf16 in registers and
 // multiplied by unquantized activations with bf16 MFMAs. mode 0 reads bf16 rows (a, row stride K elements) and
 // writes fp32 h rows to hq (as float*); mode 1 reads fp32 h rows (a as
 // float*, split into bf16 hi + lo) and writes fp32 rows to y (as float*).
-// bf: 0 / 1 fp8 (block scales applied in fp32), 2 MXFP4.
+// bf: 0 / 1 fp8 (block scales applied in fp32), 2 MXFP4; bf1 (-1: bf): the
+// second segment's format, which may differ only as MXFP4 first segment and
+// fp8 second (a DeepSeek layer's routed and shared experts in one launch).
 //
 // A mode-0 decode launch may also finish its K-split items itself
 // (DecFuse.cnt non-null): every workgroup, after its last item, counts its
@@ -341,7 +353,7 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       hipStream_t st, int bm = 16,
                       const DecFuse* fuse = nullptr,
                       const RouteInline* route = nullptr,
-                      const DecCombine* comb = nullptr);
+                      const DecCombine* comb = nullptr, int bf1 = -1);
 // Counter ints of a fused gate/up launch: N routed rows, T shared rows.
 inline long dec_fuse_counters(long N, long T, int I, int Is) {
   return N * (I / 128) + T * (Is / 128);

@@ -38,9 +38,11 @@ struct Plan {
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
   // decode, streamed kernels: item bounds of the gate/up and down launches
-  // (Qwen: routed and shared segments in one launch each; DeepSeek: the
-  // shared expert's launches are the *_sh ones)
+  // (routed and shared segments in one launch each; a DeepSeek layer whose
+  // shared expert takes taller tiles than the routed experts (sh_sep) runs
+  // it in launches of its own, the *_sh ones)
   long up_items, dn_items, up_sh_items, dn_sh_items;
+  bool sh_sep;
   size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters,
                 // then the fused combine's (fcnt_on)
   bool fcnt_on;
@@ -124,13 +126,31 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     if (!force_gemv) {  // the streamed kernels (the GEMV path does not split)
       const long rt = p.max_tiles;
       const long sh_rt = has_shared ? (T + p.bm_sh - 1) / p.bm_sh : 0;
-      if (deepseek) {
+      // DeepSeek: MXFP4 routed and FP8 shared segments share a launch (a
+      // mixed-format launch) when their tiles are equally tall (up to 16
+      // tokens; C4 B=1 91.5 -> 89.0 us, B=8 289 -> 278 us); taller shared
+      // tiles (32 rows from 17 tokens, which stream the shared weights once
+      // per 32 rows) keep launches of their own
+      p.sh_sep = deepseek && has_shared && p.bm_sh != p.bm;
+      if (p.sh_sep) {
         p.ks_up = dec_ksplit_up(rt * (I / 128), H / 128);
         p.ks_dn = dec_ksplit(rt * (H / 256), I / 128);
         if (has_shared) {
           p.ks_up_sh = dec_ksplit_up(sh_rt * (Is / 128), H / 128);
           p.ks_dn_sh = dec_ksplit(sh_rt * (H / 256), Is / 128);
         }
+      } else if (deepseek && has_shared) {
+        // mixed-format launches: an fp8 shared-expert K step streams twice
+        // the bytes of an MXFP4 routed one, so the shared items count double
+        // for the split and are cut twice as finely (items of equal bytes for
+        // the count-based deal; gate/up only where it splits anyway, which
+        // leaves the finish launch as it is)
+        p.ks_up = dec_ksplit_up(rt * (I / 128) + 2 * sh_rt * (Is / 128), H / 128);
+        p.ks_up_sh = p.ks_up > 1
+                         ? std::min(2 * p.ks_up, std::max(1, std::min(H / 128 / 4, 8)))
+                         : 1;
+        p.ks_dn = dec_ksplit(rt * (H / 256) + 2 * sh_rt * (H / 256), I / 128);
+        p.ks_dn_sh = std::min(2 * p.ks_dn, std::min(Is / 128, 32));
       } else {
         p.ks_up = p.ks_up_sh =
             dec_ksplit_up(rt * (I / 128) + sh_rt * (Is / 128), H / 128);
@@ -142,7 +162,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
       p.dn_items = rt * (H / 256) * p.ks_dn;
       const long sh_up = sh_rt * (Is / 128) * p.ks_up_sh;
       const long sh_dn = sh_rt * (H / 256) * p.ks_dn_sh;
-      if (deepseek) {
+      if (p.sh_sep) {
         p.up_sh_items = sh_up;
         p.dn_sh_items = sh_dn;
       } else {
@@ -875,7 +895,7 @@ int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,
     // a one-expert Qwen layer, run as a dense MLP), the DeepSeek shared
     // expert's are identity rows
     const bool routed = j < 2 && (deepseek || E > 1 || topk > 1);
-    const long cb = dec_deal_chunk(segN[j], ntw[j], segks[j], routed);
+    const long cb = dec_deal_chunk(segN[j], ntw[j], segks[j], routed, items[j]);
     out[10 + 3 * j] = items[j];
     out[11 + 3 * j] = cb;
     out[12 + 3 * j] = dec_launch_grid(items[j], cb);
@@ -1017,6 +1037,20 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     float* y = (float*)(ws + p.y);
     float* h_sh = sh ? (float*)(ws + p.hq_sh) : nullptr;
     float* y_sh = sh ? (float*)(ws + p.y_sh) : nullptr;
+    // shared expert (fp8, identity rows): the second segment of the routed
+    // launches (a mixed-format launch), or launches of its own (sh_sep)
+    SegDesc s1{};
+    s1.a = (const uint8_t*)a->x; s1.total_rows = T;
+    s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
+    s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
+    s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
+    s1.pstride = (long)T * Is;
+    SegDesc s2{};
+    s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
+    s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
+    s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
+    s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
+    const bool sh_in = sh && !p.sh_sep;
     SegDesc r1{};
     r1.a = (const uint8_t*)a->x; r1.sorted_idx = sorted; r1.gather = 1;
     r1.tile_info = tiles; r1.num_tiles = ntiles; r1.max_tiles = p.max_tiles;
@@ -1041,28 +1075,24 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           first_rc(
               [&] {
-                return launch_stream_dec(2, 0, r1, nullptr, k, L, p.up_items,
-                                         st, p.bm, nullptr,
-                                         perm_inl ? &ri : nullptr);
+                return launch_stream_dec(2, 0, r1, sh_in ? &s1 : nullptr, k,
+                                         L, p.up_items, st, p.bm, nullptr,
+                                         perm_inl ? &ri : nullptr, nullptr,
+                                         SF_FP8_F32S);
               },
               [&] {
-                return p.ks_up > 1 ? launch_split_finish(r1, nullptr, L, st)
-                                   : 0;
+                return p.ks_up > 1
+                           ? launch_split_finish(r1, sh_in ? &s1 : nullptr, L, st)
+                           : 0;
               }));
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
-          launch_stream_dec(2, 1, r2, nullptr, k, 0.f, p.dn_items, st, p.bm));
-    if (sh) {
-      SegDesc s1{};
-      s1.a = (const uint8_t*)a->x; s1.total_rows = T;
-      s1.wp = (const uint8_t*)a->s13_packed; s1.s0 = a->s1_s; s1.s1 = a->s3_s;
-      s1.N = Is; s1.K = H; s1.hq = (uint8_t*)h_sh;
-      s1.ksplit = p.ks_up_sh; s1.pp = (float*)(ws + p.gu_sh);
-      s1.pstride = (long)T * Is;
-      SegDesc s2{};
-      s2.a = (const uint8_t*)h_sh; s2.total_rows = T;
-      s2.wp = (const uint8_t*)a->s2_packed; s2.s0 = a->s2_s;
-      s2.N = H; s2.K = Is; s2.y = (uint16_t*)y_sh;
-      s2.ksplit = p.ks_dn_sh; s2.pstride = (long)T * H;
+          launch_stream_dec(2, 1, r2, sh_in ? &s2 : nullptr, k, 0.f,
+                            p.dn_items, st, p.bm, nullptr, nullptr, nullptr,
+                            SF_FP8_F32S));
+    if (!sh || sh_in) {
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
+      STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
+    } else {
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP,
             first_rc(
                 [&] {

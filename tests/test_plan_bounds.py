@@ -14,7 +14,8 @@ tests port the kernels' dealing exactly:
   workgroups; CB is one row tile's items of the first segment (column slabs,
   times K chunks in decode), an eighth of that (rounded up) in decode
   launches whose first segment has identity rows (the DeepSeek shared
-  expert, a one-expert layer).
+  expert, a one-expert layer), and in decode at most a 64th of the
+  launch's item bound.
 
 They take the library's own plans (sllm_moe_plan_query: tile rows, K
 splits, item bounds, deal chunks and grids) for decode batches of the
@@ -133,6 +134,11 @@ def test_stream_dec_grid_deals_at_most_32_items(ncu):
             assert worst <= ST_MAX_ITEMS, (upper, cb, grid, worst)
 
 
+def _chunk_cap(cb, upper):
+    """A deal chunk holds at most a 64th of the launch's items (at least 1)."""
+    return max(1, min(cb, upper // 64))
+
+
 def _plan(lib, ds, T, H, E, I, Is, k, mode=2, logits_given=0):
     out = (ctypes.c_long * PLAN_FIELDS)()
     rc = lib.sllm_moe_plan_query(ds, T, H, E, I, Is, k, mode, logits_given,
@@ -167,24 +173,31 @@ def test_decode_plans_deal_at_most_32_items(shape):
         bm, bm_sh, max_tiles = p[1], p[2], p[3]
         ks_up, ks_up_sh, ks_dn, ks_dn_sh = p[5], p[6], p[7], p[8]
         sh_rt = -(-T // bm_sh) if Is else 0
+        # a DeepSeek shared expert with taller tiles than the routed ones
+        # runs in launches of its own; otherwise it is the routed launches'
+        # second segment
+        sep = bool(ds and Is and bm_sh != bm)
         # per launch: (routed tiles -> items, shared items)
         launches = [
-            (I // 128 * ks_up, (0 if ds else sh_rt * (Is // 128) * ks_up_sh)),
-            (H // 256 * ks_dn, (0 if ds else sh_rt * (H // 256) * ks_dn_sh)),
+            (I // 128 * ks_up, (0 if sep else sh_rt * (Is // 128) * ks_up_sh)),
+            (H // 256 * ks_dn, (0 if sep else sh_rt * (H // 256) * ks_dn_sh)),
         ]
         for j, (per_tile, shared) in enumerate(launches):
             upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
             assert upper == max_tiles * per_tile + shared, (T, j)
             # identity rows (a one-expert layer): an eighth of a tile
-            want_cb = per_tile if (ds or E > 1 or k > 1) else max(1, -(-per_tile // 8))
-            assert cb == want_cb and grid % 8 == 0, (T, j)
+            want_cb = per_tile if (ds or E > 1 or k > 1) else -(-per_tile // 8)
+            assert cb == _chunk_cap(want_cb, upper) and grid % 8 == 0, (T, j)
             worst = max(_max_items(rt * per_tile + shared, grid, cb)
                         for rt in range(1, max_tiles + 1))
             assert worst <= ST_MAX_ITEMS, (T, j, upper, cb, grid, worst)
-        if ds and Is:
+        if not sep:
+            assert p[16] == p[19] == 0, T  # no launches of its own
+        else:
             for j, per_tile in ((2, Is // 128 * ks_up_sh), (3, H // 256 * ks_dn_sh)):
                 upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
-                assert upper == sh_rt * per_tile and cb == max(1, -(-per_tile // 8))
+                assert upper == sh_rt * per_tile
+                assert cb == _chunk_cap(-(-per_tile // 8), upper), (T, j)
                 assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS, (T, j)
 
 
@@ -193,7 +206,9 @@ def test_old_contiguous_sizing_would_overflow():
     eighth of the items (sllm_moe_stream_grid) deals 37 items to a
     workgroup of the H 4096, E 128, top-8, I 1536 layer at 6 tokens, and
     36 to the H 3584, E 64, I 2560, Is 20480 layer at 7 tokens; the
-    chunk-aware grid the library now launches keeps them at 32."""
+    chunk-aware grid the library now launches keeps them at 32. (The old
+    deal's chunks were whole row tiles; the library's are now capped at a
+    64th of the items.)"""
     lib = _need_lib()
     for (ds, H, E, k, I, Is), T, old_worst in (
             ((0, 4096, 128, 8, 1536, 1536), 6, 37),
@@ -202,8 +217,9 @@ def test_old_contiguous_sizing_would_overflow():
         bad = None
         for j in (0, 1):
             upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
+            tile_cb = (I // 128 * p[5], H // 256 * p[7])[j]
             old = lib.sllm_moe_stream_grid(upper, p[9])
-            w_old = _max_items(upper, old, cb)
+            w_old = _max_items(upper, old, tile_cb)
             if w_old > ST_MAX_ITEMS:
                 bad = w_old
             assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS
