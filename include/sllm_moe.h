@@ -248,7 +248,8 @@ long sllm_moe_stream_dec_grid(long upper_items, int num_cus, long chunk);
  * #CUs used for planning; then, decode only, for the streamed launches
  * j = 0 gate/up, 1 down (Qwen: routed + shared segment), 2 and 3 the
  * DeepSeek shared expert's gate/up and down: out[10 + 3j] the launch's
- * item bound, out[11 + 3j] its XCD deal chunk, out[12 + 3j] its grid
+ * item bound, out[11 + 3j] its XCD deal chunk (0: a stream-K deal, each
+ * workgroup an equal range of the units' K steps), out[12 + 3j] its grid
  * (0 where a launch does not run). n_out >= SLLM_MOE_PLAN_FIELDS. */
 #define SLLM_MOE_PLAN_FIELDS 22
 int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,

@@ -792,7 +792,7 @@ __device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, long off) {
 template <int BM>
 __device__ __forceinline__ void dec_fused_finish(
     const SegDesc& S0, const SegDesc& S1, float limit, const DecFuse& F,
-    const int4* desc, int nitems, int* jobs, int& njob) {
+    const int4* desc, const int4* kr, int nitems, int* jobs, int& njob) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores done
   if (tid == 0) njob = 0;
@@ -814,8 +814,10 @@ __device__ __forceinline__ void dec_fused_finish(
     // device-scope (sc1) loads that miss any stale L2 copy. An acq_rel
     // count (a whole-L2 write-back before it and an L2 invalidate after)
     // gives the same bits and cost B=1 / 2 / 4 layers 2 / 7 / 7.5 us.
-    if (__hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT) == S.ksplit - 1)
+    // (a stream-K unit's first item also arrives for its zero slices)
+    const int inc = 1 + kr[i].z;
+    if (__hip_atomic_fetch_add(c, inc, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) == S.ksplit - inc)
       jobs[atomicAdd(&njob, 1)] = i;
   }
   __syncthreads();
@@ -868,8 +870,8 @@ constexpr int DC_BATCH = 8;  // combine_f32_kernel's batch of slice loads
 template <int BM>
 __device__ __forceinline__ void dec_fused_combine(
     const SegDesc& S0, const SegDesc& S1, const DecCombine& C,
-    const int4* desc, int nitems, int* jobs, int& njob, int (*pos)[64],
-    float4 (*part)[4][64]) {
+    const int4* desc, const int4* kr, int nitems, int* jobs, int& njob,
+    int (*pos)[64], float4 (*part)[4][64]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nslab = C.H / 256;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores done
@@ -885,9 +887,11 @@ __device__ __forceinline__ void dec_fused_combine(
     int kept = 0;
     for (int j = 0; j < C.topk; ++j) kept += C.inv[t * C.topk + j] >= 0;
     const int want = kept * C.ks + (C.y_sh ? C.ks_sh : 0);
-    // relaxed device-scope count: see dec_fused_finish
-    if (__hip_atomic_fetch_add(C.cnt + t * nslab + nt, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT) == want - 1)
+    // relaxed device-scope count: see dec_fused_finish (a stream-K unit's
+    // first item also arrives for its zero slices)
+    const int inc = 1 + kr[i].z;
+    if (__hip_atomic_fetch_add(C.cnt + t * nslab + nt, inc, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) == want - inc)
       jobs[atomicAdd(&njob, 1)] = t * nslab + nt;
   }
   __syncthreads();
@@ -950,7 +954,7 @@ __device__ __forceinline__ void dec_fused_combine(
 template <int BF, int MODE, bool WNT, int BM, int BF1 = BF>
 __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     SegDesc S0, SegDesc S1, int nseg, int topk, float limit, DecFuse F,
-    RouteInline RI, DecCombine C, int CB) {
+    RouteInline RI, DecCombine C, int CB, int SK) {
   constexpr int RB = BM / 16;
   // BF1 != BF: the first segment's weights are MXFP4 and the second's FP8
   // with fp32 block scales (a DeepSeek layer's routed and shared experts in
@@ -961,6 +965,10 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   __shared__ int mix_nf4;  // mixed: the workgroup's MXFP4 items
   static_assert(BM == 16 || BM == 32, "decode tiles are 16 or 32 rows");
   __shared__ int4 desc[ST_MAX_ITEMS];
+  // per item: first K step, K steps, zero slices to write (the first item
+  // of a stream-K unit that fewer than ks ranges reach), 0
+  __shared__ int4 kr[ST_MAX_ITEMS];
+  __shared__ int sk_n;  // stream-K: the workgroup's items
   __shared__ int rsrc[ST_MAX_ITEMS][BM];
   __shared__ float rwl[ST_MAX_ITEMS][BM];
   __shared__ __attribute__((aligned(16))) uint16_t a_hi[2][BM * SD_LS];
@@ -1020,39 +1028,24 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   const int* tiles0 = inl ? ri_tiles : S0.tile_info;
   const int* sorted0 = inl ? ri_sorted : S0.sorted_idx;
 
-  auto seg_items_dec = [&](const SegDesc& S, bool own) {
+  // Units: a row tile's column slab of a segment (routed units first, then
+  // the shared expert's). Items: K steps [kb0, kb0 + nkb) of a unit, whose
+  // partial sums go to K slice `slot` (desc.x bits 16-30; kr).
+  auto seg_units = [&](const SegDesc& S, bool own) {
     const int rt = own ? ri_sh[ST_WAVES]
                  : S.tile_info ? *S.num_tiles : (S.total_rows + BM - 1) / BM;
-    return rt * (S.N / NTW) * S.ksplit;
+    return rt * (S.N / NTW);
   };
-  const int n0 = seg_items_dec(S0, inl);
-  const int n1 = nseg > 1 ? seg_items_dec(S1, false) : 0;
-  const int total = n0 + n1;
+  const int nu0 = seg_units(S0, inl);
+  const int nu1 = nseg > 1 ? seg_units(S1, false) : 0;
   const int nx = gridDim.x / 8;
   const int xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
-  // XCD x takes chunks x, x + 8, ... of CB items (a row tile's items, its
-  // column slabs and K chunks, at most: dec_deal_chunk), so that every XCD
-  // gets the same mix of routed and shared-expert items (as in the prefill
-  // kernel; C3 B=32 163.1 / 164.2 -> 161.6 / 160.6 us, B=1 and B=8
-  // unchanged) (the host sizes the grid for this deal: stream_dec_grid)
-  const int ncf = total / CB, crem = total % CB;
-  const int xcount = (ncf > xcd ? (ncf - xcd + 7) / 8 : 0) * CB + (ncf % 8 == xcd ? crem : 0);
-  const int nitems = xcount > jx ? (xcount - jx + nx - 1) / nx : 0;
-  if (nitems > ST_MAX_ITEMS) {  // host sizes the grid: a sizing error
-    if (tid == 0) stream_item_overflow = 1;
-    return;
-  }
-  if (nitems == 0) return;
-
-  if (tid < nitems) {
-    const int qx = jx + tid * nx;  // the XCD's qx-th item
-    const int it = (xcd + 8 * (qx / CB)) * CB + qx % CB;
-    const int seg = it >= n0;
+  // item idx := unit li of segment seg, K steps [kb0, kb0 + nkb), slice slot
+  auto make_item = [&](int idx, int seg, int li, int kb0, int nkb, int slot,
+                       int fill) {
     const SegDesc& S = seg ? S1 : S0;
-    const int li = seg ? it - n0 : it;
     const int ntn = S.N / NTW;
-    const int q = li / S.ksplit, kc = li % S.ksplit;
-    const int rt = q / ntn, nt = q % ntn;
+    const int rt = li / ntn, nt = li % ntn;
     int e = 0, rb, rows;
     const int* ti = seg ? S.tile_info : tiles0;
     if (ti) {
@@ -1064,18 +1057,102 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       rb = rt * BM;
       rows = min(BM, S.total_rows - rb);
     }
-    int slot = tid;
-    if constexpr (MIX) {  // MXFP4 (first-segment) items first, in deal order
-      static_assert(ST_MAX_ITEMS <= 64, "a workgroup's items are one wave's lanes");
-      const uint64_t fp8 = __ballot(seg);  // lanes tid < nitems <= 32 of wave 0
-      const int nf8_below = __popcll(fp8 & ((1ull << tid) - 1));
-      const int nf4 = nitems - __popcll(fp8);
-      slot = seg ? nf4 + nf8_below : tid - nf8_below;
-      if (tid == 0) mix_nf4 = nf4;
+    // x: segment (bit 0), column slab (bits 1-15), K slice (bits 16-30)
+    desc[idx] = make_int4(seg | (nt << 1) | (slot << 16), e, rb, rows);
+    kr[idx] = make_int4(kb0, nkb, fill, 0);
+  };
+  int nitems;
+  if (SK) {
+    // stream-K: this workgroup's range of the units' cost line (sk_lreq);
+    // the ranges of an XCD are adjacent, so that a tile's units meet in
+    // its L2. The MXFP4 units come first on the line: so do their items.
+    constexpr int W1 = MIX ? 2 : 1;
+    const int KB0 = S0.K / 128, KB1 = nseg > 1 ? S1.K / 128 : 1;
+    const long c0 = KB0, c1 = (long)KB1 * W1, cs = (long)nu0 * c0;
+    const long C = cs + (long)nu1 * c1;
+    long lreq = sk_lreq(KB0, 1, S0.ksplit);
+    if (nseg > 1) lreq = max(lreq, sk_lreq(KB1, W1, S1.ksplit));
+    const long G = sk_ranges(C, lreq, gridDim.x);
+    const long r = (long)xcd * nx + jx;
+    if (C == 0 || r >= G) return;
+    const long a = r * C / G, b = (r + 1) * C / G;
+    auto unit_of = [&](long c) { return c < cs ? c / c0 : nu0 + (c - cs) / c1; };
+    const long ua = unit_of(a), ncand = unit_of(b - 1) - ua + 1;
+    if (ncand > 64) {  // more units than a wave's lanes: a sizing error
+      if (tid == 0) stream_item_overflow = 1;
+      return;
     }
-    // x: segment (bit 0), column slab (bits 1-15), K chunk (bits 16-30)
-    desc[slot] = make_int4(seg | (nt << 1) | (kc << 16), e, rb, rows);
+    if (wave == 0) {
+      bool live = false;
+      int seg = 0, li = 0, kb0 = 0, nkb = 0, slot = 0, fill = 0;
+      if (lane < ncand) {
+        const long u = ua + lane;
+        seg = u >= nu0;
+        li = (int)(seg ? u - nu0 : u);
+        const int KB = seg ? KB1 : KB0, w = seg ? W1 : 1;
+        const int ks = seg ? S1.ksplit : S0.ksplit;
+        const long cu = seg ? cs + (long)li * c1 : (long)li * c0;
+        // the unit's steps whose start cu + j w lies in [a, b)
+        const long jlo = a <= cu ? 0 : (a - cu + w - 1) / w;
+        const long jhi = min((long)KB, (b - cu + w - 1) / w);
+        live = jlo < jhi;
+        // range of a cost position: the r with r C / G <= c < (r + 1) C / G
+        auto range_of = [&](long c) { return ((c + 1) * G - 1) / C; };
+        const long rfirst = range_of(cu);
+        const int nsl = (int)(range_of(cu + (long)(KB - 1) * w) - rfirst + 1);
+        slot = (int)(r - rfirst);
+        fill = slot == 0 ? ks - nsl : 0;
+        kb0 = (int)jlo;
+        nkb = (int)(jhi - jlo);
+      }
+      const uint64_t lm = __ballot(live);
+      const int idx = __popcll(lm & ((1ull << lane) - 1));
+      if (live && idx < ST_MAX_ITEMS) make_item(idx, seg, li, kb0, nkb, slot, fill);
+      const uint64_t f8 = __ballot(live && seg);
+      if (lane == 0) {
+        sk_n = __popcll(lm);
+        if constexpr (MIX) mix_nf4 = __popcll(lm) - __popcll(f8);
+      }
+    }
+    __syncthreads();
+    nitems = sk_n;
+  } else {
+    // XCD x takes chunks x, x + 8, ... of CB items (a row tile's items, its
+    // column slabs and K chunks, at most: dec_deal_chunk), so that every
+    // XCD gets the same mix of routed and shared-expert items (as in the
+    // prefill kernel; C3 B=32 163.1 / 164.2 -> 161.6 / 160.6 us, B=1 and
+    // B=8 unchanged) (the host sizes the grid for this deal: stream_dec_grid)
+    const int n0 = nu0 * S0.ksplit;
+    const int total = n0 + nu1 * (nseg > 1 ? S1.ksplit : 1);
+    const int ncf = total / CB, crem = total % CB;
+    const int xcount = (ncf > xcd ? (ncf - xcd + 7) / 8 : 0) * CB + (ncf % 8 == xcd ? crem : 0);
+    nitems = xcount > jx ? (xcount - jx + nx - 1) / nx : 0;
+    if (nitems <= ST_MAX_ITEMS && tid < nitems) {
+      const int qx = jx + tid * nx;  // the XCD's qx-th item
+      const int it = (xcd + 8 * (qx / CB)) * CB + qx % CB;
+      const int seg = it >= n0;
+      const SegDesc& S = seg ? S1 : S0;
+      const int li = seg ? it - n0 : it;
+      const int kc = li % S.ksplit, KB = S.K / 128;
+      const int kb0 = kc * KB / S.ksplit;
+      int idx = tid;
+      if constexpr (MIX) {  // MXFP4 (first-segment) items first, in deal order
+        static_assert(ST_MAX_ITEMS <= 64, "a workgroup's items are one wave's lanes");
+        const uint64_t fp8 = __ballot(seg);  // lanes tid < nitems <= 32 of wave 0
+        const int nf8_below = __popcll(fp8 & ((1ull << tid) - 1));
+        const int nf4 = nitems - __popcll(fp8);
+        idx = seg ? nf4 + nf8_below : tid - nf8_below;
+        if (tid == 0) mix_nf4 = nf4;
+      }
+      make_item(idx, seg, li / S.ksplit, kb0, (kc + 1) * KB / S.ksplit - kb0, kc, 0);
+    }
   }
+  if (nitems > ST_MAX_ITEMS) {  // host sizes the grid: a sizing error
+    if (tid == 0) stream_item_overflow = 1;
+    return;
+  }
+  if (nitems == 0) return;
+
   __syncthreads();
   for (int q = tid; q < nitems * BM; q += ST_THREADS) {
     const int i = q / BM, r = q % BM;
@@ -1094,13 +1171,10 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   }
   __syncthreads();
 
-  // K steps [kb0, kb0 + nkb) of item i: chunk kc of ksplit near-equal parts
+  // K steps [kb0, kb0 + nkb) of item i
   auto kchunk = [&](int i, int& kb0, int& nkb) {
-    const int x = desc[i].x;
-    const SegDesc& S = (x & 1) ? S1 : S0;
-    const int KB = S.K / 128, kc = x >> 16;
-    kb0 = kc * KB / S.ksplit;
-    nkb = (kc + 1) * KB / S.ksplit - kb0;
+    kb0 = kr[i].x;
+    nkb = kr[i].y;
   };
 
   // activation tile of a K step: BM rows x 128 values; thread tid takes
@@ -1125,10 +1199,12 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
 
   // acc[r][s][v]: row 16 r + lc of the tile, output column 4 lg + v of
   // subtile s
+  // (slices [ks - fill, ks) of a stream-K unit no range reached: zeros)
   auto epilogue = [&](int i) {
     const int4 d = desc[i];
     const int seg = d.x & 1, nt = (d.x >> 1) & 0x7FFF, kc = d.x >> 16;
     const SegDesc& S = seg ? S1 : S0;
+    const int fill = kr[i].z;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const int row = 16 * r + lc;
@@ -1140,14 +1216,24 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
                           nt * 128 + wave * 16 + lg * 4;
           float* pg = S.pp + og;
           float* pu = pg + S.ksplit * S.pstride;
+          const long o0 = og - kc * S.pstride;  // slice 0
           if (F.cnt) {
             const __amdgpu_buffer_rsrc_t rp = dev_rsrc(S.pp);
             st_dev4(rp, og, acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
             st_dev4(rp, og + S.ksplit * S.pstride, acc[r][1][0], acc[r][1][1],
                     acc[r][1][2], acc[r][1][3]);
+            for (int z = S.ksplit - fill; z < S.ksplit; ++z) {
+              st_dev4(rp, o0 + z * S.pstride, 0.f, 0.f, 0.f, 0.f);
+              st_dev4(rp, o0 + (S.ksplit + z) * S.pstride, 0.f, 0.f, 0.f, 0.f);
+            }
           } else {
             *(float4*)pg = make_float4(acc[r][0][0], acc[r][0][1], acc[r][0][2], acc[r][0][3]);
             *(float4*)pu = make_float4(acc[r][1][0], acc[r][1][1], acc[r][1][2], acc[r][1][3]);
+            for (int z = S.ksplit - fill; z < S.ksplit; ++z) {
+              *(float4*)(S.pp + o0 + z * S.pstride) = make_float4(0.f, 0.f, 0.f, 0.f);
+              *(float4*)(S.pp + o0 + (S.ksplit + z) * S.pstride) =
+                  make_float4(0.f, 0.f, 0.f, 0.f);
+            }
           }
           continue;
         }
@@ -1166,15 +1252,22 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       } else {
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
-          const long o = kc * S.pstride + (long)(d.z + row) * S.N + nt * 256 +
-                         wave * 32 + sb * 16 + lg * 4;
-          if (C.cnt)  // read by the fused combine's finisher: device scope
-            st_dev4(dev_rsrc((const float*)S.y), o, acc[r][sb][0] * rw,
-                    acc[r][sb][1] * rw, acc[r][sb][2] * rw, acc[r][sb][3] * rw);
-          else
+          const long o0 = (long)(d.z + row) * S.N + nt * 256 + wave * 32 +
+                          sb * 16 + lg * 4;
+          const long o = kc * S.pstride + o0;
+          if (C.cnt) {  // read by the fused combine's finisher: device scope
+            const __amdgpu_buffer_rsrc_t ry = dev_rsrc((const float*)S.y);
+            st_dev4(ry, o, acc[r][sb][0] * rw, acc[r][sb][1] * rw,
+                    acc[r][sb][2] * rw, acc[r][sb][3] * rw);
+            for (int z = S.ksplit - fill; z < S.ksplit; ++z)
+              st_dev4(ry, o0 + z * S.pstride, 0.f, 0.f, 0.f, 0.f);
+          } else {
             *(float4*)((float*)S.y + o) =
                 make_float4(acc[r][sb][0] * rw, acc[r][sb][1] * rw,
                             acc[r][sb][2] * rw, acc[r][sb][3] * rw);
+            for (int z = S.ksplit - fill; z < S.ksplit; ++z)
+              *(float4*)((float*)S.y + o0 + z * S.pstride) = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
         }
       }
     }
@@ -1377,7 +1470,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     if (F.cnt) {
       __shared__ int jobs[ST_MAX_ITEMS];
       __shared__ int njob;
-      dec_fused_finish<BM>(S0, S1, limit, F, desc, nitems, jobs, njob);
+      dec_fused_finish<BM>(S0, S1, limit, F, desc, kr, nitems, jobs, njob);
     }
   } else {
     if (C.cnt) {
@@ -1385,7 +1478,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       __shared__ int ncj;
       __shared__ int cpos[2][64];
       __shared__ float4 cpart[2][4][64];
-      dec_fused_combine<BM>(S0, S1, C, desc, nitems, cjobs, ncj, cpos, cpart);
+      dec_fused_combine<BM>(S0, S1, C, desc, kr, nitems, cjobs, ncj, cpos, cpart);
     }
   }
 }
@@ -1520,6 +1613,58 @@ int dec_ksplit(long upper_items, int KB) {
   return dec_best_split(upper_items, KB, std::min(KB, DEC_MAX_KSPLIT), 0, 0.2);
 }
 
+// Stream-K launches. Items a workgroup can receive: a range of length L
+// (at most ceil(C / grid), or under 2 lreq where the ranges are made
+// longer) meets at most ceil(L / cmin) + 1 units.
+static long sk_items_bound(long cbound, long grid, long cmin, long lreq) {
+  const long l = std::max((cbound + grid - 1) / grid, 2 * lreq);
+  return (l + cmin - 1) / cmin + 1;
+}
+
+// The grid of a stream-K launch over a cost line of at most cbound: the
+// device's CUs (a multiple of 8), grown until no workgroup can receive
+// more than ST_MAX_ITEMS items; 0 when the ranges' least length alone
+// exceeds that.
+static long sk_grid(long cbound, long cmin, long lreq) {
+  if (sk_items_bound(0, 1, cmin, lreq) > ST_MAX_ITEMS) return 0;
+  long grid = 8L * ((num_cus() + 7) / 8);
+  while (sk_items_bound(cbound, grid, cmin, lreq) > ST_MAX_ITEMS) grid += 8;
+  return grid;
+}
+
+long dec_sk_launch_grid(int nseg, const long* units, const int* KB,
+                        const int* w, const int* ks) {
+  long cbound = 0, cmin = 0, lreq = 1;
+  for (int i = 0; i < nseg; ++i) {
+    if (ks[i] < 2 || ks[i] > KB[i]) return 0;
+    const long cu = (long)KB[i] * w[i];
+    cbound += units[i] * cu;
+    cmin = i ? std::min(cmin, cu) : cu;
+    lreq = std::max(lreq, sk_lreq(KB[i], w[i], ks[i]));
+  }
+  return sk_grid(cbound, cmin, lreq);
+}
+
+bool dec_sk_plan(int nseg, const long* units, const int* KB, const int* w,
+                 int cap, int* ks) {
+  long cbound = 0, cmin = 0, lreq = 1;
+  for (int i = 0; i < nseg; ++i) cbound += units[i] * KB[i] * w[i];
+  if (cbound <= 0) return false;
+  // a range of the expected length (the tile bound overstates the routed
+  // tiles: 5/8 of it) spans each unit in ks_i slices
+  const long G0 = 8L * ((num_cus() + 7) / 8);
+  const long lest = std::max(1L, cbound * 5 / (8 * G0));
+  for (int i = 0; i < nseg; ++i) {
+    const long need = ((long)(KB[i] - 1) * w[i] + lest - 1) / lest + 1;
+    ks[i] = (int)std::max(2L, std::min((long)std::min(cap, KB[i]), need));
+    if (ks[i] < 2) return false;  // one K step: nothing to split
+    const long cu = (long)KB[i] * w[i];
+    cmin = i ? std::min(cmin, cu) : cu;
+    lreq = std::max(lreq, sk_lreq(KB[i], w[i], ks[i]));
+  }
+  return sk_grid(cbound, cmin, lreq) > 0;
+}
+
 
 // Host bound of a launch's item count: per segment, (row tiles: the tile
 // table's bound, or ceil(total_rows / bm) for identity rows) x column slabs
@@ -1612,18 +1757,38 @@ template <int BF, int MODE, int BM, int BF1 = BF>
 static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                          float limit, long upper_items, hipStream_t st,
                          const DecFuse& fuse, const RouteInline& route,
-                         const DecCombine& comb) {
+                         const DecCombine& comb, bool sk) {
+  constexpr int NTW = MODE == 0 ? 128 : 256;
   {
-    const int rc = check_item_bound(s0, s1, MODE == 0 ? 128 : 256, BM,
-                                    upper_items, "stream decode gemm");
+    const int rc = check_item_bound(s0, s1, NTW, BM, upper_items,
+                                    "stream decode gemm");
     if (rc) return rc;
   }
-  // the kernel deals its items to the XCDs in chunks of (at most) one row
-  // tile's items of the first segment (column slabs x K chunks)
-  const long cb = dec_deal_chunk(s0, MODE == 0 ? 128 : 256, upper_items);
-  const long grid = dec_launch_grid(upper_items, cb);
-  SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
-  {
+  long cb = 1, grid;
+  if (sk) {
+    // stream-K: the cost line's bound from the segments' row-tile bounds
+    long un[2];
+    int kb[2], w[2], ks[2];
+    for (int i = 0; i < (s1 ? 2 : 1); ++i) {
+      const SegDesc& s = i ? *s1 : s0;
+      const long rt = s.tile_info ? s.max_tiles : (s.total_rows + BM - 1) / BM;
+      SLLM_REQUIRE(s.ksplit >= 2 && s.ksplit <= s.K / 128,
+                   "stream decode gemm: stream-K needs 2..K/128 slices (%d)",
+                   s.ksplit);
+      un[i] = rt * (s.N / NTW);
+      kb[i] = s.K / 128;
+      w[i] = i && BF1 != BF ? 2 : 1;
+      ks[i] = s.ksplit;
+    }
+    grid = dec_sk_launch_grid(s1 ? 2 : 1, un, kb, w, ks);
+    SLLM_CAPACITY(grid > 0,
+                  "stream decode gemm: stream-K ranges cannot keep %d items "
+                  "per workgroup", ST_MAX_ITEMS);
+  } else {
+    // the kernel deals its items to the XCDs in chunks of (at most) one row
+    // tile's items of the first segment (column slabs x K chunks)
+    cb = dec_deal_chunk(s0, NTW, upper_items);
+    grid = dec_launch_grid(upper_items, cb);
     const long nx = grid / 8;
     const long worst = (chunked_xcd_share(upper_items, cb) + nx - 1) / nx;
     SLLM_CAPACITY(worst <= ST_MAX_ITEMS,
@@ -1631,10 +1796,11 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
                   "(upper_items %ld, chunk %ld, grid %ld)", worst,
                   ST_MAX_ITEMS, upper_items, cb, grid);
   }
+  SLLM_REQUIRE(grid < (1L << 31), "stream decode gemm: grid too large");
   SegDesc dummy = s0;
   moe_stream_dec_kernel<BF, MODE, true, BM, BF1><<<(unsigned)grid, ST_THREADS, 0, st>>>(
       s0, s1 ? *s1 : dummy, s1 ? 2 : 1, topk, limit, fuse, route, comb,
-      (int)cb);
+      (int)cb, sk ? 1 : 0);
   SLLM_LAUNCHED();
   return 0;
 }
@@ -1643,7 +1809,7 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                       const SegDesc* s1_in, int topk, float limit,
                       long upper_items, hipStream_t st, int bm,
                       const DecFuse* fuse_in, const RouteInline* route_in,
-                      const DecCombine* comb_in, int bf1) {
+                      const DecCombine* comb_in, int bf1, bool sk) {
   if (bf1 < 0 || !s1_in) bf1 = bf;
   SLLM_REQUIRE(bf >= 0 && bf <= 2 && (mode == 0 || mode == 1) &&
                    (bm == 16 || bm == 32) &&
@@ -1731,8 +1897,8 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
   }
   // fp32 scale arithmetic covers power-of-two fp8 scales (bf 1)
 #define GO(B, M, B1)                                                     \
-  return bm == 32 ? go_stream_dec<B, M, 32, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb) \
-                  : go_stream_dec<B, M, 16, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb)
+  return bm == 32 ? go_stream_dec<B, M, 32, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb, sk) \
+                  : go_stream_dec<B, M, 16, B1>(s0, s1, topk, limit, upper_items, st, fuse, route, comb, sk)
   if (mode == 0) {
     if (bf == SF_FP4 && bf1 != SF_FP4) GO(SF_FP4, 0, SF_FP8_F32S);
     if (bf == SF_FP4) GO(SF_FP4, 0, SF_FP4);

@@ -253,6 +253,27 @@ inline int dec_deal_chunk(const SegDesc& s, int ntw, long upper_items) {
   return dec_deal_chunk(s.N, ntw, s.ksplit, s.tile_info != nullptr,
                         upper_items);
 }
+// Stream-K deal of a decode launch (sk): its units (a row tile's column
+// slab of a segment, routed units first) lie end to end on a line of cost
+// (a unit costs its K steps times its weight w: 1, and 2 for the fp8
+// segment of a mixed-format launch, whose steps stream twice the bytes);
+// G equal ranges of that line go one to a workgroup, which takes the K
+// steps whose start lies in its range (a unit's steps across two ranges are
+// two items). An item's partial sums go to K slice (its range) - (the
+// range of its unit's first step), of ks slices per unit; the unit's
+// first item also writes zeros to the slices no range reached and counts
+// them as arrivals, so that every unit holds ks slices, as a K-split unit
+// does. Ranges are at least sk_lreq long, which keeps a unit within ks of
+// them (and no range without a step of a unit it spans).
+__host__ __device__ inline long sk_lreq(int KB, int w, int ks) {
+  const long l = ((long)(KB - 1) * w + ks - 2) / (ks - 1);
+  return l > w ? l : w;
+}
+// ranges over a line of cost C with grid workgroups
+__host__ __device__ inline long sk_ranges(long C, long lreq, long grid) {
+  const long g = C / lreq;
+  return g < 1 ? 1 : (g < grid ? g : grid);
+}
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                   int topk, float limit, int pow2, long upper_items,
                   hipStream_t st);
@@ -353,7 +374,18 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
                       hipStream_t st, int bm = 16,
                       const DecFuse* fuse = nullptr,
                       const RouteInline* route = nullptr,
-                      const DecCombine* comb = nullptr, int bf1 = -1);
+                      const DecCombine* comb = nullptr, int bf1 = -1,
+                      bool sk = false);
+// Stream-K plan of a decode launch of nseg segments with units[i] units
+// (row-tile bound x column slabs) of KB[i] K steps of weight w[i] (sk_lreq):
+// K slices ks[i] (2..cap) that keep a unit within ks[i] ranges of the
+// expected length; false when the deal cannot hold a workgroup's items.
+bool dec_sk_plan(int nseg, const long* units, const int* KB, const int* w,
+                 int cap, int* ks);
+// The persistent grid of such a launch with ks[i] slices (0: the deal
+// cannot hold a workgroup's items).
+long dec_sk_launch_grid(int nseg, const long* units, const int* KB,
+                        const int* w, const int* ks);
 // Counter ints of a fused gate/up launch: N routed rows, T shared rows.
 inline long dec_fuse_counters(long N, long T, int I, int Is) {
   return N * (I / 128) + T * (Is / 128);

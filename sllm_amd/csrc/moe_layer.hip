@@ -43,6 +43,9 @@ struct Plan {
   // it in launches of its own, the *_sh ones)
   long up_items, dn_items, up_sh_items, dn_sh_items;
   bool sh_sep;
+  // decode, streamed kernels: stream-K deal (dec_sk_plan) of the gate/up
+  // and down launches
+  bool sk_up, sk_dn;
   size_t fcnt;  // decode (Qwen, T <= DEC_FUSE_MAX_T): fused finish counters,
                 // then the fused combine's (fcnt_on)
   bool fcnt_on;
@@ -62,6 +65,7 @@ static int weights_reused(long rows, long experts, int bm) {
 
 static int dense8_mode();
 static bool route_inline_on();
+static bool streamk_on();
 static int device_cus();
 
 static size_t take(size_t& cur, size_t bytes) {
@@ -158,6 +162,36 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
             dec_ksplit(rt * (H / 256) + sh_rt * (H / 256),
                        (has_shared ? std::min(I, Is) : I) / 128);
       }
+      // Stream-K deal (a workgroup takes an equal range of K steps across
+      // the launch's units) for the DeepSeek mixed-format launches (up to 16
+      // tokens): whole items there leave a last round of a few workgroups
+      // (C4 B=8 gate/up: 1040 items, the fifth round 16 items of 56 steps).
+      // C4 B=1 / 2 / 4 / 8 / 16: 84.5 / 111.4 / 173.8 / 269.4 / 445.4 ->
+      // 79.4 / 109.4 / 166.2 / 248.7 / 427.5 us. Elsewhere whole items stay:
+      // the Qwen launches stream at the HBM rate with a fuller last round,
+      // and a stream-K deal of them ran 10-25% slower per K step (C3 B=32
+      // gate/up 89.5 -> 104.8 us, down 50.5 -> 57.2; workgroups' ranges
+      // placed XCD-adjacent or in block order, items rotated, or units
+      // permuted on the line: no better), as did the DeepSeek launches at
+      // 32 and 64 tokens (651 -> 700, 898 -> 978 us).
+      if (streamk_on() && deepseek && has_shared && !p.sh_sep) {
+        long un[2] = {rt * (I / 128), sh_rt * (Is / 128)};
+        int kb[2] = {H / 128, H / 128}, w[2] = {1, 2}, ks[2] = {1, 1};
+        if (dec_sk_plan(2, un, kb, w, 8, ks)) {
+          p.sk_up = true;
+          p.ks_up = ks[0];
+          p.ks_up_sh = ks[1];
+        }
+        un[0] = rt * (H / 256);
+        un[1] = sh_rt * (H / 256);
+        kb[0] = I / 128;
+        kb[1] = Is / 128;
+        if (dec_sk_plan(2, un, kb, w, 32, ks)) {
+          p.sk_dn = true;
+          p.ks_dn = ks[0];
+          p.ks_dn_sh = ks[1];
+        }
+      }
       p.up_items = rt * (I / 128) * p.ks_up;
       p.dn_items = rt * (H / 256) * p.ks_dn;
       const long sh_up = sh_rt * (Is / 128) * p.ks_up_sh;
@@ -177,7 +211,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.gu = p.ks_up > 1 ? take(c, (size_t)2 * p.ks_up * p.N * I * 4) : 0;
     p.gu_sh = has_shared && p.ks_up_sh > 1
                   ? take(c, (size_t)2 * p.ks_up_sh * T * Is * 4) : 0;
-    if (!deepseek && !force_gemv && T <= DEC_FUSE_MAX_T) {
+    if (!deepseek && !force_gemv && (T <= DEC_FUSE_MAX_T || p.sk_up)) {
       p.fcnt_on = true;
       p.fcnt = take(c, (size_t)(dec_fuse_counters(p.N, T, I, has_shared ? Is : 0) +
                                 dec_combine_counters(T, H)) * 4);
@@ -359,13 +393,16 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   // permutation launch clears, which saves the finish launch (B=1: 44 ->
   // 42 us); with the routing in the gate/up launch the router launch
   // clears them. From 5 tokens on the finish launch is as fast or faster
-  // (B=8: 76.5 vs 76.9 us with the fused finish).
+  // (B=8: 76.5 vs 76.9 us with the fused finish). A stream-K gate/up
+  // launch (every unit in K slices) finishes in the launch at any decode
+  // batch whose router launch clears the counters.
+  const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool fused = p.decode && a->wgu_packed && !one_expert && !bf16w &&
-                     T <= DEC_FUSE_MAX_T && (p.ks_up > 1 || p.ks_up_sh > 1);
+                     p.fcnt_on && (p.ks_up > 1 || p.ks_up_sh > 1) &&
+                     (T <= DEC_FUSE_MAX_T || (p.sk_up && small_router));
   int* fcnt = fused ? (int*)(ws + p.fcnt) : nullptr;
   const long nfcnt = fused ? dec_fuse_counters(p.N, T, I, sh ? Is : 0) : 0;
   SLLM_REQUIRE(nfcnt < (1L << 31), "sllm_moe_qwen_forward: too many counters");
-  const bool small_router = p.decode && !a->logits_given && T <= 64;
   const bool small_route = p.decode && route_permute_small_fits(T, E, k);
   // Streamed decode of a routed layer: the gate/up launch builds the
   // permutation in every workgroup (the tables written out by workgroup 0)
@@ -382,7 +419,11 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                       route_inline_on();
   const bool route_inl = inl_ok && small_router && T <= RI_MAX_ROUTE_T &&
                          (!a->logits_out || p.ks_r == 1);
-  const bool perm_inl = inl_ok && !route_inl && !small_route && !fused;
+  // the router launch clears the fused finish's and fused combine's
+  // counters when it runs; else the permutation launch clears the finish's
+  const bool router_clears = small_router && p.fcnt_on && (fused || route_inl);
+  const bool perm_inl = inl_ok && !route_inl && !small_route &&
+                        (!fused || router_clears);
   // One token: the down launch also does the combine (DecCombine: a
   // counter per 256-column slab), which leaves three launches (router,
   // gate/up, down; B=1 39.2 -> 39.0 us). From two tokens on the units'
@@ -394,7 +435,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
   int* ccnt = comb_inl ? (int*)(ws + p.fcnt) + dec_fuse_counters(p.N, T, I, sh ? Is : 0)
                        : nullptr;
   // the counters the router launch clears (both sets, whichever run)
-  int* rzero = route_inl && p.fcnt_on ? (int*)(ws + p.fcnt) : nullptr;
+  int* rzero = router_clears ? (int*)(ws + p.fcnt) : nullptr;
   const long nrzero = rzero ? dec_fuse_counters(p.N, T, I, sh ? Is : 0) + nccnt : 0;
   // Prefill: the softmax routing launch also quantizes each token's row
   // (and forms the shared-expert gate), in place of the activation-quant
@@ -468,7 +509,8 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
           launch_route_permute_small(logits, w, ids, T, E, k, eps, p.bm,
                                      counts, offsets, sorted, inv, tiles,
                                      ntiles, p.max_tiles, st, p.ks_r,
-                                     gate_fin, fcnt, (int)nfcnt,
+                                     gate_fin, router_clears ? nullptr : fcnt,
+                                     router_clears ? 0 : (int)nfcnt,
                                      a->router_bias));
     STAGE(clk, SLLM_MOE_STAGE_PERMUTE, 0);
   } else {
@@ -483,8 +525,9 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
           perm_inl ? 0
                    : launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted,
                                     inv, tiles, ntiles, p.max_tiles,
-                                    ws + p.pscr, st, route_hist, fcnt,
-                                    (int)nfcnt));
+                                    ws + p.pscr, st, route_hist,
+                                    router_clears ? nullptr : fcnt,
+                                    router_clears ? 0 : (int)nfcnt));
   }
 
   if (p.decode) {
@@ -536,7 +579,8 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
                   return launch_stream_dec(0, 0, r1, sh ? &s1 : nullptr, k,
                                            0.f, p.up_items, st, p.bm,
                                            fused ? &f_up : nullptr,
-                                           route_inl || perm_inl ? &ri : nullptr);
+                                           route_inl || perm_inl ? &ri : nullptr,
+                                           nullptr, -1, p.sk_up);
                 },
                 [&] {
                   return !fused && p.ks_up > 1
@@ -571,7 +615,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
             launch_stream_dec(0, 1, r2, sh ? &s2 : nullptr, k, 0.f,
                               p.dn_items, st, p.bm, nullptr, nullptr,
-                              comb_inl ? &dc : nullptr));
+                              comb_inl ? &dc : nullptr, -1, p.sk_dn));
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
       STAGE(clk, SLLM_MOE_STAGE_COMBINE,
@@ -889,14 +933,29 @@ int sllm_moe_plan_query(int deepseek, int T, int H, int E, int I, int Is,
   const int segN[4] = {I, H, Is, H}, ntw[4] = {128, 256, 128, 256};
   const int segks[4] = {p.ks_up, p.ks_dn, p.ks_up_sh, p.ks_dn_sh};
   const long items[4] = {p.up_items, p.dn_items, p.up_sh_items, p.dn_sh_items};
+  const bool sk[4] = {p.sk_up, p.sk_dn, false, false};
+  const long sh_rt = Is > 0 ? (T + p.bm_sh - 1) / p.bm_sh : 0;
+  const bool two = Is > 0 && !p.sh_sep;  // shared segment in launches 0, 1
   for (int j = 0; j < 4; ++j) {
     if (items[j] <= 0) continue;
+    out[10 + 3 * j] = items[j];
+    if (sk[j]) {  // stream-K (routed + shared launches): chunk 0, the grid
+                  // from the cost line's bound
+      const bool up = j == 0;
+      const long un[2] = {(long)p.max_tiles * (up ? I / 128 : H / 256),
+                          sh_rt * (up ? Is / 128 : H / 256)};
+      const int kb[2] = {up ? H / 128 : I / 128, up ? H / 128 : Is / 128};
+      const int w[2] = {1, deepseek ? 2 : 1};
+      const int ks[2] = {up ? p.ks_up : p.ks_dn, up ? p.ks_up_sh : p.ks_dn_sh};
+      out[11 + 3 * j] = 0;
+      out[12 + 3 * j] = dec_sk_launch_grid(two ? 2 : 1, un, kb, w, ks);
+      continue;
+    }
     // the routed launches' rows come from the tile table (identity rows for
     // a one-expert Qwen layer, run as a dense MLP), the DeepSeek shared
     // expert's are identity rows
     const bool routed = j < 2 && (deepseek || E > 1 || topk > 1);
     const long cb = dec_deal_chunk(segN[j], ntw[j], segks[j], routed, items[j]);
-    out[10 + 3 * j] = items[j];
     out[11 + 3 * j] = cb;
     out[12 + 3 * j] = dec_launch_grid(items[j], cb);
   }
@@ -939,6 +998,13 @@ static int dense8_mode() {
 
 // SLLM_MOE_ROUTE_INLINE=0: decode routes in its own launches (the same
 // tables, bit for bit).
+// SLLM_MOE_STREAMK=0: decode launches deal whole (K-split) items instead
+// of stream-K ranges (A/B runs)
+static bool streamk_on() {
+  const char* v = std::getenv("SLLM_MOE_STREAMK");
+  return !(v && v[0] == '0');
+}
+
 static bool route_inline_on() {
   const char* v = std::getenv("SLLM_MOE_ROUTE_INLINE");
   return !(v && v[0] == '0');
@@ -1078,7 +1144,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
                 return launch_stream_dec(2, 0, r1, sh_in ? &s1 : nullptr, k,
                                          L, p.up_items, st, p.bm, nullptr,
                                          perm_inl ? &ri : nullptr, nullptr,
-                                         SF_FP8_F32S);
+                                         SF_FP8_F32S, p.sk_up);
               },
               [&] {
                 return p.ks_up > 1
@@ -1088,7 +1154,7 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
           launch_stream_dec(2, 1, r2, sh_in ? &s2 : nullptr, k, 0.f,
                             p.dn_items, st, p.bm, nullptr, nullptr, nullptr,
-                            SF_FP8_F32S));
+                            SF_FP8_F32S, p.sk_dn));
     if (!sh || sh_in) {
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);

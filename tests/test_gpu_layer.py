@@ -621,6 +621,44 @@ def test_deepseek_decode_inline_permutation_matches_launch(B, hashed, monkeypatc
                                       np.asarray(r0[n]).view(np.uint32), err_msg=n)
 
 
+@pytest.mark.parametrize("B", [1, 3, 8, 16])
+def test_deepseek_decode_streamk_matches_whole_items(B, monkeypatch):
+    """DeepSeek decode up to 16 tokens deals its mixed-format launches
+    stream-K: each workgroup an equal range of the units' K steps, a unit's
+    steps across two ranges summed from K slices (the first item writing
+    zeros to slices no range reached). SLLM_MOE_STREAMK=0 deals whole
+    K-split items. The two differ only in how the fp32 K partials are
+    grouped: outputs within 2e-6 relative L2 of each other and routing
+    equal; at 1 and 3 tokens the stream-K output is also checked against
+    the decode oracle (bf16 activations, dequantized experts)."""
+    import functools
+    from oracle.codecs import dequant_fp4_block, dequant_fp8_block
+    x, W = deepseek_mxfp4_gpu(seed=70 + B, T=B, H=4096, E=64, I=1536, Is=1536)
+    kw = dict(n_group=8, topk_group=4, scoring="sigmoid", route_scale=2.5,
+              swiglu_limit=10.0)
+    layer = deepseek_layer(W, 6, **kw)
+    monkeypatch.setenv("SLLM_MOE_STREAMK", "1")
+    y1, r1 = layer.forward(x, mode="decode", return_routing=True)
+    monkeypatch.setenv("SLLM_MOE_STREAMK", "0")
+    y0, r0 = layer.forward(x, mode="decode", return_routing=True)
+    np.testing.assert_array_equal(r1["ids"], r0["ids"])
+    assert rel_l2(y1, y0) < 2e-6
+    if B > 3:
+        return
+
+    @functools.lru_cache(maxsize=None)
+    def ex(e):
+        return (dequant_fp4_block(W.w1_p[e], W.w1_s[e]),
+                dequant_fp4_block(W.w3_p[e], W.w3_s[e]),
+                dequant_fp4_block(W.w2_p[e], W.w2_s[e]))
+    sh = (dequant_fp8_block(W.s1_q, W.s1_s), dequant_fp8_block(W.s3_q, W.s3_s),
+          dequant_fp8_block(W.s2_q, W.s2_s))
+    want = dm.moe_block_forward(x, r1["logits"], W.bias, ex, sh, 6, 10.0,
+                                "sigmoid", 2.5, 8, 4)
+    rel, mabs, scale = _report(f"deepseek decode stream-K B={B}", y1, want)
+    assert rel < 1e-4
+
+
 @pytest.mark.parametrize("T", [1, 13, 32, 64])
 def test_decode_router_split_logits(T):
     """Decode-size router GEMM with its K split over workgroups: the

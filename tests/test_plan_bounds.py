@@ -134,6 +134,72 @@ def test_stream_dec_grid_deals_at_most_32_items(ncu):
             assert worst <= ST_MAX_ITEMS, (upper, cb, grid, worst)
 
 
+def _sk_lreq(KB, w, ks):
+    """Least stream-K range length keeping a unit within ks ranges."""
+    return max(w, ((KB - 1) * w + ks - 2) // (ks - 1))
+
+
+def _sample_tiles(max_tiles):
+    """Routed tile counts to deal: the ends and a spread in between."""
+    return sorted({1, 2, 3, max_tiles // 3, max_tiles // 2, max_tiles - 1,
+                   max_tiles} - {0})
+
+
+def _check_sk_deal(nu, KB, w, ks, grid, where):
+    """Port of moe_stream_dec_kernel's stream-K deal: units of segment s
+    (routed first) cost KB[s] w[s] on one line cut into G equal ranges, one
+    per workgroup; a workgroup's items are the K steps of each unit whose
+    start lies in its range. Checks that every unit's steps are dealt
+    exactly once, in slices 0..P-1 with P <= ks (the first item zero-fills
+    the rest), and that no workgroup meets more than 64 candidate units or
+    holds more than 32 items."""
+    assert grid % 8 == 0 and grid > 0, where
+    c = [KB[s] * w[s] for s in range(len(nu))]
+    cs = nu[0] * c[0]
+    C = cs + (nu[1] * c[1] if len(nu) > 1 else 0)
+    lreq = max(_sk_lreq(KB[s], w[s], ks[s]) for s in range(len(nu)))
+    G = max(1, min(grid, C // lreq))
+
+    def unit_of(x):
+        return x // c[0] if x < cs else nu[0] + (x - cs) // c[1]
+
+    def range_of(x):
+        return ((x + 1) * G - 1) // C
+
+    seen = {}
+    for r in range(G):
+        a, b = r * C // G, (r + 1) * C // G
+        ua = unit_of(a)
+        ncand = unit_of(b - 1) - ua + 1
+        assert ncand <= 64, (where, r, ncand)
+        items = 0
+        for u in range(ua, ua + ncand):
+            seg = int(u >= nu[0])
+            li = u - nu[0] if seg else u
+            cu = cs + li * c[1] if seg else li * c[0]
+            kb, ww = KB[seg], w[seg]
+            jlo = 0 if a <= cu else (a - cu + ww - 1) // ww
+            jhi = min(kb, (b - cu + ww - 1) // ww)
+            if jlo >= jhi:
+                continue
+            items += 1
+            rfirst = range_of(cu)
+            nsl = range_of(cu + (kb - 1) * ww) - rfirst + 1
+            slot = r - rfirst
+            fill = ks[seg] - nsl if slot == 0 else 0
+            assert 0 <= slot < nsl <= ks[seg] and fill >= 0, (where, r, u)
+            seen.setdefault(u, []).append((slot, jlo, jhi, fill))
+        assert items <= ST_MAX_ITEMS, (where, r, items)
+    assert len(seen) == sum(nu), where
+    for u, pieces in seen.items():
+        kb = KB[int(u >= nu[0])]
+        pieces.sort()
+        assert [p_[0] for p_ in pieces] == list(range(len(pieces))), (where, u)
+        assert pieces[0][1] == 0 and pieces[-1][2] == kb, (where, u)
+        for p0, p1 in zip(pieces, pieces[1:]):
+            assert p0[2] == p1[1], (where, u)  # the steps tile the unit
+
+
 def _chunk_cap(cb, upper):
     """A deal chunk holds at most a 64th of the launch's items (at least 1)."""
     return max(1, min(cb, upper // 64))
@@ -160,11 +226,14 @@ SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("streamk", ["1", "0"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_decode_plans_deal_at_most_32_items(shape):
+def test_decode_plans_deal_at_most_32_items(shape, streamk, monkeypatch):
     """Every decode launch of the library's plans, at every batch size and
-    every routed tile count up to the plan's bound, deals no workgroup more
-    than 32 items."""
+    every routed tile count up to the plan's bound (sampled for stream-K
+    deals), deals no workgroup more than 32 items; with stream-K
+    (SLLM_MOE_STREAMK=1, the default) every unit's K steps exactly once."""
+    monkeypatch.setenv("SLLM_MOE_STREAMK", streamk)
     lib = _need_lib()
     ds, H, E, k, I, Is = shape
     for T in range(1, 65):
@@ -185,6 +254,18 @@ def test_decode_plans_deal_at_most_32_items(shape):
         for j, (per_tile, shared) in enumerate(launches):
             upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
             assert upper == max_tiles * per_tile + shared, (T, j)
+            if cb == 0:  # stream-K deal
+                up = j == 0
+                nu = [0, (sh_rt * (Is // 128 if up else H // 256)) if not sep else 0]
+                KB = [H // 128 if up else I // 128, H // 128 if up else max(1, Is // 128)]
+                w = [1, 2 if ds else 1]
+                ks = [ks_up if up else ks_dn, ks_up_sh if up else ks_dn_sh]
+                nseg = 2 if nu[1] else 1
+                for rt in _sample_tiles(max_tiles):
+                    nu[0] = rt * (I // 128 if up else H // 256)
+                    _check_sk_deal(nu[:nseg], KB[:nseg], w[:nseg], ks[:nseg],
+                                   grid, (T, j, rt))
+                continue
             # identity rows (a one-expert layer): an eighth of a tile
             want_cb = per_tile if (ds or E > 1 or k > 1) else -(-per_tile // 8)
             assert cb == _chunk_cap(want_cb, upper) and grid % 8 == 0, (T, j)
@@ -197,18 +278,26 @@ def test_decode_plans_deal_at_most_32_items(shape):
             for j, per_tile in ((2, Is // 128 * ks_up_sh), (3, H // 256 * ks_dn_sh)):
                 upper, cb, grid = p[10 + 3 * j], p[11 + 3 * j], p[12 + 3 * j]
                 assert upper == sh_rt * per_tile
+                if cb == 0:  # stream-K deal
+                    units = sh_rt * (Is // 128 if j == 2 else H // 256)
+                    KB = H // 128 if j == 2 else Is // 128
+                    _check_sk_deal([units], [KB], [1], [ks_up_sh if j == 2 else ks_dn_sh],
+                                   grid, (T, j))
+                    continue
                 assert cb == _chunk_cap(-(-per_tile // 8), upper), (T, j)
                 assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS, (T, j)
 
 
-def test_old_contiguous_sizing_would_overflow():
+def test_old_contiguous_sizing_would_overflow(monkeypatch):
     """Regression: sizing the decode grid as if each XCD held a contiguous
     eighth of the items (sllm_moe_stream_grid) deals 37 items to a
     workgroup of the H 4096, E 128, top-8, I 1536 layer at 6 tokens, and
     36 to the H 3584, E 64, I 2560, Is 20480 layer at 7 tokens; the
     chunk-aware grid the library now launches keeps them at 32. (The old
     deal's chunks were whole row tiles; the library's are now capped at a
-    64th of the items.)"""
+    64th of the items. The plans here deal whole items, as they did then:
+    SLLM_MOE_STREAMK=0.)"""
+    monkeypatch.setenv("SLLM_MOE_STREAMK", "0")
     lib = _need_lib()
     for (ds, H, E, k, I, Is), T, old_worst in (
             ((0, 4096, 128, 8, 1536, 1536), 6, 37),
@@ -222,7 +311,8 @@ def test_old_contiguous_sizing_would_overflow():
             w_old = _max_items(upper, old, tile_cb)
             if w_old > ST_MAX_ITEMS:
                 bad = w_old
-            assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS
+            if cb:  # (a stream-K launch, chunk 0, is checked by its port)
+                assert _max_items(upper, grid, cb) <= ST_MAX_ITEMS
         assert bad == old_worst, (H, T, bad)
 
 
