@@ -252,7 +252,8 @@ def c4_result(args):
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
     t0 = time.perf_counter()
     layer = DeviceLayerDS(c, seed=args.seed)
-    x = to_device_raw(to_bf16(c4_inputs(layer)))
+    xh = c4_inputs(layer)
+    x = to_device_raw(to_bf16(xh))
     out = DeviceBuffer(T * H * 2)
     ws = DeviceBuffer(deepseek_workspace_bytes(T, H, E, I, Is, k, "prefill"))
     cnt = DeviceBuffer(E * 4)
@@ -283,9 +284,53 @@ def c4_result(args):
                          "TFLOPs": round(up_flops / t_up / 1e12, 1),
                          "mfma_frac_fp8_rate": round(up_flops / t_up / (PEAK_FP8_TFLOPS * 1e12), 4)},
            "routing_us": routing_us}
+    if not args.no_decode:
+        res["decode"] = c4_decode(layer, xh, (1, 8, 32), args.decode_iters)
     del layer
     sync()
     return res
+
+
+def c4_decode(layer, xh, batches, iters):
+    """The C4 layer in decode mode at each batch size B (its first B tokens),
+    per call between HIP events with a 512 MiB fill before each timed call
+    (L2 and MALL flushed), as the C3 decode leg: us, touched experts, the
+    algorithmic bytes (touched experts' MXFP4 weights and e8m0 scales, the
+    FP8 shared expert and its scales, the bf16 router) and their rate."""
+    import numpy as np
+    from sllm_amd.moe import deepseek_workspace_bytes
+    from sllm_amd.runtime import DeviceBuffer, Event, memset, sync, to_bf16, to_device_raw
+    c = layer.cfg
+    H, E, I, Is, k = c["H"], c["E"], c["I"], c["Is"], c["k"]
+    flush = DeviceBuffer(512 << 20)
+    a0, a1 = Event(), Event()
+    out = {}
+    for B in batches:
+        xb = to_device_raw(to_bf16(xh[:B]))
+        ob = DeviceBuffer(B * H * 2)
+        wsb = DeviceBuffer(deepseek_workspace_bytes(B, H, E, I, Is, k, "decode"))
+        cb = DeviceBuffer(E * 4)
+        ds_call(layer, xb, ob, wsb, B, "decode", debug={"counts_out": cb})
+        sync()
+        tb = int((cb.copy_host_raw(np.int32, (E,)) > 0).sum())
+        t = []
+        for it in range(iters + 3):
+            memset(flush, it & 0xFF, flush.nbytes)
+            a0.record()
+            ds_call(layer, xb, ob, wsb, B, "decode")
+            a1.record()
+            a1.synchronize()
+            if it >= 3:
+                t.append(a0.elapsed_ms(a1) * 1e3)
+        us = statistics.median(t)
+        nb = (tb * (3 * H * I // 2 + 3 * H * I // 32) + 3 * H * Is +
+              3 * (H // 128) * (Is // 128) * 4 + E * H * 2)
+        out[str(B)] = {"us": round(us, 2), "touched_experts": tb, "bytes": nb,
+                       "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                       "hbm_frac": round(nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"C4 decode B={B}: {us:.1f} us, touched {tb}, "
+            f"{nb / (us * 1e-6) / 1e9:.1f} GB/s")
+    return out
 
 
 def run_loader(args):
@@ -1005,6 +1050,8 @@ def main(argv=None) -> int:
                 extra[name]["expert_up"] = r["expert_up"]
             if "routing_us" in r:
                 extra[name]["routing_us"] = r["routing_us"]
+            if "decode" in r:
+                extra[name]["decode"] = r["decode"]
             log(f"{name}: {r['ms_per_step']} ms, {r['value']} tok/s")
 
     res = {
