@@ -852,8 +852,17 @@ def decode_leg(layer, batches, iters, flush):
 
 def run_decode_batch(args):
     """One C3 decode batch alone (the C2 layer at B = --decode-batch
-    tokens), one JSON line: for profiling the decode kernels."""
+    tokens; with --config c4 the C4 layer's first B tokens), one JSON line:
+    for profiling the decode kernels."""
     from sllm_amd.runtime import DeviceBuffer
+    if args.config == "c4":
+        layer = DeviceLayerDS(dict(C4), seed=args.seed)
+        d = c4_decode(layer, c4_inputs(layer), (args.decode_batch,),
+                      args.decode_iters)
+        print(json.dumps({"metric": "C4 decode layer us",
+                          "batch": args.decode_batch,
+                          **d[str(args.decode_batch)]}), flush=True)
+        return 0
     layer = DeviceLayer(dict(C2), seed=args.seed)
     flush = DeviceBuffer(512 << 20)
     d = decode_leg(layer, (args.decode_batch,), args.decode_iters, flush)
@@ -887,7 +896,8 @@ def main(argv=None) -> int:
                          "checkpoint (safetensors, reference naming) to the "
                          "device and exit")
     ap.add_argument("--decode-batch", type=int, default=0, metavar="B",
-                    help="only time the C3 decode layer at B tokens and exit")
+                    help="only time the C3 decode layer at B tokens and exit "
+                         "(with --config c4: the C4 layer's decode)")
     ap.add_argument("--device-decode", action="store_true",
                     help="only time the device-decode drop-ins (MoE hook and "
                          "dense SwiGLU MLP) at decode batch sizes and exit")

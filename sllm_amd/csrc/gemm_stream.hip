@@ -1001,11 +1001,23 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
         // wave w routes token w; other workgroups read the rows meanwhile:
         // no write-back of the summed slices (store false)
         if (wave < RI.T) {
-          route_softmax_token<8, 2>(RI.logits + (size_t)wave * RI.E, RI.ks,
-                                    (long)RI.T * RI.E, RI.E, k, RI.eps,
-                                    lead ? RI.w + (size_t)wave * k : nullptr,
-                                    lead ? RI.ids + (size_t)wave * k : nullptr,
-                                    ri_ids + wave * k, RI.bias, false);
+          if (RI.grouped) {
+            // scratch: the wave's histogram row, unused until the permutation
+            static_assert(2 * RI_MAX_E_GROUPED <= RI_MAX_E, "grouped routing scratch");
+            float* scr = (float*)ri_hist[wave];
+            route_grouped_token<RI_MAX_E_GROUPED / 64>(
+                RI.logits + (size_t)wave * RI.E, RI.ks, (long)RI.T * RI.E,
+                false, RI.E, k, RI.n_group, RI.topk_group, RI.scoring,
+                RI.route_scale, RI.bias, scr, scr + RI_MAX_E_GROUPED,
+                lead ? RI.w + (size_t)wave * k : nullptr,
+                lead ? RI.ids + (size_t)wave * k : nullptr, ri_ids + wave * k);
+          } else {
+            route_softmax_token<8, 2>(RI.logits + (size_t)wave * RI.E, RI.ks,
+                                      (long)RI.T * RI.E, RI.E, k, RI.eps,
+                                      lead ? RI.w + (size_t)wave * k : nullptr,
+                                      lead ? RI.ids + (size_t)wave * k : nullptr,
+                                      ri_ids + wave * k, RI.bias, false);
+          }
           if (lead && RI.gate && lane == 0) route_gate_finish(RI.gate, RI.T, wave, RI.ks);
         }
       } else {
@@ -1862,6 +1874,15 @@ int launch_stream_dec(int bf, int mode, const SegDesc& s0_in,
                                    route.ids && !route.ids_in),
                  "stream decode gemm: bad in-launch routing (T=%d ks=%d)",
                  route.T, route.ks);
+    SLLM_REQUIRE(!route.grouped ||
+                     (route.logits && route.E <= RI_MAX_E_GROUPED &&
+                      route.scoring >= 0 && route.scoring <= 2 &&
+                      (route.n_group <= 1 ||
+                       (route.n_group <= 64 && route.E % route.n_group == 0 &&
+                        route.topk_group >= 1 &&
+                        route.topk_group <= route.n_group))),
+                 "stream decode gemm: bad in-launch grouped routing (E=%d "
+                 "groups %d keep %d)", route.E, route.n_group, route.topk_group);
     SLLM_REQUIRE(mode == 0 && s0.gather && s0.tile_info && s0.sorted_idx &&
                      route.topk == topk && route.bm == bm &&
                      route.max_tiles == s0.max_tiles &&

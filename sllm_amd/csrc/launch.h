@@ -346,7 +346,13 @@ struct RouteInline {
   int* ntiles;
   int T, E, topk, ks, nbits, bm, max_tiles;
   float eps;
+  // grouped: the DeepSeek scored routing (route_grouped_token: scoring,
+  // bias, n_group / topk_group limit, route_scale) in place of the Qwen
+  // softmax top-k; E <= RI_MAX_E_GROUPED
+  int grouped, scoring, n_group, topk_group;
+  float route_scale;
 };
+constexpr int RI_MAX_E_GROUPED = 256;
 bool route_inline_fits(int T, int E, int topk, long max_tiles);
 // A mode-1 decode launch may also do the weighted combine (DecCombine.cnt
 // non-null): its y slices go out as device-scope stores, every workgroup

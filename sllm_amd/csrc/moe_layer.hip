@@ -211,7 +211,10 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
     p.gu = p.ks_up > 1 ? take(c, (size_t)2 * p.ks_up * p.N * I * 4) : 0;
     p.gu_sh = has_shared && p.ks_up_sh > 1
                   ? take(c, (size_t)2 * p.ks_up_sh * T * Is * 4) : 0;
-    if (!deepseek && !force_gemv && (T <= DEC_FUSE_MAX_T || p.sk_up)) {
+    // (DeepSeek: the launches that route the batch in the gate/up launch,
+    // whose router launch clears the counters)
+    if (!force_gemv &&
+        (deepseek ? T <= RI_MAX_ROUTE_T : (T <= DEC_FUSE_MAX_T || p.sk_up))) {
       p.fcnt_on = true;
       p.fcnt = take(c, (size_t)(dec_fuse_counters(p.N, T, I, has_shared ? Is : 0) +
                                 dec_combine_counters(T, H)) * 4);
@@ -1062,6 +1065,28 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
   // launch, which would read x again (C4: 117 MB).
   const bool rq_fused = !p.decode && !a->logits_given &&
                         router_logits_quant_fits(T, H);
+  // Streamed decode up to RI_MAX_ROUTE_T tokens with the router launch: the
+  // routed gate/up launch also routes the batch (grouped scoring, a token
+  // per wave, in every workgroup), in place of the routing launch; the
+  // router launch clears the counters of the gate/up launch's fused finish
+  // and, at one token, of the down launch's fused combine (as in the Qwen
+  // layer). Not with hash routing, caller-given logits, or a split
+  // router's logits asked for (the launch leaves the slices unsummed).
+  const bool route_inl = p.decode && a->w13_packed && p.fcnt_on &&
+                         !a->tid2eid && !a->logits_given &&
+                         T <= RI_MAX_ROUTE_T && E <= RI_MAX_E_GROUPED &&
+                         (!a->logits_out || p.ks_r == 1) &&
+                         route_inline_fits(T, E, k, p.max_tiles) &&
+                         route_inline_on();
+  const bool fused = route_inl && (p.ks_up > 1 || (sh && p.ks_up_sh > 1));
+  // (the down launch's fused combine, a gain for the Qwen layer at one
+  // token, lost here: C4 B=1 down 24.2 -> 31.6 us against the 4.3 us
+  // combine launch, with H / 256 = 28 units of 8 routed K-split slots and
+  // the shared slices to add at the launch's end)
+  const bool comb_inl = false;
+  int* fcnt = route_inl ? (int*)(ws + p.fcnt) : nullptr;
+  const long nfcnt = route_inl ? dec_fuse_counters(p.N, T, I, Is) : 0;
+  const long nccnt = comb_inl ? dec_combine_counters(T, H) : 0;
   // with caller-provided logits the router stage is recorded with zero
   // length, so every stage's events exist on every call
   STAGE(clk, SLLM_MOE_STAGE_ROUTER_GEMM,
@@ -1070,28 +1095,35 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
             ? launch_router_logits_quant(
                   (const uint16_t*)a->x, (const uint16_t*)a->router_w, logits,
                   T, E, H, (uint8_t*)(ws + p.xq), (float*)(ws + p.sx), 1, st)
+        : route_inl
+            ? launch_router_small_gate((const uint16_t*)a->x,
+                                       (const uint16_t*)a->router_w, logits,
+                                       T, E, H, nullptr, nullptr, st, p.ks_r,
+                                       fcnt, nfcnt + nccnt)
             : launch_router_gemm((const uint16_t*)a->x,
                                  (const uint16_t*)a->router_w, logits, T, E,
                                  H, st, p.ks_r));
   STAGE(clk, SLLM_MOE_STAGE_ROUTE,
-        a->tid2eid
+        route_inl ? 0
+        : a->tid2eid
             ? launch_route_hash(logits, a->token_ids, a->tid2eid, a->vocab, w,
                                 ids, T, E, k, a->scoring, a->route_scale, st,
                                 p.ks_r)
             : launch_route_grouped(logits, a->bias, w, ids, T, E, k,
                                    a->n_group, a->topk_group, a->scoring,
                                    a->route_scale, st, p.ks_r));
-  // Streamed decode: the routed gate/up launch builds the permutation from
-  // the routing launch's ids in every workgroup (RouteInline.ids_in), in
-  // place of the permutation launch, as in the Qwen layer.
-  const bool perm_inl = p.decode && a->w13_packed &&
+  // Streamed decode otherwise: the routed gate/up launch builds the
+  // permutation from the routing launch's ids in every workgroup
+  // (RouteInline.ids_in), in place of the permutation launch, as in the
+  // Qwen layer.
+  const bool perm_inl = p.decode && a->w13_packed && !route_inl &&
                         route_inline_fits(T, E, k, p.max_tiles) &&
                         route_inline_on();
   STAGE(clk, SLLM_MOE_STAGE_PERMUTE,
-        perm_inl ? 0
-                 : launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted,
-                                  inv, tiles, ntiles, p.max_tiles, ws + p.pscr,
-                                  st));
+        route_inl || perm_inl
+            ? 0
+            : launch_permute(ids, p.N, E, p.bm, counts, offsets, sorted, inv,
+                             tiles, ntiles, p.max_tiles, ws + p.pscr, st));
 
   if (p.decode && a->w13_packed) {
     // streamed packed weights, unquantized activations; the route weight
@@ -1131,30 +1163,45 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
     r2.N = H; r2.K = I; r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
     r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
     RouteInline ri{};
-    if (perm_inl) {
-      ri.ids_in = ids;
+    if (route_inl || perm_inl) {
+      ri.logits = route_inl ? logits : nullptr;
+      ri.ids_in = perm_inl ? ids : nullptr;
+      ri.bias = a->bias; ri.w = w; ri.ids = ids;
       ri.counts = counts; ri.offsets = offsets; ri.sorted = sorted;
       ri.inv = inv; ri.tiles = tiles; ri.ntiles = ntiles;
-      ri.T = T; ri.E = E; ri.topk = k; ri.ks = 1; ri.bm = p.bm;
-      ri.max_tiles = p.max_tiles;
+      ri.T = T; ri.E = E; ri.topk = k; ri.ks = route_inl ? p.ks_r : 1;
+      ri.bm = p.bm; ri.max_tiles = p.max_tiles;
+      ri.grouped = route_inl; ri.scoring = a->scoring; ri.n_group = a->n_group;
+      ri.topk_group = a->topk_group; ri.route_scale = a->route_scale;
     }
+    const DecFuse f_up{fcnt, (long)p.N * (I / 128)};
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
           first_rc(
               [&] {
                 return launch_stream_dec(2, 0, r1, sh_in ? &s1 : nullptr, k,
-                                         L, p.up_items, st, p.bm, nullptr,
-                                         perm_inl ? &ri : nullptr, nullptr,
-                                         SF_FP8_F32S, p.sk_up);
+                                         L, p.up_items, st, p.bm,
+                                         fused ? &f_up : nullptr,
+                                         route_inl || perm_inl ? &ri : nullptr,
+                                         nullptr, SF_FP8_F32S, p.sk_up);
               },
               [&] {
-                return p.ks_up > 1
+                return !fused && (p.ks_up > 1 || (sh_in && p.ks_up_sh > 1))
                            ? launch_split_finish(r1, sh_in ? &s1 : nullptr, L, st)
                            : 0;
               }));
+    DecCombine dc{};
+    if (comb_inl) {
+      dc.cnt = fcnt + nfcnt; dc.inv = inv; dc.sorted = sorted;
+      dc.y = y; dc.kstride = (long)p.N * H; dc.ks = p.ks_dn;
+      dc.y_sh = sh_in ? y_sh : nullptr; dc.kstride_sh = (long)T * H;
+      dc.ks_sh = sh_in ? p.ks_dn_sh : 0;
+      dc.T = T; dc.H = H; dc.topk = k; dc.out_f32 = a->out_f32;
+      dc.out = a->out;
+    }
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_DOWN,
           launch_stream_dec(2, 1, r2, sh_in ? &s2 : nullptr, k, 0.f,
-                            p.dn_items, st, p.bm, nullptr, nullptr, nullptr,
-                            SF_FP8_F32S, p.sk_dn));
+                            p.dn_items, st, p.bm, nullptr, nullptr,
+                            comb_inl ? &dc : nullptr, SF_FP8_F32S, p.sk_dn));
     if (!sh || sh_in) {
       STAGE(clk, SLLM_MOE_STAGE_SHARED_UP, 0);
       STAGE(clk, SLLM_MOE_STAGE_SHARED_DOWN, 0);
@@ -1175,9 +1222,10 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
                               p.bm_sh));
     }
     STAGE(clk, SLLM_MOE_STAGE_COMBINE,
-          launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32, a->out,
-                               p.ks_dn, (long)p.N * H, p.ks_dn_sh,
-                               (long)T * H, st));
+          comb_inl ? 0
+                   : launch_combine_split(y, inv, k, y_sh, T, H, a->out_f32,
+                                          a->out, p.ks_dn, (long)p.N * H,
+                                          p.ks_dn_sh, (long)T * H, st));
   } else if (p.decode) {
     float* h = (float*)(ws + p.hq);
     float* y = (float*)(ws + p.y);

@@ -1,8 +1,9 @@
-// Per-token softmax top-k routing on one wave, shared by the routing
-// launches (router.hip) and the decode gate/up launch that routes its
-// batch itself (gemm_stream.hip): top-k keys, the wave's top-k, the
-// logits of a row held as K-chunk slices, and the softmax weights
-// (ref/qwen4_exp.py:118-140; tie rule of kernels/cuda/qwen4.cu:259-270).
+// Per-token routing on one wave, shared by the routing launches
+// (router.hip) and the decode gate/up launch that routes its batch itself
+// (gemm_stream.hip): top-k keys, the wave's top-k, the logits of a row held
+// as K-chunk slices, the softmax weights (ref/qwen4_exp.py:118-140; tie
+// rule of kernels/cuda/qwen4.cu:259-270), and the scored, biased and
+// group-limited routing (ref/deepseek_v4.py:522-561).
 #pragma once
 #include "common.h"
 
@@ -219,5 +220,170 @@ __device__ __forceinline__ void route_gate_finish(float* gate, int T, int t,
   gate[t] = sigmoid_f32(g);
 }
 
+// --------------------------------------------------------------------------
+// scored routing with selection bias and optional group limit
+// (ref/deepseek_v4.py:522-561; group limit per DeepSeek-V3 noaux_tc)
+// --------------------------------------------------------------------------
+enum Scoring { SCORE_SOFTMAX = 0, SCORE_SIGMOID = 1, SCORE_SQRTSOFTPLUS = 2 };
+
+// Scores of one token's logits row on the calling wave (lane holds experts
+// lane + 64 i): softmax in fp64 (ref/deepseek_v4.py:524-525), sigmoid in
+// fp64 then fp32 (:526-528), sqrt(softplus) (:529-530, :534-537).
+template <int EPL>
+__device__ __forceinline__ void gate_scores_row(float* row, int ks,
+                                                long kstride, bool store,
+                                                int E, int scoring,
+                                                float (&sc)[EPL]) {
+  const int lane = threadIdx.x & 63;
+  float lv[EPL];
+  logit_sums<EPL>(row, ks, kstride, E, store, 0.f, lv);
+  if (scoring == SCORE_SOFTMAX) {
+    double m = -INFINITY;
+    double xv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      int e = lane + 64 * i;
+      xv[i] = e < E ? (double)lv[i] : -INFINITY;
+      m = xv[i] > m ? xv[i] : m;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      double q = __shfl_xor(m, o, kWave);
+      m = q > m ? q : m;
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      xv[i] = (lane + 64 * i) < E ? exp(xv[i] - m) : 0.0;
+      s += xv[i];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sc[i] = (float)(xv[i] / s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      int e = lane + 64 * i;
+      double xv = e < E ? (double)lv[i] : 0.0;
+      if (scoring == SCORE_SIGMOID) {
+        sc[i] = (float)(1.0 / (1.0 + exp(-xv)));
+      } else {
+        double sp = log1p(exp(-fabs(xv))) + (xv > 0.0 ? xv : 0.0);
+        sc[i] = sqrtf((float)sp);
+      }
+    }
+  }
+}
+
+// One token's scored routing on the calling wave: the row's scores
+// (gate_scores_row) plus bias select; with n_group > 1 each group of
+// E / n_group experts is scored by the sum of its two largest biased scores
+// and the topk_group best groups are kept (ties: the lower group); the
+// top-k of the kept experts' biased scores (ties: the lower id); the
+// weights are their unbiased scores, renormalized over the picks unless
+// softmax, times route_scale. sb, scl: this wave's LDS scratch of EPL * 64
+// floats each. Lane j < topk writes slot j of w_row / id_row (both or
+// neither non-null) and of id_lds (when non-null).
+template <int EPL>
+__device__ __forceinline__ void route_grouped_token(
+    float* row, int ks, long kstride, bool store, int E, int topk, int n_group,
+    int topk_group, int scoring, float route_scale,
+    const float* __restrict__ bias, float* sb, float* scl,
+    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
+  const int lane = threadIdx.x & 63;
+  float sc[EPL];
+  gate_scores_row<EPL>(row, ks, kstride, store, E, scoring, sc);
+  float b[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    b[i] = e < E ? sc[i] + (bias ? bias[e] : 0.f) : -INFINITY;
+  }
+  const bool keep_all = n_group <= 1;
+  uint64_t gkeep = ~0ull;  // bit g set: group g kept (n_group <= 64)
+  if (!keep_all) {
+    const int gs = E / n_group;
+    // group score = the sum of the group's two largest biased scores (NaN
+    // never one of them, -inf when fewer than two others)
+    uint64_t gkey = 0;
+    if (gs <= 64 && (gs & (gs - 1)) == 0 && E % 64 == 0) {
+      // a group is gs adjacent lanes of one register: (largest, second)
+      // pairs merged across the group's lanes, NaN as -inf
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        float m1 = b[i] == b[i] ? b[i] : -INFINITY, m2 = -INFINITY;
+        for (int o = 1; o < gs; o <<= 1) {
+          const float p1 = __shfl_xor(m1, o, kWave), p2 = __shfl_xor(m2, o, kWave);
+          m2 = fmaxf(fminf(m1, p1), fmaxf(m2, p2));
+          m1 = fmaxf(m1, p1);
+        }
+        // lane g of the wave takes group g = (64 i + lane') / gs from the
+        // group's first lane lane'
+        const float gsum = m1 + m2;
+        const int ng_i = 64 / gs;  // groups in register i
+        for (int q = 0; q < ng_i; ++q) {
+          const float v = __shfl(gsum, q * gs, kWave);
+          const int g = i * ng_i + q;
+          if (lane == g && g < n_group)
+            gkey = ((uint64_t)f32_order_key(v) << 32) |
+                   (uint64_t)(0xFFFFFFFFu - (uint32_t)g);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (lane + 64 * i < E) sb[lane + 64 * i] = b[i];
+      __builtin_amdgcn_wave_barrier();  // the wave's LDS accesses stay in order
+      // lane g < n_group: its group's elements in turn
+      if (lane < n_group) {
+        float m1 = -INFINITY, m2 = -INFINITY;
+        for (int q = 0; q < gs; ++q) {
+          const float val = sb[lane * gs + q];
+          if (val > m1) {
+            m2 = m1;
+            m1 = val;
+          } else if (val > m2) {
+            m2 = val;
+          }
+        }
+        const float gsum = m1 + m2;
+        gkey = ((uint64_t)f32_order_key(gsum) << 32) |
+               (uint64_t)(0xFFFFFFFFu - (uint32_t)lane);
+      }
+    }
+    gkeep = 0;
+    for (int r = 0; r < topk_group; ++r) {
+      const uint64_t best = wave_max_u64(gkey);
+      const int g = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+      gkeep |= 1ull << g;
+      if (lane == g) gkey = 0;
+    }
+  }
+  uint64_t key[EPL];
+  const int gs = keep_all ? E : E / n_group;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    const bool ok = e < E && (keep_all || ((gkeep >> (e / gs)) & 1ull));
+    key[i] = ok ? topk_key(b[i], e) : 0ull;
+    if (e < E) scl[e] = sc[i];  // the picks' unbiased scores, by id
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
+  const int myid = topk_key_id(pick);
+  const float mine = lane < topk ? scl[min(max(myid, 0), E - 1)] : 0.f;
+  float wsum = 0.f;
+  for (int j = 0; j < topk; ++j)
+    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mine), j));
+  if (lane < topk) {
+    const float wv = scoring == SCORE_SOFTMAX ? mine : mine / wsum;
+    if (w_row) {
+      w_row[lane] = wv * route_scale;
+      id_row[lane] = myid;
+    }
+    if (id_lds) id_lds[lane] = myid;
+  }
+}
 
 }  // namespace sllm

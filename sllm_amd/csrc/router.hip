@@ -769,62 +769,9 @@ __global__ __launch_bounds__(1024) void route_permute_small_kernel(
                      hist, sh, zero, nzero);
 }
 
-// --------------------------------------------------------------------------
-// scored routing with selection bias and optional group limit
-// (ref/deepseek_v4.py:522-561; group limit per DeepSeek-V3 noaux_tc)
-// --------------------------------------------------------------------------
-enum Scoring { SCORE_SOFTMAX = 0, SCORE_SIGMOID = 1, SCORE_SQRTSOFTPLUS = 2 };
-
-// Scores of one token's logits row on the calling wave (lane holds experts
-// lane + 64 i): softmax in fp64 (ref/deepseek_v4.py:524-525), sigmoid in
-// fp64 then fp32 (:526-528), sqrt(softplus) (:529-530, :534-537).
-template <int EPL>
-__device__ __forceinline__ void gate_scores_row(float* row, int ks,
-                                                long kstride, bool store,
-                                                int E, int scoring,
-                                                float (&sc)[EPL]) {
-  const int lane = threadIdx.x & 63;
-  float lv[EPL];
-  logit_sums<EPL>(row, ks, kstride, E, store, 0.f, lv);
-  if (scoring == SCORE_SOFTMAX) {
-    double m = -INFINITY;
-    double xv[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      int e = lane + 64 * i;
-      xv[i] = e < E ? (double)lv[i] : -INFINITY;
-      m = xv[i] > m ? xv[i] : m;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      double q = __shfl_xor(m, o, kWave);
-      m = q > m ? q : m;
-    }
-    double s = 0.0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      xv[i] = (lane + 64 * i) < E ? exp(xv[i] - m) : 0.0;
-      s += xv[i];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) sc[i] = (float)(xv[i] / s);
-  } else {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      int e = lane + 64 * i;
-      double xv = e < E ? (double)lv[i] : 0.0;
-      if (scoring == SCORE_SIGMOID) {
-        sc[i] = (float)(1.0 / (1.0 + exp(-xv)));
-      } else {
-        double sp = log1p(exp(-fabs(xv))) + (xv > 0.0 ? xv : 0.0);
-        sc[i] = sqrtf((float)sp);
-      }
-    }
-  }
-}
-
+// Scored routing with selection bias and optional group limit
+// (ref/deepseek_v4.py:522-561; group limit per DeepSeek-V3 noaux_tc): one
+// token per wave (route_grouped_token).
 template <int EPL>
 __global__ __launch_bounds__(256) void route_grouped_kernel(
     float* logits, const float* __restrict__ bias, float* __restrict__ w_out,
@@ -832,74 +779,17 @@ __global__ __launch_bounds__(256) void route_grouped_kernel(
     int topk_group, int scoring, float route_scale, int ks) {
   __shared__ float sb[4][EPL * 64];
   __shared__ float scl[4][EPL * 64];
-  const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int t_raw = blockIdx.x * (blockDim.x >> 6) + wv;
   const bool active = t_raw < T;
   const int t = active ? t_raw : T - 1;  // idle waves mirror the last row
-  float sc[EPL];
   // waves past T mirror row T - 1 without writing it
-  gate_scores_row<EPL>(logits + (size_t)t * E, ks, (long)T * E, active, E,
-                       scoring, sc);
-  float b[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + 64 * i;
-    b[i] = e < E ? sc[i] + (bias ? bias[e] : 0.f) : -INFINITY;
-  }
-  bool keep_all = n_group <= 1;
-  uint64_t gkeep = ~0ull;  // bit g set: group g kept (n_group <= 64)
-  if (!keep_all) {
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (lane + 64 * i < E) sb[wv][lane + 64 * i] = b[i];
-    __syncthreads();  // n_group is uniform: every wave of the block is here
-    const int gs = E / n_group;
-    // lane g < n_group: group score = sum of the two largest biased scores
-    uint64_t gkey = 0;
-    if (lane < n_group) {
-      float m1 = -INFINITY, m2 = -INFINITY;
-      for (int q = 0; q < gs; ++q) {
-        float val = sb[wv][lane * gs + q];
-        if (val > m1) {
-          m2 = m1;
-          m1 = val;
-        } else if (val > m2) {
-          m2 = val;
-        }
-      }
-      float gsum = m1 + m2;
-      gkey = ((uint64_t)f32_order_key(gsum) << 32) |
-             (uint64_t)(0xFFFFFFFFu - (uint32_t)lane);
-    }
-    gkeep = 0;
-    for (int r = 0; r < topk_group; ++r) {
-      uint64_t best = wave_max_u64(gkey);
-      int g = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
-      gkeep |= 1ull << g;
-      if (lane == g) gkey = 0;
-    }
-  }
-  uint64_t key[EPL];
-  const int gs = keep_all ? E : E / n_group;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = lane + 64 * i;
-    bool ok = e < E && (keep_all || ((gkeep >> (e / gs)) & 1ull));
-    key[i] = ok ? topk_key(b[i], e) : 0ull;
-    if (e < E) scl[wv][e] = sc[i];  // the picks' unbiased scores, by id
-  }
-  const uint64_t pick = wave_topk_keys<EPL>(key, topk);
-  const int myid = topk_key_id(pick);
-  const float mine = lane < topk ? scl[wv][min(max(myid, 0), E - 1)] : 0.f;
-  float wsum = 0.f;
-  for (int j = 0; j < topk; ++j)
-    wsum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(mine), j));
-  if (active && lane < topk) {
-    float wv_ = scoring == SCORE_SOFTMAX ? mine : mine / wsum;
-    w_out[(size_t)t * topk + lane] = wv_ * route_scale;
-    id_out[(size_t)t * topk + lane] = myid;
-  }
+  route_grouped_token<EPL>(logits + (size_t)t * E, ks, (long)T * E, active, E,
+                           topk, n_group, topk_group, scoring, route_scale,
+                           bias, sb[wv], scl[wv],
+                           active ? w_out + (size_t)t * topk : nullptr,
+                           active ? id_out + (size_t)t * topk : nullptr,
+                           nullptr);
 }
 
 // Hash layers (ref/deepseek_v4.py:545-552; upstream model.py:620-627,
