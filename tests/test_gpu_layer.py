@@ -621,6 +621,50 @@ def test_deepseek_decode_inline_permutation_matches_launch(B, hashed, monkeypatc
                                       np.asarray(r0[n]).view(np.uint32), err_msg=n)
 
 
+@pytest.mark.parametrize("B,scoring,groups,shared,E", [
+    (1, "softmax", (4, 2), True, 32), (3, "sqrtsoftplus", (4, 2), True, 32),
+    (5, "sigmoid", (1, 1), True, 32), (8, "sigmoid", (4, 2), False, 32),
+    (2, "sigmoid", (8, 3), True, 32), (4, "sigmoid", (16, 4), True, 64),
+    (16, "sigmoid", (4, 2), True, 32), (17, "sigmoid", (4, 2), True, 32)])
+def test_deepseek_decode_variants_match_launches(B, scoring, groups, shared, E,
+                                                 monkeypatch):
+    """DeepSeek decode across the paths this batch size selects, against
+    the separate launches (SLLM_MOE_ROUTE_INLINE=0: routing, permutation,
+    finish launches) bit for bit, and against the decode oracle: every
+    scoring rule and a group limit or none routed in the gate/up launch (up
+    to 8 tokens), no shared expert (routed-only stream-K launches), 16
+    tokens (the last batch whose shared expert joins the routed launches)
+    and 17 (its own launches, 32-row tiles). Group scores: E = 64 (groups
+    of 4 adjacent lanes) merges them by lane shuffles, E = 32 scans them."""
+    ng, kg = groups
+    x, W = deepseek_mxfp4(seed=300 + B, T=B, H=1024, E=E, I=512, Is=512,
+                          shared=shared)
+    kw = dict(n_group=ng, topk_group=kg, scoring=scoring, route_scale=2.5,
+              swiglu_limit=10.0)
+    layer = deepseek_layer(W, 4, **kw)
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "1")
+    y1, r1 = layer.forward(x, mode="decode", return_routing=True)
+    monkeypatch.setenv("SLLM_MOE_ROUTE_INLINE", "0")
+    y0, r0 = layer.forward(x, mode="decode", return_routing=True)
+    np.testing.assert_array_equal(y1.view(np.uint32), y0.view(np.uint32))
+    for n in ("w", "ids", "counts"):
+        np.testing.assert_array_equal(np.asarray(r1[n]).view(np.uint32),
+                                      np.asarray(r0[n]).view(np.uint32), err_msg=n)
+    from oracle.codecs import dequant_fp4_block, dequant_fp8_block
+
+    def ex(e):
+        return (dequant_fp4_block(W.w1_p[e], W.w1_s[e]),
+                dequant_fp4_block(W.w3_p[e], W.w3_s[e]),
+                dequant_fp4_block(W.w2_p[e], W.w2_s[e]))
+    sh = ((dequant_fp8_block(W.s1_q, W.s1_s), dequant_fp8_block(W.s3_q, W.s3_s),
+           dequant_fp8_block(W.s2_q, W.s2_s)) if shared else None)
+    want = dm.moe_block_forward(x, r1["logits"], W.bias, ex, sh, 4, 10.0,
+                                scoring, 2.5, ng, kg)
+    rel, mabs, scale = _report(f"deepseek decode {scoring} g{ng}/{kg} "
+                               f"shared={shared} B={B}", y1, want)
+    assert rel < 1e-4
+
+
 @pytest.mark.parametrize("B", [1, 3, 8, 16])
 def test_deepseek_decode_streamk_matches_whole_items(B, monkeypatch):
     """DeepSeek decode up to 16 tokens deals its mixed-format launches
