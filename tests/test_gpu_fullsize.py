@@ -1,5 +1,6 @@
-"""Full-size parity of the layers bench.py times (C2, C4, C5), on the
-bench's own device-generated weights and inputs.
+"""Full-size parity of the layers bench.py times (C2, C4, C5, and C4 in
+decode mode at the bench's decode batch sizes), on the bench's own
+device-generated weights and inputs.
 
 For every token of each configuration:
 - the router GEMM the layer ran (the fused router of the default path; its
@@ -239,27 +240,58 @@ def test_c5_full_size_skewed():
     _qwen_full(bench.C5, skew=True)
 
 
-def test_c4_full_size():
+@pytest.fixture(scope="module")
+def c4_layer():
+    """The bench's C4 layer and its activations (bf16 values), built once
+    for the prefill and decode tests."""
+    c = dict(bench.C4)
+    print(f"[C4] building the bench layer T={c['T']} E={c['E']}", flush=True)
+    layer = bench.DeviceLayerDS(c, seed=0)
+    return layer, codecs.round_bf16(bench.c4_inputs(layer))
+
+
+def _c4_route(c):
+    return dict(n_group=c["n_group"], topk_group=c["topk_group"], scoring="sigmoid",
+                route_scale=c["route_scale"], swiglu_limit=c["swiglu_limit"])
+
+
+def _c4_weights(layer):
+    c, w = layer.cfg, layer.w
+    E, H, I, Is = c["E"], c["H"], c["I"], c["Is"]
+    return dm.DeepseekMxfp4Weights(
+        router_w=None, bias=w["bias"].copy_host(),
+        w1_p=_DeviceExperts(w["w1"], E, (I, H // 2), np.uint8),
+        w1_s=_DeviceExperts(w["w1_s"], E, (I, H // 32), np.uint8),
+        w3_p=_DeviceExperts(w["w3"], E, (I, H // 2), np.uint8),
+        w3_s=_DeviceExperts(w["w3_s"], E, (I, H // 32), np.uint8),
+        w2_p=_DeviceExperts(w["w2"], E, (H, I // 2), np.uint8),
+        w2_s=_DeviceExperts(w["w2_s"], E, (H, I // 32), np.uint8),
+        s1_q=_whole(w["s1"], (Is, H), np.uint8),
+        s1_s=_whole(w["s1_s"], (Is // 128, H // 128), np.float32),
+        s3_q=_whole(w["s3"], (Is, H), np.uint8),
+        s3_s=_whole(w["s3_s"], (Is // 128, H // 128), np.float32),
+        s2_q=_whole(w["s2"], (H, Is), np.uint8),
+        s2_s=_whole(w["s2_s"], (H // 128, Is // 128), np.float32))
+
+
+def test_c4_full_size(c4_layer):
     """C4: DeepSeek MXFP4, T=8192, H=7168, E=256, top-8 of 4 kept groups out
     of 8, sigmoid scores with selection bias, route scale 2.5, SwiGLU limit
     10, FP8 shared expert."""
     from sllm_amd.moe import deepseek_forward_dev, deepseek_workspace_bytes, stream_status
     from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
-    c = dict(bench.C4)
+    layer, xh = c4_layer
+    c = layer.cfg
     T, H, E, I, Is, k = c["T"], c["H"], c["E"], c["I"], c["Is"], c["k"]
-    print(f"[C4] building the bench layer T={T} E={E}", flush=True)
-    layer = bench.DeviceLayerDS(c, seed=0)
     bias = layer.w["bias"].copy_host()
-    xh = codecs.round_bf16(bench.c4_inputs(layer))
     x = to_device_raw(to_bf16(xh))
     ws = DeviceBuffer(deepseek_workspace_bytes(T, H, E, I, Is, k, "prefill"))
     o32, o16 = DeviceBuffer(T * H * 4), DeviceBuffer(T * H * 2)
     dbg = _debug_bufs(T, E, k)
-    route = dict(n_group=c["n_group"], topk_group=c["topk_group"], scoring="sigmoid",
-                 route_scale=c["route_scale"], swiglu_limit=c["swiglu_limit"])
     for out, f32, d in ((o32, True, dbg), (o16, False, None)):
         deepseek_forward_dev(x, out, layer.w, T=T, H=H, E=E, I=I, Is=Is, topk=k,
-                             mode="prefill", out_f32=f32, workspace=ws, debug=d, **route)
+                             mode="prefill", out_f32=f32, workspace=ws, debug=d,
+                             **_c4_route(c))
     sync()
     stream_status()
     y = o32.copy_host().reshape(T, H)
@@ -285,24 +317,88 @@ def test_c4_full_size():
           f"{counts.max()}", flush=True)
     rng = np.random.default_rng(11)
     s, hot = _sample_tokens(r["ids"], counts, rng, 32)
-    w = layer.w
-    W = dm.DeepseekMxfp4Weights(
-        router_w=None, bias=bias,
-        w1_p=_DeviceExperts(w["w1"], E, (I, H // 2), np.uint8),
-        w1_s=_DeviceExperts(w["w1_s"], E, (I, H // 32), np.uint8),
-        w3_p=_DeviceExperts(w["w3"], E, (I, H // 2), np.uint8),
-        w3_s=_DeviceExperts(w["w3_s"], E, (I, H // 32), np.uint8),
-        w2_p=_DeviceExperts(w["w2"], E, (H, I // 2), np.uint8),
-        w2_s=_DeviceExperts(w["w2_s"], E, (H, I // 32), np.uint8),
-        s1_q=_whole(w["s1"], (Is, H), np.uint8),
-        s1_s=_whole(w["s1_s"], (Is // 128, H // 128), np.float32),
-        s3_q=_whole(w["s3"], (Is, H), np.uint8),
-        s3_s=_whole(w["s3_s"], (Is // 128, H // 128), np.float32),
-        s2_q=_whole(w["s2"], (H, Is), np.uint8),
-        s2_s=_whole(w["s2_s"], (H // 128, Is // 128), np.float32))
+    W = _c4_weights(layer)
     print(f"  oracle over {len(s)} sampled tokens "
           f"({len(np.unique(r['ids'][s]))} experts)", flush=True)
     want = dm.moe_layer_mxfp4(xh[s], r["logits"][s], W, k, c["swiglu_limit"],
                               "sigmoid", c["route_scale"], c["n_group"], c["topk_group"])
     _report(f"C4 sampled {len(s)} tokens (hot expert {hot}: {counts[hot]} rows)",
             y[s], want)
+
+
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_c4_decode_full_size(c4_layer, B):
+    """The C4 layer in decode mode at the batch sizes bench.py times (the
+    first B tokens of the C4 activations): up to 8 tokens the routed gate/up
+    launch routes the batch itself (grouped sigmoid scores, 8 groups of 32
+    experts merged by lane shuffles) and deals its MXFP4 routed and FP8
+    shared items stream-K in one launch; at 32 tokens the routing and the
+    shared expert run in launches of their own. Checked:
+    - the fp32 output and routing of the in-launch routing path bit for bit
+      against the separate router and routing launches (the call that asks
+      for the router logits, which a split router leaves unsummed in the
+      in-launch path);
+    - the bf16 output the bench times equal to the bf16 rounding of the
+      fp32 output;
+    - the logits within the fp32 accumulation bound of fp64 x . W_r^T and
+      the ids bit-exact against the oracle's grouped routing of them
+      (ref/deepseek_v4.py:540-561);
+    - the output against the decode oracle (bf16 activations, dequantized
+      experts; ref/deepseek_v4.py:564-570 with the upstream combine of
+      ref/hf_sources/dsv4/model.py:684-699) on the first and last token
+      and two between them (each row depends only on its own token)."""
+    from sllm_amd.moe import deepseek_forward_dev, deepseek_workspace_bytes, stream_status
+    from sllm_amd.runtime import DeviceBuffer, sync, to_bf16, to_device_raw
+    from oracle.codecs import dequant_fp4_block, dequant_fp8_block
+    layer, xh_all = c4_layer
+    c = layer.cfg
+    H, E, I, Is, k = c["H"], c["E"], c["I"], c["Is"], c["k"]
+    xh = xh_all[:B]
+    x = to_device_raw(to_bf16(xh))
+    ws = DeviceBuffer(deepseek_workspace_bytes(B, H, E, I, Is, k, "decode"))
+    o_inl, o_sep, o16 = DeviceBuffer(B * H * 4), DeviceBuffer(B * H * 4), DeviceBuffer(B * H * 2)
+    d_sep = _debug_bufs(B, E, k)
+    d_inl = {n: DeviceBuffer(d_sep[n].nbytes) for n in ("w_out", "ids_out", "counts_out")}
+    print(f"[C4 decode B={B}] in-launch routing, bf16 output, separate launches",
+          flush=True)
+    for out, f32, d in ((o_inl, True, d_inl), (o16, False, None), (o_sep, True, d_sep)):
+        deepseek_forward_dev(x, out, layer.w, T=B, H=H, E=E, I=I, Is=Is, topk=k,
+                             mode="decode", out_f32=f32, workspace=ws, debug=d,
+                             **_c4_route(c))
+    sync()
+    stream_status()
+    y = o_inl.copy_host().reshape(B, H)
+    _check_bf16_out(o16, y, B, H)
+    np.testing.assert_array_equal(y.view(np.uint32),
+                                  o_sep.copy_host().reshape(B, H).view(np.uint32))
+    r = _host_debug(d_sep, B, E, k)
+    inl = {"w": d_inl["w_out"].copy_host().reshape(B, k),
+           "ids": d_inl["ids_out"].copy_host_raw(np.int32, (B, k)),
+           "counts": d_inl["counts_out"].copy_host_raw(np.int32, (E,))}
+    for n in ("w", "ids", "counts"):
+        np.testing.assert_array_equal(np.asarray(inl[n]).view(np.uint32),
+                                      np.asarray(r[n]).view(np.uint32), err_msg=n)
+    rw = codecs.decode_bf16(layer.w["router_w"].copy_host_raw(np.uint16, (E, H)))
+    check_router_logits(f"C4 decode B={B}", xh, rw, r["logits"])
+    W = _c4_weights(layer)
+    w_ref, ids_ref = dm.moe_route(r["logits"], W.bias, k, "sigmoid", c["route_scale"],
+                                  c["n_group"], c["topk_group"])
+    np.testing.assert_array_equal(r["ids"], ids_ref.astype(np.int32))
+    np.testing.assert_allclose(r["w"], w_ref, rtol=2e-6, atol=1e-7)
+    _check_permutation(r, E)
+    s = np.unique(np.linspace(0, B - 1, 4).astype(np.int64))
+    print(f"  oracle over {len(s)} tokens ({len(np.unique(r['ids'][s]))} experts)",
+          flush=True)
+
+    def ex(e):
+        return (dequant_fp4_block(W.w1_p[e], W.w1_s[e]),
+                dequant_fp4_block(W.w3_p[e], W.w3_s[e]),
+                dequant_fp4_block(W.w2_p[e], W.w2_s[e]))
+    sh = (dequant_fp8_block(W.s1_q, W.s1_s), dequant_fp8_block(W.s3_q, W.s3_s),
+          dequant_fp8_block(W.s2_q, W.s2_s))
+    want = dm.moe_block_forward(xh[s], r["logits"][s], W.bias, ex, sh, k,
+                                c["swiglu_limit"], "sigmoid", c["route_scale"],
+                                c["n_group"], c["topk_group"])
+    rel = rel_l2(y[s], want)
+    print(f"C4 decode B={B}: rel-L2 {rel:.3e}", flush=True)
+    assert rel < 1e-4
