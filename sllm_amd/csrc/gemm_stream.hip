@@ -45,6 +45,10 @@ constexpr int ST_LDS = 144;          // A row stride in LDS (128 + 16 pad)
 constexpr int ST_MAX_ITEMS = 32;     // work items per workgroup
 constexpr int ST_WAVES = 8;          // waves per workgroup
 constexpr int ST_THREADS = 64 * ST_WAVES;
+// Register sets per operand of the decode kernel's weight stream (prefetch
+// distance one less): MXFP4 steps carry 16 KB of weights, FP8 steps 32 KB.
+constexpr int DEC_SETS_F4 = 4;
+constexpr int DEC_SETS_F8 = 4;
 static_assert(ST_THREADS == 4 * ST_BM, "four lanes per activation-scale row");
 
 // ---------------------------------------------------------------------------
@@ -1448,23 +1452,24 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       }
     };
 
-    BSetD b0, b1, b2, b3;
-    ASet a0, a1, a2, a3;
+    // NS register sets per operand, prefetch distance NS - 1
+    constexpr int NS = F4 ? DEC_SETS_F4 : DEC_SETS_F8;
+    BSetD bs[NS];
+    ASet as[NS];
     p_enter(i0);
     c_enter(i0);
-    prefetch(a0, b0);
-    prefetch(a1, b1);
-    prefetch(a2, b2);
+#pragma unroll
+    for (int j = 0; j + 1 < NS; ++j) prefetch(as[j], bs[j]);
     int st = 0;
-    for (; st + 4 <= total_steps; st += 4) {
-      step(st, a0, a3, b0, b3);
-      step(st + 1, a1, a0, b1, b0);
-      step(st + 2, a2, a1, b2, b1);
-      step(st + 3, a3, a2, b3, b2);
+    for (; st + NS <= total_steps; st += NS) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        step(st + j, as[j], as[(j + NS - 1) % NS], bs[j], bs[(j + NS - 1) % NS]);
     }
-    if (st < total_steps) step(st, a0, a3, b0, b3);
-    if (st + 1 < total_steps) step(st + 1, a1, a0, b1, b0);
-    if (st + 2 < total_steps) step(st + 2, a2, a1, b2, b1);
+#pragma unroll
+    for (int j = 0; j + 1 < NS; ++j)
+      if (st + j < total_steps)
+        step(st + j, as[j], as[(j + NS - 1) % NS], bs[j], bs[(j + NS - 1) % NS]);
   };
   if constexpr (MIX) {
     // the MXFP4 items were placed first; the barrier hands the LDS

@@ -845,12 +845,18 @@ static int epl_for(int E) {
 // CUs rather than T / 4 (the reads are bound by per-CU bandwidth).
 static int route_tokens_per_block(int ks) { return ks > 1 ? 1 : 4; }
 
-// Two chunks: the routing kernel's reads of every further slice cost about
-// what the router saves (C3 B=32, layer: unsplit 155-157 us, 2 chunks
-// 153-155, 4 chunks 153-156, 8 chunks 156-157).
+// K chunks of the decode router: at least two, and enough that each of a
+// workgroup's 8 waves takes at most four 32-wide K slices, one round of
+// loads in flight together. H = 2048 (C3): 2, as every further slice costs
+// the routing about what the router saves (C3 B=32, layer: unsplit
+// 155-157 us, 2 chunks 153-155, 4 chunks 153-156, 8 chunks 156-157).
+// H = 7168 (C4): 7; two chunks left each wave four rounds of loads (the
+// router 8.9 us at B=1), and 8 chunks took C4 decode B=1 / 8 / 32 from
+// 98 / 281 / 680 to 94 / 274 / 672 us.
 int router_ksplit(int T, int H) {
   if (T > RG_SMALL_T) return 1;
-  return std::max(1, std::min(2, H / 256));
+  const int one_round = (H / 32 + 31) / 32;
+  return std::max(std::max(1, std::min(2, H / 256)), one_round);
 }
 
 static int launch_router_small(const uint16_t* x, const uint16_t* w,
