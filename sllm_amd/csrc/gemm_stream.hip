@@ -1082,18 +1082,21 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     // stream-K: this workgroup's range of the units' cost line (sk_lreq);
     // the ranges of an XCD are adjacent, so that a tile's units meet in
     // its L2. The MXFP4 units come first on the line: so do their items.
-    constexpr int W1 = MIX ? 2 : 1;
-    const int KB0 = S0.K / 128, KB1 = nseg > 1 ? S1.K / 128 : 1;
-    const long c0 = KB0, c1 = (long)KB1 * W1, cs = (long)nu0 * c0;
-    const long C = cs + (long)nu1 * c1;
-    long lreq = sk_lreq(KB0, 1, S0.ksplit);
-    if (nseg > 1) lreq = max(lreq, sk_lreq(KB1, W1, S1.ksplit));
-    const long G = sk_ranges(C, lreq, gridDim.x);
-    const long r = (long)xcd * nx + jx;
+    // 32-bit arithmetic: the host bounds the line's cost times the grid
+    // below 2^31 (go_stream_dec).
+    using U = uint32_t;
+    constexpr U W1 = MIX ? 2 : 1;
+    const U KB0 = S0.K / 128, KB1 = nseg > 1 ? S1.K / 128 : 1;
+    const U c0 = KB0, c1 = KB1 * W1, cs = (U)nu0 * c0;
+    const U C = cs + (U)nu1 * c1;
+    U lreq = sk_lreq<U>(KB0, 1, S0.ksplit);
+    if (nseg > 1) lreq = max(lreq, sk_lreq<U>(KB1, W1, S1.ksplit));
+    const U G = sk_ranges<U>(C, lreq, gridDim.x);
+    const U r = (U)xcd * nx + jx;
     if (C == 0 || r >= G) return;
-    const long a = r * C / G, b = (r + 1) * C / G;
-    auto unit_of = [&](long c) { return c < cs ? c / c0 : nu0 + (c - cs) / c1; };
-    const long ua = unit_of(a), ncand = unit_of(b - 1) - ua + 1;
+    const U a = r * C / G, b = (r + 1) * C / G;
+    auto unit_of = [&](U c) { return c < cs ? c / c0 : nu0 + (c - cs) / c1; };
+    const U ua = unit_of(a), ncand = unit_of(b - 1) - ua + 1;
     if (ncand > 64) {  // more units than a wave's lanes: a sizing error
       if (tid == 0) stream_item_overflow = 1;
       return;
@@ -1101,25 +1104,26 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
     if (wave == 0) {
       bool live = false;
       int seg = 0, li = 0, kb0 = 0, nkb = 0, slot = 0, fill = 0;
-      if (lane < ncand) {
-        const long u = ua + lane;
-        seg = u >= nu0;
+      if ((U)lane < ncand) {
+        const U u = ua + lane;
+        seg = u >= (U)nu0;
         li = (int)(seg ? u - nu0 : u);
-        const int KB = seg ? KB1 : KB0, w = seg ? W1 : 1;
+        const U KB = seg ? KB1 : KB0, w = seg ? W1 : 1;
         const int ks = seg ? S1.ksplit : S0.ksplit;
-        const long cu = seg ? cs + (long)li * c1 : (long)li * c0;
-        // the unit's steps whose start cu + j w lies in [a, b)
-        const long jlo = a <= cu ? 0 : (a - cu + w - 1) / w;
-        const long jhi = min((long)KB, (b - cu + w - 1) / w);
+        const U cu = seg ? cs + (U)li * c1 : (U)li * c0;
+        // the unit's steps whose start cu + j w lies in [a, b) (b > cu:
+        // the unit starts before the range ends)
+        const U jlo = a <= cu ? 0 : (a - cu + w - 1) / w;
+        const U jhi = min(KB, (b - cu + w - 1) / w);
         live = jlo < jhi;
         // range of a cost position: the r with r C / G <= c < (r + 1) C / G
-        auto range_of = [&](long c) { return ((c + 1) * G - 1) / C; };
-        const long rfirst = range_of(cu);
-        const int nsl = (int)(range_of(cu + (long)(KB - 1) * w) - rfirst + 1);
-        slot = (int)(r - rfirst);
+        auto range_of = [&](U c) { return ((c + 1) * G - 1) / C; };
+        const U rfirst = range_of(cu);
+        const int nsl = (int)(range_of(cu + (KB - 1) * w) - rfirst + 1);
+        slot = (int)r - (int)rfirst;
         fill = slot == 0 ? ks - nsl : 0;
         kb0 = (int)jlo;
-        nkb = (int)(jhi - jlo);
+        nkb = (int)jhi - (int)jlo;
       }
       const uint64_t lm = __ballot(live);
       const int idx = __popcll(lm & ((1ull << lane) - 1));
@@ -1129,8 +1133,7 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
         sk_n = __popcll(lm);
         if constexpr (MIX) mix_nf4 = __popcll(lm) - __popcll(f8);
       }
-    }
-    __syncthreads();
+    }    __syncthreads();
     nitems = sk_n;
   } else {
     // XCD x takes chunks x, x + 8, ... of CB items (a row tile's items, its
@@ -1801,6 +1804,12 @@ static int go_stream_dec(const SegDesc& s0, const SegDesc* s1, int topk,
     SLLM_CAPACITY(grid > 0,
                   "stream decode gemm: stream-K ranges cannot keep %d items "
                   "per workgroup", ST_MAX_ITEMS);
+    // the kernel deals in 32-bit arithmetic: products of a cost position
+    // and a range count stay below 2^31
+    const long cmax = un[0] * kb[0] * w[0] + (s1 ? un[1] * kb[1] * w[1] : 0);
+    SLLM_REQUIRE(cmax * grid < (1L << 31),
+                 "stream decode gemm: stream-K cost line %ld too long for a "
+                 "grid of %ld", cmax, grid);
   } else {
     // the kernel deals its items to the XCDs in chunks of (at most) one row
     // tile's items of the first segment (column slabs x K chunks)

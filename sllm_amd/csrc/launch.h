@@ -265,13 +265,18 @@ inline int dec_deal_chunk(const SegDesc& s, int ntw, long upper_items) {
 // them as arrivals, so that every unit holds ks slices, as a K-split unit
 // does. Ranges are at least sk_lreq long, which keeps a unit within ks of
 // them (and no range without a step of a unit it spans).
-__host__ __device__ inline long sk_lreq(int KB, int w, int ks) {
-  const long l = ((long)(KB - 1) * w + ks - 2) / (ks - 1);
-  return l > w ? l : w;
+// (I: the kernel's deal takes them in 32-bit unsigned arithmetic, whose
+// division is a short sequence where a 64-bit one runs to hundreds of
+// scalar instructions: ten of them took 3.5 us of each launch)
+template <class I = long>
+__host__ __device__ inline I sk_lreq(int KB, int w, int ks) {
+  const I l = ((I)(KB - 1) * (I)w + (I)(ks - 2)) / (I)(ks - 1);
+  return l > (I)w ? l : (I)w;
 }
 // ranges over a line of cost C with grid workgroups
-__host__ __device__ inline long sk_ranges(long C, long lreq, long grid) {
-  const long g = C / lreq;
+template <class I = long>
+__host__ __device__ inline I sk_ranges(I C, I lreq, I grid) {
+  const I g = C / lreq;
   return g < 1 ? 1 : (g < grid ? g : grid);
 }
 int launch_stream(int bf, int mode, const SegDesc& s0, const SegDesc* s1,
