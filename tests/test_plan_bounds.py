@@ -333,3 +333,26 @@ def test_prefill_grid_deals_every_item(ncu):
                 dealt = _deal(total, grid, slabs, ranges)
                 assert sum(len(w) for w in dealt) == total, name
                 assert len({i for w in dealt for i in w}) == total, name
+
+
+@pytest.mark.parametrize("H", [1024, 2048, 4096, 5120, 7168, 16384])
+def test_decode_router_chunks_one_load_round_per_wave(H):
+    """The decode router splits K into at least 2 chunks and enough that a
+    workgroup's 8 waves take at most four 32-wide K slices each (one round
+    of loads): 2 chunks at H = 2048 (C3), 7 at H = 7168 (C4); prefill-size
+    batches (T > 64) keep one. Read from the DeepSeek plan, whose decode
+    batches all route from the split logits."""
+    lib = _need_lib()
+    E, k, I = 256, 8, 2048
+    for T in (1, 8, 16, 32, 64, 65):
+        ks = _plan(lib, 1, T, H, E, I, I, k)[4]
+        if T > 64:
+            assert ks == 1, (H, T, ks)
+            continue
+        slices = H // 32
+        assert ks >= 2 and -(-slices // ks) <= 32, (H, T, ks)
+        # and no more than that: one chunk fewer would need a second round
+        if ks > 2:
+            assert -(-slices // (ks - 1)) > 32, (H, T, ks)
+    assert _plan(lib, 1, 1, 2048, E, I, I, k)[4] == 2
+    assert _plan(lib, 1, 1, 7168, E, I, I, k)[4] == 7
