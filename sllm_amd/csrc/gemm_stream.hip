@@ -1559,6 +1559,41 @@ int dec_ksplit_up(long upper_items, int KB) {
                         DEC_FINISH_STEPS, 0.0);
 }
 
+// The largest number of K steps a workgroup of a chunk-dealt decode launch
+// streams (chunks of a routed row tile's items to the XCDs in turn, dealt
+// round-robin over an XCD's workgroups; dec_deal_chunk, stream_dec_grid)
+// when its items, exp_items of them routed as expected (the chunk and the
+// grid follow the launch's bound upper_items), are cut into ks K chunks.
+static long dec_dealt_steps(long exp_items, long upper_items, long tile_items,
+                            int KB, int ks) {
+  const long n = exp_items * ks, nu = upper_items * ks;
+  const long cb = std::max(1L, std::min(tile_items * ks, nu / 64));
+  const long nx = stream_dec_grid(nu, num_cus(), cb, ST_MAX_ITEMS) / 8;
+  return (chunked_xcd_share(n, cb) + nx - 1) / nx * ((KB + ks - 1) / ks);
+}
+
+constexpr long DEC_TARGET_ITEMS_DEALT = 768;
+// a split (its finish launch, or the fused finish's slice reads) costs
+// about four K steps of the launch
+constexpr long DEC_FINISH_STEPS_DEALT = 4;
+
+int dec_ksplit_up_dealt(long upper_items, long exp_items, long tile_items,
+                        int KB) {
+  if (upper_items <= 0 || upper_items >= DEC_TARGET_ITEMS_DEALT) return 1;
+  const int cap = std::max(1, std::min(KB / 4, 8));
+  int best = 1;
+  long bcost = dec_dealt_steps(exp_items, upper_items, tile_items, KB, 1);
+  for (int ks = 2; ks <= cap; ++ks) {
+    const long c = dec_dealt_steps(exp_items, upper_items, tile_items, KB, ks) +
+                   DEC_FINISH_STEPS_DEALT;
+    if (c < bcost) {
+      best = ks;
+      bcost = c;
+    }
+  }
+  return best;
+}
+
 // h = silu(g) * u from the K-chunk slices of split mode-0 segments, rows
 // [0, total_rows) of each. A thread takes four columns of one row: all of
 // its 2 ks slice loads are issued together, then added in chunk order.

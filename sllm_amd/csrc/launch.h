@@ -407,6 +407,14 @@ inline long dec_fuse_counters(long N, long T, int I, int Is) {
 // that would leave most CUs idle).
 int dec_ksplit(long upper_items, int KB);
 int dec_ksplit_up(long upper_items, int KB);
+// Gate/up of a launch dealt in row-tile chunks (routed segment first, as the
+// Qwen decode launch): the split of fewest steps for the busiest workgroup
+// under the launch's own deal, for exp_items items (those a uniform routing
+// touches) of a launch sized for upper_items, tile_items items per routed
+// row tile unsplit; each split charged four steps (its finish). Batches of
+// 768 bound items and more stay unsplit.
+int dec_ksplit_up_dealt(long upper_items, long exp_items, long tile_items,
+                        int KB);
 // Grid of a decode streamed launch of at most upper_items items dealt in
 // chunks of `chunk` (dec_deal_chunk) on this device.
 long dec_launch_grid(long upper_items, long chunk);
