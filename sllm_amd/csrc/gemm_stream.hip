@@ -1033,9 +1033,15 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
                                : PermDst{};
       const PermDst mine{nullptr, nullptr, ri_sorted, nullptr, ri_tiles,
                          &ri_sh[ST_WAVES]};
-      permute_block<ST_WAVES, RI_G, RI_MAX_E>(ri_ids, RI.T * k, RI.E, RI.nbits,
-                                               RI.bm, RI.max_tiles, out, mine,
-                                               ri_hist, ri_sh);
+      // a batch routed here (distinct experts per token) of at most bm
+      // tokens and 64 assignments: one tile per expert, sorted in one wave
+      if (RI.logits && RI.T <= RI.bm && RI.T * k <= 64)
+        permute_small_wave(ri_ids, RI.T * k, RI.E, RI.max_tiles, out, mine,
+                           (uint32_t*)ri_hist[0]);
+      else
+        permute_block<ST_WAVES, RI_G, RI_MAX_E>(ri_ids, RI.T * k, RI.E, RI.nbits,
+                                                 RI.bm, RI.max_tiles, out, mine,
+                                                 ri_hist, ri_sh);
       __syncthreads();
     }
   }

@@ -169,7 +169,90 @@ __device__ __forceinline__ void permute_block(
   }
 }
 
-// The permutation launches' form: 16 waves, results to global memory.
+// The permutation of at most 64 assignments whose experts each hold at most
+// bm of them (an expert's rows are one tile: a batch of at most bm tokens
+// with distinct experts per token), with permute_block's results. Wave 0
+// sorts the keys expert << 6 | assignment with a bitonic network over its
+// lanes (dropped assignments, expert outside [0, E), last), so sorted
+// position p holds its assignment and each run of one expert is a tile;
+// no per-wave histograms over E or block scans. When d0 or d1 takes
+// counts / offsets, every thread then finds its experts' runs in the sorted
+// keys (keys: 64 words of LDS scratch). The caller synchronizes before
+// reading d1.
+__device__ __forceinline__ void permute_small_wave(const int* ids, int N, int E,
+                                                   int max_tiles,
+                                                   const PermDst& d0,
+                                                   const PermDst& d1,
+                                                   uint32_t* keys) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (wave == 0) {
+    const int raw = lane < N ? ids[lane] : -1;
+    const bool valid = lane < N && raw >= 0 && raw < E;
+    if (lane < N && !valid) {  // dropped: the combine skips it
+      if (d0.inv_pos) d0.inv_pos[lane] = -1;
+      if (d1.inv_pos) d1.inv_pos[lane] = -1;
+    }
+    uint32_t key = valid ? ((uint32_t)raw << 6) | (uint32_t)lane : 0xFFFFFFFFu;
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)key, j, kWave);
+        const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+        key = keep_min ? (o < key ? o : key) : (o > key ? o : key);
+      }
+    keys[lane] = key;
+    const bool v = key != 0xFFFFFFFFu;
+    const int e = (int)(key >> 6), a = (int)(key & 63u);
+    const int ep = __shfl((int)e, lane > 0 ? lane - 1 : 0, kWave);
+    const bool start = v && (lane == 0 || ep != e);
+    const uint64_t starts = __ballot(start);
+    const int nvalid = __popcll(__ballot(v));
+    if (v) {
+      if (d0.sorted_idx) d0.sorted_idx[lane] = a;
+      if (d1.sorted_idx) d1.sorted_idx[lane] = a;
+      if (d0.inv_pos) d0.inv_pos[a] = lane;
+      if (d1.inv_pos) d1.inv_pos[a] = lane;
+    }
+    if (start) {
+      const int t = __popcll(starts & ((1ull << lane) - 1ull));
+      const uint64_t later = lane < 63 ? starts >> (lane + 1) : 0ull;
+      const int end = later ? lane + 1 + (int)__builtin_ctzll(later) : nvalid;
+      if (t < max_tiles) {
+        const int4 t4 = make_int4(e, lane, end - lane, 0);
+        if (d0.tile_info) *(int4*)(d0.tile_info + 4 * t) = t4;
+        if (d1.tile_info) *(int4*)(d1.tile_info + 4 * t) = t4;
+      }
+    }
+    if (lane == 0) {
+      const int nt = __popcll(starts) < max_tiles ? __popcll(starts) : max_tiles;
+      if (d0.num_tiles) *d0.num_tiles = nt;
+      if (d1.num_tiles) *d1.num_tiles = nt;
+      if (d0.offsets) d0.offsets[E] = nvalid;
+      if (d1.offsets) d1.offsets[E] = nvalid;
+    }
+  }
+  if (d0.counts || d0.offsets || d1.counts || d1.offsets) {
+    __syncthreads();  // the sorted keys
+    for (int x = tid; x < E; x += blockDim.x) {
+      // sorted positions of expert x: [lo, hi), the first keys >= x << 6
+      // and >= (x + 1) << 6 (binary searches over the 64 ascending keys)
+      int lo = 0, hi = 0;
+#pragma unroll
+      for (int step = 64; step > 0; step >>= 1) {
+        if (lo + step <= 64 && keys[lo + step - 1] < ((uint32_t)x << 6)) lo += step;
+        if (hi + step <= 64 && keys[hi + step - 1] < ((uint32_t)(x + 1) << 6))
+          hi += step;
+      }
+      if (d0.counts) d0.counts[x] = hi - lo;
+      if (d1.counts) d1.counts[x] = hi - lo;
+      if (d0.offsets) d0.offsets[x] = lo;
+      if (d1.offsets) d1.offsets[x] = lo;
+    }
+  }
+}
+
+// The permutation launches' form: 16 waves, results to global memory.// The permutation launches' form: 16 waves, results to global memory.
 __device__ __forceinline__ void permute_fused_body(
     const int* ids, int N, int E, int nbits, int bm, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted_idx,
