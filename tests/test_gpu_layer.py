@@ -138,7 +138,8 @@ def test_qwen_decode_32_row_tiles(B, E, k):
 
 
 @pytest.mark.parametrize("B,E,k,biased", [(1, 512, 10, False), (3, 64, 6, True),
-                                          (4, 512, 10, True), (8, 512, 10, False),
+                                          (4, 512, 10, True), (6, 512, 10, False),
+                                          (8, 8, 4, True), (8, 512, 10, False),
                                           (16, 64, 6, False), (17, 64, 6, True),
                                           (32, 512, 10, True), (40, 4, 2, False),
                                           (64, 512, 10, False)])
@@ -156,7 +157,9 @@ def test_decode_inline_routing_matches_launches(B, E, k, biased, monkeypatch):
     go to the one-workgroup route + permute launch). Covered: with and
     without a router bias, the fused gate/up finish (B <= 4), the split
     router's logit slices and shared-gate partials, and 32-row tiles
-    (E = 4). The output also matches the oracle layer on the logits."""
+    (E = 4). Up to 64 assignments the launch sorts them in one wave (B=6:
+    60 assignments; E = 8 at B=8: several rows per expert). The output
+    also matches the oracle layer on the logits."""
     from sllm_amd.moe import QwenMoE, _up, qwen_forward_dev
     from sllm_amd.runtime import DeviceBuffer, to_bf16
     H, I = 512, 256
