@@ -984,6 +984,9 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
   static_assert(RI_MAX_ROUTE_T <= ST_WAVES, "one routed token per wave");
   __shared__ int ri_hist[RTE ? ST_WAVES : 1][RTE ? RI_MAX_E : 1];
   __shared__ int ri_ids[RTE ? RI_MAX_N : 1];
+  // workgroup 0: the weights of the picks routed here (up to 8 tokens of
+  // at most 64 picks, one wave each), for the sorted-position table
+  __shared__ float ri_w[RTE ? RI_MAX_ROUTE_T * 64 : 1];
   __shared__ int ri_sorted[RTE ? RI_MAX_N : 1];
   __shared__ __attribute__((aligned(16))) int ri_tiles[RTE ? 4 * RI_MAX_TILES : 4];
   __shared__ int ri_sh[ST_WAVES + 1];
@@ -1014,13 +1017,15 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
                 false, RI.E, k, RI.n_group, RI.topk_group, RI.scoring,
                 RI.route_scale, RI.bias, scr, scr + RI_MAX_E_GROUPED,
                 lead ? RI.w + (size_t)wave * k : nullptr,
-                lead ? RI.ids + (size_t)wave * k : nullptr, ri_ids + wave * k);
+                lead ? RI.ids + (size_t)wave * k : nullptr, ri_ids + wave * k,
+                lead ? ri_w + wave * k : nullptr);
           } else {
             route_softmax_token<8, 2>(RI.logits + (size_t)wave * RI.E, RI.ks,
                                       (long)RI.T * RI.E, RI.E, k, RI.eps,
                                       lead ? RI.w + (size_t)wave * k : nullptr,
                                       lead ? RI.ids + (size_t)wave * k : nullptr,
-                                      ri_ids + wave * k, RI.bias, false);
+                                      ri_ids + wave * k, RI.bias, false,
+                                      lead ? ri_w + wave * k : nullptr);
           }
           if (lead && RI.gate && lane == 0) route_gate_finish(RI.gate, RI.T, wave, RI.ks);
         }
@@ -1029,19 +1034,22 @@ __global__ __launch_bounds__(ST_THREADS, 1) void moe_stream_dec_kernel(
       }
       __syncthreads();
       const PermDst out = lead ? PermDst{RI.counts, RI.offsets, RI.sorted,
-                                         RI.inv, RI.tiles, RI.ntiles}
+                                         RI.inv, RI.tiles, RI.ntiles,
+                                         RI.rw_sorted}
                                : PermDst{};
       const PermDst mine{nullptr, nullptr, ri_sorted, nullptr, ri_tiles,
                          &ri_sh[ST_WAVES]};
+      // (the batches routed here; the table is not asked for otherwise)
+      const float* w_src = lead && RI.rw_sorted && RI.logits ? ri_w : nullptr;
       // a batch routed here (distinct experts per token) of at most bm
       // tokens and 64 assignments: one tile per expert, sorted in one wave
       if (RI.logits && RI.T <= RI.bm && RI.T * k <= 64)
         permute_small_wave(ri_ids, RI.T * k, RI.E, RI.max_tiles, out, mine,
-                           (uint32_t*)ri_hist[0]);
+                           (uint32_t*)ri_hist[0], w_src);
       else
         permute_block<ST_WAVES, RI_G, RI_MAX_E>(ri_ids, RI.T * k, RI.E, RI.nbits,
                                                  RI.bm, RI.max_tiles, out, mine,
-                                                 ri_hist, ri_sh);
+                                                 ri_hist, ri_sh, nullptr, 0, w_src);
       __syncthreads();
     }
   }

@@ -356,6 +356,10 @@ struct RouteInline {
   // softmax top-k; E <= RI_MAX_E_GROUPED
   int grouped, scoring, n_group, topk_group;
   float route_scale;
+  // optional, with logits (the batch routed in the launch): workgroup 0
+  // also writes each sorted position's route weight (N floats), so that the
+  // down launch reads its row weights by position
+  float* rw_sorted;
 };
 constexpr int RI_MAX_E_GROUPED = 256;
 bool route_inline_fits(int T, int E, int topk, long max_tiles);

@@ -37,6 +37,7 @@ struct Plan {
   // shared) and partial-logit slices of the router GEMM
   int ks_up, ks_up_sh, ks_dn, ks_dn_sh, ks_r;
   size_t logits, w, ids, counts, offsets, sorted, inv, tiles, ntiles, pscr;
+  size_t rws;  // decode: the route weight of each sorted position
   size_t xq, sx, gate, hq, hs, hq_sh, hs_sh, y, y_sh, gu, gu_sh;
   // decode, streamed kernels: item bounds of the gate/up and down launches
   // (routed and shared segments in one launch each; a DeepSeek layer whose
@@ -119,6 +120,7 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
   p.counts = take(c, (size_t)E * 4);
   p.offsets = take(c, (size_t)(E + 1) * 4);
   p.sorted = take(c, (size_t)p.N * 4);
+  p.rws = p.decode ? take(c, (size_t)p.N * 4) : 0;
   p.inv = take(c, (size_t)p.N * 4);
   p.tiles = take(c, (size_t)p.max_tiles * 16);
   p.ntiles = take(c, 4);
@@ -586,6 +588,7 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
         ri.sorted = sorted; ri.inv = inv; ri.tiles = tiles; ri.ntiles = ntiles;
         ri.T = T; ri.E = E; ri.topk = k; ri.ks = p.ks_r; ri.bm = p.bm;
         ri.max_tiles = p.max_tiles; ri.eps = eps;
+        ri.rw_sorted = route_inl ? (float*)(ws + p.rws) : nullptr;
       }
       STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,
             first_rc(
@@ -607,6 +610,15 @@ static int qwen_forward_ws(const sllm_moe_qwen_args* a, char* ws,
       r2.tile_info = tiles; r2.num_tiles = ntiles; r2.max_tiles = p.max_tiles;
       r2.wp = (const uint8_t*)a->wd_packed; r2.s0 = a->wd_s; r2.N = H; r2.K = I;
       r2.row_w = w; r2.row_w_by_idx = 1; r2.y = (uint16_t*)y;
+      if (route_inl) {
+        // workgroup 0 of the gate/up launch, which routed the batch, writes
+        // the sorted positions' route weights: read by position, one load
+        // rather than two dependent ones (C4 B=2 / 4: 110.2 / 168.7 ->
+        // 108.5 / 166.6 us; from 17 tokens, where the weights would come
+        // from the routing launch, B=32 lost 1 us)
+        r2.row_w = (float*)(ws + p.rws);
+        r2.row_w_by_idx = 0;
+      }
       r2.ksplit = p.ks_dn; r2.pstride = (long)p.N * H;
       if (one_expert) {  // route weights are exactly 1
         r2.total_rows = p.N;
@@ -1184,6 +1196,13 @@ int sllm_moe_ds_forward(const sllm_moe_ds_args* a) {
       ri.bm = p.bm; ri.max_tiles = p.max_tiles;
       ri.grouped = route_inl; ri.scoring = a->scoring; ri.n_group = a->n_group;
       ri.topk_group = a->topk_group; ri.route_scale = a->route_scale;
+      // routed here: workgroup 0 writes the sorted positions' route
+      // weights, which the down launch reads by position
+      if (route_inl) {
+        ri.rw_sorted = (float*)(ws + p.rws);
+        r2.row_w = ri.rw_sorted;
+        r2.row_w_by_idx = 0;
+      }
     }
     const DecFuse f_up{fcnt, (long)p.N * (I / 128)};
     STAGE(clk, SLLM_MOE_STAGE_EXPERT_UP,

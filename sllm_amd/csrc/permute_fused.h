@@ -71,13 +71,17 @@ struct PermDst {
   int* inv_pos;     // N
   int* tile_info;   // 4 max_tiles
   int* num_tiles;   // 1
+  // N: the route weight of the assignment at each sorted position (written
+  // when the permutation is given the weights by assignment)
+  float* rw_sorted = nullptr;
 };
 
 template <int NW, int G, int HE>
 __device__ __forceinline__ void permute_block(
     const int* ids, int N, int E, int nbits, int bm, int max_tiles,
     const PermDst& d0, const PermDst& d1, int (*hist)[HE], int* sh,
-    int* __restrict__ zero = nullptr, int nzero = 0) {
+    int* __restrict__ zero = nullptr, int nzero = 0,
+    const float* w_src = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < nzero; i += NW * 64) zero[i] = 0;
   const int R = ((N + NW - 1) / NW + 63) & ~63;
@@ -161,6 +165,8 @@ __device__ __forceinline__ void permute_block(
       const int pos = start + __popcll(peers & lt);
       if (d0.sorted_idx) d0.sorted_idx[pos] = a;
       if (d1.sorted_idx) d1.sorted_idx[pos] = a;
+      if (w_src && d0.rw_sorted) d0.rw_sorted[pos] = w_src[a];
+      if (w_src && d1.rw_sorted) d1.rw_sorted[pos] = w_src[a];
       if (d0.inv_pos) d0.inv_pos[a] = pos;
       if (d1.inv_pos) d1.inv_pos[a] = pos;
       if ((peers >> lane) == 1ull) run[e] = start + __popcll(peers);
@@ -183,7 +189,8 @@ __device__ __forceinline__ void permute_small_wave(const int* ids, int N, int E,
                                                    int max_tiles,
                                                    const PermDst& d0,
                                                    const PermDst& d1,
-                                                   uint32_t* keys) {
+                                                   uint32_t* keys,
+                                                   const float* w_src = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (wave == 0) {
     const int raw = lane < N ? ids[lane] : -1;
@@ -211,6 +218,8 @@ __device__ __forceinline__ void permute_small_wave(const int* ids, int N, int E,
     if (v) {
       if (d0.sorted_idx) d0.sorted_idx[lane] = a;
       if (d1.sorted_idx) d1.sorted_idx[lane] = a;
+      if (w_src && d0.rw_sorted) d0.rw_sorted[lane] = w_src[a];
+      if (w_src && d1.rw_sorted) d1.rw_sorted[lane] = w_src[a];
       if (d0.inv_pos) d0.inv_pos[a] = lane;
       if (d1.inv_pos) d1.inv_pos[a] = lane;
     }

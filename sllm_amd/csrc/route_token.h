@@ -153,7 +153,8 @@ __device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
                                              int topk, float eps,
                                              float* __restrict__ w_row,
                                              int* __restrict__ id_row,
-                                             int* id_lds) {
+                                             int* id_lds,
+                                             float* w_lds = nullptr) {
   const int lane = threadIdx.x & 63;
   const float pn = expf(topk_key_value(pick) - m) / s;  // lane j: pick j
   float wsum = 0.f;
@@ -166,6 +167,7 @@ __device__ __forceinline__ void softmax_emit(uint64_t pick, float m, float s,
       id_row[lane] = myid;
     }
     if (id_lds) id_lds[lane] = myid;
+    if (w_lds) w_lds[lane] = pn / (wsum + eps);
   }
 }
 
@@ -183,7 +185,8 @@ template <int EPL, int G = (EPL >= 64 ? 1 : (64 / EPL < 8 ? 64 / EPL : 8))>
 __device__ __forceinline__ void route_softmax_token(
     float* row, int ks, long kstride, int E, int topk, float eps,
     float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds,
-    const float* __restrict__ bias, bool store = true) {
+    const float* __restrict__ bias, bool store = true,
+    float* w_lds = nullptr) {
   const int lane = threadIdx.x & 63;
   float v[EPL];
   logit_sums<EPL, G>(row, ks, kstride, E, store, -INFINITY, v);
@@ -208,7 +211,7 @@ __device__ __forceinline__ void route_softmax_token(
   }
   s = wave_sum(s);
   const uint64_t pick = wave_topk_keys<EPL>(key, topk);
-  softmax_emit(pick, m, s, topk, eps, w_row, id_row, id_lds);
+  softmax_emit(pick, m, s, topk, eps, w_row, id_row, id_lds, w_lds);
 }
 
 // Token t's shared-expert gate from the split router GEMM's ks partial
@@ -290,7 +293,8 @@ __device__ __forceinline__ void route_grouped_token(
     float* row, int ks, long kstride, bool store, int E, int topk, int n_group,
     int topk_group, int scoring, float route_scale,
     const float* __restrict__ bias, float* sb, float* scl,
-    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds) {
+    float* __restrict__ w_row, int* __restrict__ id_row, int* id_lds,
+    float* w_lds = nullptr) {
   const int lane = threadIdx.x & 63;
   // the bias loads go out with the logits' (issued after the scores, they
   // added their latency: 1.6 us of the C4 in-launch routing)
@@ -407,6 +411,7 @@ __device__ __forceinline__ void route_grouped_token(
       id_row[lane] = myid;
     }
     if (id_lds) id_lds[lane] = myid;
+    if (w_lds) w_lds[lane] = wv * route_scale;
   }
 }
 
