@@ -356,3 +356,54 @@ def test_decode_router_chunks_one_load_round_per_wave(H):
             assert -(-slices // (ks - 1)) > 32, (H, T, ks)
     assert _plan(lib, 1, 1, 2048, E, I, I, k)[4] == 2
     assert _plan(lib, 1, 1, 7168, E, I, I, k)[4] == 7
+
+
+def _dealt_steps(exp_items, upper_items, tile_items, KB, ks, ncu=256):
+    """The busiest workgroup's K steps under a decode launch's row-tile
+    chunk deal (chunks of min(tile_items ks, upper ks / 64) items to the 8
+    XCDs in turn, round-robin over an XCD's workgroups; the grid sized from
+    the bound upper_items)."""
+    n, nu = exp_items * ks, upper_items * ks
+    cb = max(1, min(tile_items * ks, nu // 64))
+    per_xcd_bound = (-(-nu // cb) + 7) // 8 * cb
+    nx = max((ncu + 7) // 8, -(-per_xcd_bound // ST_MAX_ITEMS))
+    share = (-(-n // cb) + 7) // 8 * cb
+    return -(-share // nx) * -(-KB // ks)
+
+
+@pytest.mark.parametrize("shape", [(2048, 512, 10, 512, 512), (4096, 128, 8, 1536, 1536),
+                                   (2048, 64, 6, 1408, 5632)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape):
+    """The Qwen decode gate/up K split: of 1..min(KB / 4, 8) slices, the one
+    whose busiest workgroup streams the fewest K steps under the launch's
+    own deal, counting the tiles a uniform routing touches
+    (E (1 - (1 - 1/E)^N) experts) and four steps per split; batches of 768
+    bound items or more unsplit. C3 (the first shape): 4 / 2 / 1 / 4 / 4 / 1
+    slices at 1 / 2 / 4 / 8 / 16 / 32 tokens."""
+    import math
+    lib = _need_lib()
+    H, E, k, I, Is = shape
+    KB, slabs = H // 128, I // 128
+    got = {}
+    for T in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 64):
+        p = _plan(lib, 0, T, H, E, I, Is, k)
+        if p[9] != 256:
+            pytest.skip("port written for 256 CUs")
+        N, bm, rt = T * k, p[1], p[3]
+        sh_rt = -(-T // p[2])
+        upper = rt * slabs + sh_rt * (Is // 128)
+        touched = E * (1.0 - (1.0 - 1.0 / E) ** N)
+        exp_rt = min(rt, math.ceil(touched + max(0.0, N - touched) / bm))
+        exp = exp_rt * slabs + sh_rt * (Is // 128)
+        want = 1
+        if upper < 768:
+            best = _dealt_steps(exp, upper, slabs, KB, 1)
+            for ks in range(2, max(1, min(KB // 4, 8)) + 1):
+                c = _dealt_steps(exp, upper, slabs, KB, ks) + 4
+                if c < best:
+                    want, best = ks, c
+        assert p[5] == want and p[6] == want, (T, p[5], p[6], want)
+        got[T] = p[5]
+    if shape[0] == 2048 and shape[1] == 512:
+        assert [got[t] for t in (1, 2, 4, 8, 16, 32)] == [4, 2, 1, 4, 4, 1]
