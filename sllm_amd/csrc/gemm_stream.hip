@@ -1578,12 +1578,17 @@ int dec_ksplit_up(long upper_items, int KB) {
 // round-robin over an XCD's workgroups; dec_deal_chunk, stream_dec_grid)
 // when its items, exp_items of them routed as expected (the chunk and the
 // grid follow the launch's bound upper_items), are cut into ks K chunks.
-static long dec_dealt_steps(long exp_items, long upper_items, long tile_items,
-                            int KB, int ks) {
+static long dec_dealt_items(long exp_items, long upper_items, long tile_items,
+                            int ks) {
   const long n = exp_items * ks, nu = upper_items * ks;
   const long cb = std::max(1L, std::min(tile_items * ks, nu / 64));
   const long nx = stream_dec_grid(nu, num_cus(), cb, ST_MAX_ITEMS) / 8;
-  return (chunked_xcd_share(n, cb) + nx - 1) / nx * ((KB + ks - 1) / ks);
+  return (chunked_xcd_share(n, cb) + nx - 1) / nx;
+}
+static long dec_dealt_steps(long exp_items, long upper_items, long tile_items,
+                            int KB, int ks) {
+  return dec_dealt_items(exp_items, upper_items, tile_items, ks) *
+         ((KB + ks - 1) / ks);
 }
 
 constexpr long DEC_TARGET_ITEMS_DEALT = 768;
@@ -1600,6 +1605,24 @@ int dec_ksplit_up_dealt(long upper_items, long exp_items, long tile_items,
   for (int ks = 2; ks <= cap; ++ks) {
     const long c = dec_dealt_steps(exp_items, upper_items, tile_items, KB, ks) +
                    DEC_FINISH_STEPS_DEALT;
+    if (c < bcost) {
+      best = ks;
+      bcost = c;
+    }
+  }
+  return best;
+}
+
+// Down launches dealt the same way: no finish (the combine adds the
+// slices), but every item costs about one K step beyond its own (its
+// prologue and y stores; at C3 the items are 4 K steps long).
+int dec_ksplit_dealt(long upper_items, long exp_items, long tile_items, int KB) {
+  if (upper_items <= 0 || KB <= 1) return 1;
+  int best = 1;
+  long bcost = dec_dealt_items(exp_items, upper_items, tile_items, 1) * (KB + 1);
+  for (int ks = 2; ks <= std::min(KB, DEC_MAX_KSPLIT); ++ks) {
+    const long c = dec_dealt_items(exp_items, upper_items, tile_items, ks) *
+                   ((KB + ks - 1) / ks + 1);
     if (c < bcost) {
       best = ks;
       bcost = c;

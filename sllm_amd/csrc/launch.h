@@ -419,6 +419,9 @@ int dec_ksplit_up(long upper_items, int KB);
 // 768 bound items and more stay unsplit.
 int dec_ksplit_up_dealt(long upper_items, long exp_items, long tile_items,
                         int KB);
+// The down launch of the same deal: the split of fewest (steps + 1) per
+// item over the busiest workgroup's items; no finish charge.
+int dec_ksplit_dealt(long upper_items, long exp_items, long tile_items, int KB);
 // Grid of a decode streamed launch of at most upper_items items dealt in
 // chunks of `chunk` (dec_deal_chunk) on this device.
 long dec_launch_grid(long upper_items, long chunk);

@@ -68,6 +68,7 @@ static int weights_reused(long rows, long experts, int bm) {
 static int dense8_mode();
 static bool route_inline_on();
 static bool streamk_on();
+static bool split_dealt_on();
 static int device_cus();
 
 static size_t take(size_t& cur, size_t bytes) {
@@ -165,15 +166,29 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
         // sizes the launch). C3 B=2 / 4 / 8 / 16: 3 / 3 / 2 / 1 slices,
         // 49.0 / 55.8 / 76.4 / 114.3 us -> 2 / 1 / 4 / 4 slices, 45.2 / 53.6 /
         // 74.0 / 110.0 us (flushed, same box, two rounds)
-        const double touched = E * (1.0 - std::pow(1.0 - 1.0 / E, (double)p.N));
-        const long exp_rt = std::min(
-            rt, (long)std::ceil(touched + std::max(0.0, p.N - touched) / p.bm));
-        p.ks_up = p.ks_up_sh = dec_ksplit_up_dealt(
-            rt * (I / 128) + sh_rt * (Is / 128),
-            exp_rt * (I / 128) + sh_rt * (Is / 128), I / 128, H / 128);
-        p.ks_dn = p.ks_dn_sh =
-            dec_ksplit(rt * (H / 256) + sh_rt * (H / 256),
-                       (has_shared ? std::min(I, Is) : I) / 128);
+        // (a one-expert layer, a dense MLP, deals identity rows in eighth-
+        // tile chunks: the count-based rules, as measured for it; also with
+        // SLLM_MOE_SPLIT_DEALT=0)
+        const int KBd = (has_shared ? std::min(I, Is) : I) / 128;
+        if (E == 1 || !split_dealt_on()) {
+          p.ks_up = p.ks_up_sh =
+              dec_ksplit_up(rt * (I / 128) + sh_rt * (Is / 128), H / 128);
+          p.ks_dn = p.ks_dn_sh =
+              dec_ksplit(rt * (H / 256) + sh_rt * (H / 256), KBd);
+        } else {
+          const double touched = E * (1.0 - std::pow(1.0 - 1.0 / E, (double)p.N));
+          const long exp_rt = std::min(
+              rt, (long)std::ceil(touched + std::max(0.0, p.N - touched) / p.bm));
+          p.ks_up = p.ks_up_sh = dec_ksplit_up_dealt(
+              rt * (I / 128) + sh_rt * (Is / 128),
+              exp_rt * (I / 128) + sh_rt * (Is / 128), I / 128, H / 128);
+          // down: one step per item beyond its own (C3 B=2 / 3 / 7: 4 / 1 /
+          // 4 -> 1 / 2 / 1 slices, 44.4 / 53.4 / 75.2 -> 43.6 / 50.3 / 74.1
+          // us; other batches keep their split)
+          p.ks_dn = p.ks_dn_sh = dec_ksplit_dealt(
+              rt * (H / 256) + sh_rt * (H / 256),
+              exp_rt * (H / 256) + sh_rt * (H / 256), H / 256, KBd);
+        }
       }
       // Stream-K deal (a workgroup takes an equal range of K steps across
       // the launch's units) for the DeepSeek mixed-format launches (up to 16
@@ -1028,6 +1043,11 @@ static int dense8_mode() {
 // of stream-K ranges (A/B runs)
 static bool streamk_on() {
   const char* v = std::getenv("SLLM_MOE_STREAMK");
+  return !(v && v[0] == '0');
+}
+
+static bool split_dealt_on() {
+  const char* v = std::getenv("SLLM_MOE_SPLIT_DEALT");
   return !(v && v[0] == '0');
 }
 

@@ -295,9 +295,11 @@ def test_old_contiguous_sizing_would_overflow(monkeypatch):
     36 to the H 3584, E 64, I 2560, Is 20480 layer at 7 tokens; the
     chunk-aware grid the library now launches keeps them at 32. (The old
     deal's chunks were whole row tiles; the library's are now capped at a
-    64th of the items. The plans here deal whole items, as they did then:
-    SLLM_MOE_STREAMK=0.)"""
+    64th of the items. The plans here deal whole items and take the
+    count-based K splits, as they did then: SLLM_MOE_STREAMK=0,
+    SLLM_MOE_SPLIT_DEALT=0.)"""
     monkeypatch.setenv("SLLM_MOE_STREAMK", "0")
+    monkeypatch.setenv("SLLM_MOE_SPLIT_DEALT", "0")
     lib = _need_lib()
     for (ds, H, E, k, I, Is), T, old_worst in (
             ((0, 4096, 128, 8, 1536, 1536), 6, 37),
@@ -375,12 +377,13 @@ def _dealt_steps(exp_items, upper_items, tile_items, KB, ks, ncu=256):
                                    (2048, 64, 6, 1408, 5632)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape):
-    """The Qwen decode gate/up K split: of 1..min(KB / 4, 8) slices, the one
+    """The Qwen decode K splits. Gate/up: of 1..min(KB / 4, 8) slices, the one
     whose busiest workgroup streams the fewest K steps under the launch's
     own deal, counting the tiles a uniform routing touches
     (E (1 - (1 - 1/E)^N) experts) and four steps per split; batches of 768
     bound items or more unsplit. C3 (the first shape): 4 / 2 / 1 / 4 / 4 / 1
-    slices at 1 / 2 / 4 / 8 / 16 / 32 tokens."""
+    slices at 1 / 2 / 4 / 8 / 16 / 32 tokens. Down: the same deal, one step
+    per item beyond its own, no finish charge."""
     import math
     lib = _need_lib()
     H, E, k, I, Is = shape
@@ -405,5 +408,17 @@ def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape):
                     want, best = ks, c
         assert p[5] == want and p[6] == want, (T, p[5], p[6], want)
         got[T] = p[5]
+        # down: (steps + 1) per item, no finish charge, up to min(KB, 32)
+        kbd = min(I, Is) // 128
+        dn_up, dn_exp = rt * (H // 256) + sh_rt * (H // 256), exp_rt * (H // 256) + sh_rt * (H // 256)
+
+        def dn_cost(ks):
+            return (_dealt_steps(dn_exp, dn_up, H // 256, 1, ks) * (-(-kbd // ks) + 1))
+        want_dn = 1
+        best = dn_cost(1)
+        for ks in range(2, min(kbd, 32) + 1):
+            if dn_cost(ks) < best:
+                want_dn, best = ks, dn_cost(ks)
+        assert p[7] == want_dn and p[8] == want_dn, (T, p[7], p[8], want_dn)
     if shape[0] == 2048 and shape[1] == 512:
         assert [got[t] for t in (1, 2, 4, 8, 16, 32)] == [4, 2, 1, 4, 4, 1]
