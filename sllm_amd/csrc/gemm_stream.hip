@@ -1591,7 +1591,6 @@ static long dec_dealt_steps(long exp_items, long upper_items, long tile_items,
          ((KB + ks - 1) / ks);
 }
 
-constexpr long DEC_TARGET_ITEMS_DEALT = 768;
 // a split (its finish launch, or the fused finish's slice reads) costs
 // about four K steps of the launch
 constexpr long DEC_FINISH_STEPS_DEALT = 4;

@@ -411,6 +411,10 @@ inline long dec_fuse_counters(long N, long T, int I, int Is) {
 // that would leave most CUs idle).
 int dec_ksplit(long upper_items, int KB);
 int dec_ksplit_up(long upper_items, int KB);
+// Bound gate/up items below which the deal-based splits apply (larger
+// decode batches stay unsplit: their split partials cost more than the
+// balance gains).
+constexpr long DEC_TARGET_ITEMS_DEALT = 768;
 // Gate/up of a launch dealt in row-tile chunks (routed segment first, as the
 // Qwen decode launch): the split of fewest steps for the busiest workgroup
 // under the launch's own deal, for exp_items items (those a uniform routing

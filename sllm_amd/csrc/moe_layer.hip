@@ -179,15 +179,22 @@ static Plan make_plan(int T, int H, int E, int I, int Is, int topk, int mode,
           const double touched = E * (1.0 - std::pow(1.0 - 1.0 / E, (double)p.N));
           const long exp_rt = std::min(
               rt, (long)std::ceil(touched + std::max(0.0, p.N - touched) / p.bm));
+          const long up_upper = rt * (I / 128) + sh_rt * (Is / 128);
           p.ks_up = p.ks_up_sh = dec_ksplit_up_dealt(
-              rt * (I / 128) + sh_rt * (Is / 128),
-              exp_rt * (I / 128) + sh_rt * (Is / 128), I / 128, H / 128);
+              up_upper, exp_rt * (I / 128) + sh_rt * (Is / 128), I / 128,
+              H / 128);
           // down: one step per item beyond its own (C3 B=2 / 3 / 7: 4 / 1 /
           // 4 -> 1 / 2 / 1 slices, 44.4 / 53.4 / 75.2 -> 43.6 / 50.3 / 74.1
-          // us; other batches keep their split)
-          p.ks_dn = p.ks_dn_sh = dec_ksplit_dealt(
-              rt * (H / 256) + sh_rt * (H / 256),
-              exp_rt * (H / 256) + sh_rt * (H / 256), H / 256, KBd);
+          // us; other batches keep their split), for the batches the
+          // gate/up rule covers; larger ones the count-based rule, which
+          // keeps them unsplit (the deal-based one split C3 B=40-64 in 4
+          // and its y slices took B=64 from 217 to 266 us)
+          p.ks_dn = p.ks_dn_sh =
+              up_upper < DEC_TARGET_ITEMS_DEALT
+                  ? dec_ksplit_dealt(rt * (H / 256) + sh_rt * (H / 256),
+                                     exp_rt * (H / 256) + sh_rt * (H / 256),
+                                     H / 256, KBd)
+                  : dec_ksplit(rt * (H / 256) + sh_rt * (H / 256), KBd);
         }
       }
       // Stream-K deal (a workgroup takes an equal range of K steps across

@@ -376,14 +376,15 @@ def _dealt_steps(exp_items, upper_items, tile_items, KB, ks, ncu=256):
 @pytest.mark.parametrize("shape", [(2048, 512, 10, 512, 512), (4096, 128, 8, 1536, 1536),
                                    (2048, 64, 6, 1408, 5632)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape):
+def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape, monkeypatch):
     """The Qwen decode K splits. Gate/up: of 1..min(KB / 4, 8) slices, the one
     whose busiest workgroup streams the fewest K steps under the launch's
     own deal, counting the tiles a uniform routing touches
     (E (1 - (1 - 1/E)^N) experts) and four steps per split; batches of 768
     bound items or more unsplit. C3 (the first shape): 4 / 2 / 1 / 4 / 4 / 1
     slices at 1 / 2 / 4 / 8 / 16 / 32 tokens. Down: the same deal, one step
-    per item beyond its own, no finish charge."""
+    per item beyond its own, no finish charge, for the same batches; larger
+    ones take the count-based split."""
     import math
     lib = _need_lib()
     H, E, k, I, Is = shape
@@ -414,11 +415,16 @@ def test_qwen_decode_gate_up_split_fewest_dealt_steps(shape):
 
         def dn_cost(ks):
             return (_dealt_steps(dn_exp, dn_up, H // 256, 1, ks) * (-(-kbd // ks) + 1))
-        want_dn = 1
-        best = dn_cost(1)
-        for ks in range(2, min(kbd, 32) + 1):
-            if dn_cost(ks) < best:
-                want_dn, best = ks, dn_cost(ks)
+        if upper < 768:
+            want_dn = 1
+            best = dn_cost(1)
+            for ks in range(2, min(kbd, 32) + 1):
+                if dn_cost(ks) < best:
+                    want_dn, best = ks, dn_cost(ks)
+        else:  # larger batches: the count-based rule
+            monkeypatch.setenv("SLLM_MOE_SPLIT_DEALT", "0")
+            want_dn = _plan(lib, 0, T, H, E, I, Is, k)[7]
+            monkeypatch.delenv("SLLM_MOE_SPLIT_DEALT")
         assert p[7] == want_dn and p[8] == want_dn, (T, p[7], p[8], want_dn)
     if shape[0] == 2048 and shape[1] == 512:
         assert [got[t] for t in (1, 2, 4, 8, 16, 32)] == [4, 2, 1, 4, 4, 1]
